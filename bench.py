@@ -1,0 +1,342 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X EXL3 quantized-linear engine (one GPU).
+
+Headline (BASELINE.json metric, configuration 1): M = 1 decode through the 7 EXL3 linears of a
+Qwen-27B-shaped decoder layer (q, k, v, o 5120-wide attention projections and the
+5120 -> 17408 -> 5120 MLP) at 4 bpw, mul1 codebook, with the plugin's own routing (q/k/v as one
+fused module, gate/up through the grouped pointer-table launch).  One *step* = one layer's
+linears on one token.  Steps cycle over 8 distinct copies of the layer's weights (1.3 GB, ~5x the
+256 MB Infinity Cache) and are replayed from HIP graphs, so weights stream from HBM as in decode.
+
+  value        = whole-job trellis + x + suh + svh + y bytes / elapsed time  (GB/s)
+  roofline     = the dominant kernel (the M=1 4-bpw GEMV): algorithmic bytes per launch / mean
+                 launch duration from HIP events on its stream, vs 8 TB/s
+  cpu_baseline = the C oracle restatement (faithful GEMV) on a bounded sample, host cores
+
+Extras: configuration 4 prefill (M = 2048 through a 64-layer stack, TFLOPS vs 2.5 PF fp16 MFMA),
+configuration 3 small-batch crossover, configuration 2 bitrate sweep.
+
+  python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-sweep] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "qwen38-27b-exl3-rdna4_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+MFMA_FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
+HIDDEN, INTER, KV = 5120, 17408, 1024
+LAYER = [("q", HIDDEN, HIDDEN), ("k", HIDDEN, KV), ("v", HIDDEN, KV), ("o", HIDDEN, HIDDEN),
+         ("gate", HIDDEN, INTER), ("up", HIDDEN, INTER), ("down", INTER, HIDDEN)]
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def algo_bytes(m, k, n, bits):
+    return k * n * bits // 8 + 2 * m * k + 2 * k + 2 * n + 2 * m * n
+
+
+class LayerSet:
+    """One decoder layer's EXL3 weights (device), with the plugin's module grouping."""
+
+    def __init__(self, torch, base, copy_id, bits, mul1=True):
+        self.t = torch
+        self.bits = bits
+        dev = "cuda"
+        self.w = {}
+        for name, k, n in LAYER:
+            tr, su, sv = base[name]
+            T = torch.from_numpy(tr.view(np.int16)).to(dev) if copy_id == 0 else base["_dev"][name][0].clone()
+            self.w[name] = (T, torch.from_numpy(su).to(dev), torch.from_numpy(sv).to(dev))
+        self.mcg, self.mul1 = (not mul1), mul1
+        g = [self.w["gate"], self.w["up"]]
+        self.gu_ptrs = [torch.tensor([x[i].data_ptr() for x in g], dtype=torch.int64, device=dev) for i in range(3)]
+
+    def step(self, x5120, x17408):
+        t = self.t
+        ops = t.ops.exl3rocm
+        w, b, mc, m1 = self.w, self.bits, self.mcg, self.mul1
+        qkv = ops.linear_groups(x5120, [w["q"][0], w["k"][0], w["v"][0]], [w["q"][1], w["k"][1], w["v"][1]],
+                                [w["q"][2], w["k"][2], w["v"][2]], [b, b, b], mc, m1)
+        o = ops.linear(x5120, *w["o"], b, mc, m1)
+        gu = ops.linear_groups(x5120, [w["gate"][0], w["up"][0]], [w["gate"][1], w["up"][1]],
+                               [w["gate"][2], w["up"][2]], [b, b], mc, m1, *self.gu_ptrs)
+        d = ops.linear(x17408, *w["down"], b, mc, m1)
+        return qkv, o, gu, d
+
+
+def launches_per_step():
+    return 3 + 1 + 1 + 1      # q, k, v (differing widths) + o + gate/up grouped + down
+
+
+def build_layers(torch, bits, copies, mul1=True, tag="config1"):
+    from exl3rocm import synth
+    base = {name: synth.layer(tag, f"{name}-b{bits}", k, n, bits) for name, k, n in LAYER}
+    sets = [LayerSet(torch, base, 0, bits, mul1)]
+    base["_dev"] = sets[0].w
+    for c in range(1, copies):
+        sets.append(LayerSet(torch, base, c, bits, mul1))
+    return base, sets
+
+
+def capture_steps(torch, sets, x5120, x17408):
+    """One HIP graph per weight copy (each replays one decode step)."""
+    from exl3rocm import ops as exl3_ops
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for name, k, n in LAYER:
+            exl3_ops.reserve_workspace("cuda", k, n, sets[0].bits, groups=2)
+        for ls in sets:                      # warm every path on the capture stream
+            ls.step(x5120, x17408)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graphs = []
+    for ls in sets:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            ls.step(x5120, x17408)
+        graphs.append(g)
+    torch.cuda.synchronize()
+    return graphs
+
+
+def time_graphs(torch, graphs, steps, warmup):
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / 1e3, wall
+
+
+def per_shape_gemv(torch, sets, x5120, x17408, reps=64):
+    """Mean launch duration of each layer GEMV alone (graph of `reps` launches over the weight
+    copies, HIP events on the replay stream)."""
+    from exl3rocm import kernels as E
+    out = {}
+    s = torch.cuda.Stream()
+    for name, k, n in LAYER:
+        x = x17408 if k == INTER else x5120
+        y = torch.empty(1, n, dtype=torch.float16, device="cuda")
+        with torch.cuda.stream(s):
+            for ls in sets:
+                T, SU, SV = ls.w[name]
+                E.exl3_gemv(x, T, y, SU, None, SV, ls.mcg, ls.mul1)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for r in range(reps):
+                T, SU, SV = sets[r % len(sets)].w[name]
+                E.exl3_gemv(x, T, y, SU, None, SV, sets[0].mcg, sets[0].mul1)
+        with torch.cuda.stream(s):
+            g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(3):
+                g.replay()
+            e1.record(s)
+        s.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (3 * reps)
+        b = algo_bytes(1, k, n, sets[0].bits)
+        out[name] = {"k": k, "n": n, "us": round(us, 3), "gbs": round(b / us / 1e3, 1),
+                     "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+    return out
+
+
+def cpu_baseline(base, bits, budget_s=12.0):
+    """The C oracle's faithful GEMV over the layer's 7 linears (M = 1), repeated within a time
+    budget on the host cores; GB/s of the same algorithmic bytes."""
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    import cpu  # noqa: E402  (oracle: test infrastructure, used here only as the baseline)
+    from exl3rocm import synth
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, len(os.sched_getaffinity(0)))
+    x = {k: synth.activations(synth.key_of("cpu", k), 1, k) for k in (HIDDEN, INTER)}
+    layer_bytes = sum(algo_bytes(1, k, n, bits) for _, k, n in LAYER)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        for name, k, n in LAYER:
+            tr, su, sv = base[name]
+            cpu.linear(x[k], tr, bits, su, sv, 2, threads=threads)
+        reps += 1
+        if time.perf_counter() - t0 > budget_s:
+            break
+    dt = time.perf_counter() - t0
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": round(reps * layer_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} x the 7 linears of one layer at M=1, 4 bpw mul1 (C oracle, OpenMP {threads} "
+                      f"threads, {dt:.1f} s); cpu: {model}"}
+
+
+def prefill_chunk(torch, layers=64, m=2048, bits=4, iters=2):
+    """Configuration 4: M = 2048 through a 64-layer stack of the 7 linears (independent weights per
+    layer, generated on the device), fp16 activations."""
+    from exl3rocm import ops as exl3_ops  # noqa: F401
+    g = torch.Generator(device="cuda").manual_seed(20260923)
+    stack = []
+    for _ in range(layers):
+        lw = {}
+        for name, k, n in LAYER:
+            T = torch.randint(0, 65536, (k // 16, n // 16, 16 * bits), device="cuda", dtype=torch.int32,
+                              generator=g).to(torch.int16)
+            su = (torch.randn(k, device="cuda", generator=g).sign() * torch.exp(
+                0.25 * torch.randn(k, device="cuda", generator=g))).half()
+            sv = (torch.randn(n, device="cuda", generator=g).sign() * torch.exp(
+                0.25 * torch.randn(n, device="cuda", generator=g))).half()
+            lw[name] = (T, su, sv)
+        stack.append(lw)
+    xa = torch.randn(m, HIDDEN, device="cuda", dtype=torch.float16, generator=g)
+    xb = torch.randn(m, INTER, device="cuda", dtype=torch.float16, generator=g)
+    ops = torch.ops.exl3rocm
+
+    def chunk():
+        for lw in stack:
+            for name, k, n in LAYER:
+                ops.linear(xb if k == INTER else xa, *lw[name], bits, False, True)
+
+    chunk()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        chunk()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / iters
+    flops = 2.0 * m * sum(k * n for _, k, n in LAYER) * layers
+    tf = flops / us / 1e6
+    del stack
+    torch.cuda.empty_cache()
+    return {"m": m, "layers": layers, "bits": bits, "us_per_chunk": round(us, 1), "tflops": round(tf, 1),
+            "frac_mfma_fp16": round(tf / MFMA_FP16_PEAK_TFLOPS, 4), "flops_per_chunk": flops}
+
+
+def small_batch(torch, sets, ms=(1, 4, 8, 16, 32)):
+    """Configuration 3: gate/up and down at M in {1, 4, 8, 16, 32}, heavy-tail activations."""
+    from exl3rocm import synth
+    res = {}
+    for name in ("gate", "down"):
+        k = INTER if name == "down" else HIDDEN
+        row = {}
+        for m in ms:
+            x = torch.from_numpy(synth.activations(synth.key_of("cfg3", k, m), m, k, heavy_tail=True)).cuda()
+            fn = (lambda ls, x=x: torch.ops.exl3rocm.linear(x, *ls.w[name], ls.bits, ls.mcg, ls.mul1))
+            for ls in sets:
+                fn(ls)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 4 * len(sets)
+            e0.record()
+            for i in range(reps):
+                fn(sets[i % len(sets)])
+            e1.record()
+            torch.cuda.synchronize()
+            row[f"m{m}_us"] = round(e0.elapsed_time(e1) * 1e3 / reps, 2)
+        res[name] = row
+    return res
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--copies", type=int, default=8)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this engine runs on one GPU; multi-GPU runs are not part of this build "
+              "(see DESIGN.md for how the path would shard)", file=sys.stderr)
+        return 2
+
+    import torch
+    from exl3rocm import _lib, ops  # noqa: F401
+    _lib.lib()
+    bits = 4
+    log("building layer set (4 bpw, mul1) x %d copies" % args.copies)
+    base, sets = build_layers(torch, bits, args.copies)
+    from exl3rocm import synth
+    x5120 = torch.from_numpy(synth.activations(synth.key_of("config1", "x", HIDDEN), 1, HIDDEN)).cuda()
+    x17408 = torch.from_numpy(synth.activations(synth.key_of("config1", "x", INTER), 1, INTER)).cuda()
+    graphs = capture_steps(torch, sets, x5120, x17408)
+    log("timing %d decode steps" % args.steps)
+    elapsed, wall = time_graphs(torch, graphs, args.steps, args.warmup)
+    step_bytes = sum(algo_bytes(1, k, n, bits) for _, k, n in LAYER)
+    value = args.steps * step_bytes / elapsed / 1e9
+    ms_per_step = elapsed * 1e3 / args.steps
+    lps = launches_per_step()
+    avg_launch_us = ms_per_step * 1e3 / lps
+    achieved = step_bytes / lps / avg_launch_us / 1e3
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "gemv_kernel<4,2,1> (every M=1 launch of the step)",
+                "bytes_per_launch": step_bytes / lps, "mean_launch_us": round(avg_launch_us, 3)}
+    extra = {"launches_per_step": lps, "step_bytes": step_bytes, "wall_s": round(wall, 3)}
+    log("per-shape GEMV timing")
+    extra["per_shape_m1"] = per_shape_gemv(torch, sets, x5120, x17408)
+    if not args.no_sweep:
+        log("small-batch crossover")
+        extra["config3_small_batch"] = small_batch(torch, sets)
+        del graphs
+        sweep = {}
+        for b in (2, 3, 5, 6, 8):
+            _, ss = build_layers(torch, b, 4, tag="config2")
+            sweep[f"{b}bpw"] = per_shape_gemv(torch, ss, x5120, x17408, reps=32)
+            del ss
+        _, ss = build_layers(torch, 4, 4, mul1=False, tag="config2")
+        sweep["4bpw_mcg"] = per_shape_gemv(torch, ss, x5120, x17408, reps=32)
+        del ss
+        extra["config2_sweep_m1"] = sweep
+        torch.cuda.empty_cache()
+    if not args.no_prefill:
+        log("prefill chunk (M=2048, 64 layers)")
+        del sets
+        torch.cuda.empty_cache()
+        extra["config4_prefill"] = prefill_chunk(torch)
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline")
+        cpu = cpu_baseline(base, bits)
+    line = {
+        "metric": "EXL3 GEMV GB/s (% HBM peak) at M=1; prefill TFLOPS (% MFMA) at M=2048",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16", "data": "synthetic (counter-RNG seeded trellis / suh / svh / x)",
+        "config": {"workload": "config1: M=1 decode step through the 7 EXL3 linears of a Qwen-27B-shaped layer "
+                               "(hidden 5120, 40q/8kv x 128, intermediate 17408), 4 bpw mul1, 8 weight copies",
+                   "m": 1, "bits": bits, "codebook": "mul1", "copies": args.copies},
+        "frac_hbm": round(value / HBM_PEAK_GBS, 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

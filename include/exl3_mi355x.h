@@ -1,0 +1,139 @@
+/*
+ * exl3_mi355x.h -- C ABI of the MI355X (gfx950) EXL3 quantized-linear library
+ * (libexl3_mi355x.so).
+ *
+ * Every entry point replaces one call of the reference's kernel extension (`exllamav3_ext`,
+ * bound by pybind11 in the un-vendored exllamav3 ROCm fork) as it is called from the vLLM
+ * plugin's custom ops (vllm_plugin/exl3rocm/ops.py) and tests.  Arguments are raw device
+ * pointers, element counts and strides (in elements), plus a hipStream_t passed as void*.
+ * No torch types cross this boundary.
+ *
+ * Conventions
+ *   - fp16 tensors are IEEE binary16; the trellis is the checkpoint's (k/16, n/16, 16*K) int16
+ *     tensor, read as little-endian 16-bit words; suh [k], svh [n] are fp16.
+ *   - Alignment: trellis 16 bytes; x, y, suh, svh 4 bytes with even row strides (fp16 pairs
+ *     move as 32-bit words); violations return EXL3_EINVAL before any launch.
+ *   - Codebook flags: mul1 != 0 -> mul1 (cb 2), else mcg != 0 -> mcg (cb 1), else 3inst (cb 0).
+ *   - K is the bitrate (bits per weight, 1..8).
+ *   - Return status: 0 done; > 0 declined (ineligible but valid call, outputs untouched);
+ *     < 0 invalid arguments or launch failure.
+ *   - All buffers are caller-owned.  Nothing here allocates device memory.  Launches are
+ *     asynchronous on `stream`; no call synchronizes or reads back.  Calls are graph-capturable.
+ *   - The GEMV entry points need a caller workspace of exl3_gemv_workspace_size() bytes whose
+ *     first bytes (completion counters) are zero before the first call; every call leaves them
+ *     zero again.  Calls that overlap on one workspace race: give concurrent streams their own.
+ *   - Results are deterministic: repeat calls and different streams give bitwise-equal output,
+ *     and each row of an m-row call equals the m == 1 call of that row.
+ */
+#ifndef EXL3_MI355X_H
+#define EXL3_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define EXL3_ABI_VERSION 1
+#define EXL3_MAX_GROUPS 4       /* groups per grouped launch (reference EXL3_GEMV_MRG_MAX) */
+#define EXL3_GEMV_MAX_ROWS 32   /* rows handled by the fused GEMV */
+
+#define EXL3_OK 0
+#define EXL3_DECLINED 1
+#define EXL3_EINVAL (-1)
+#define EXL3_ELAUNCH (-2)
+#define EXL3_EWORKSPACE (-3)
+
+int exl3_abi_version(void);
+
+/* Codebook decode of raw 16-bit states to fp32 values.
+ * Replaces `decode(codes int16[16,256], out fp32[16,256], mcg, mul1)`
+ * (reference tests/test_gpu_parity.py:101-109). */
+int exl3_decode(const void* states, void* out_f32, int64_t count, int mcg, int mul1, void* stream);
+
+/* Dense fp16 W[k, n] from the trellis.
+ * Replaces `reconstruct(W, trellis, K, mcg, mul1)` (reference vllm_plugin/exl3rocm/ops.py:93). */
+int exl3_reconstruct(void* W, const void* trellis, int k, int n, int K, int mcg, int mul1, void* stream);
+
+/* Columns [n0, n0 + n_out) of W into a [k, n_out] buffer with row stride ldw (multiples of 16).
+ * Replaces `reconstruct_slice(W, trellis, K, mcg, mul1, n0)` (reference ops.py:95). */
+int exl3_reconstruct_slice(void* W, int64_t ldw, const void* trellis, int k, int n, int K, int mcg, int mul1, int n0,
+                           int n_out, void* stream);
+
+/* Blockwise 128-point Hadamard over rows: out = fp16(H128(in [* pre]) * r * scale) [* post],
+ * r = 0.088388347648; pre / post may be NULL; in == out is allowed.
+ * Replaces `had_r_128(in, out, pre, post, scale)` (reference ops.py:88,97). */
+int exl3_had_r_128(const void* in, int64_t ld_in, void* out, int64_t ld_out, int rows, int cols, const void* pre,
+                   const void* post, float scale, void* stream);
+
+/* Split count the fused GEMV uses for a (k, n) layer (diagnostic). */
+int exl3_gemv_splits(int k, int n);
+
+/* Workspace bytes the fused GEMV needs for m rows and `groups` groups.
+ * Has no reference counterpart: the reference fork allocates its counters inside the extension
+ * (vllm_plugin/patches/exl3-fork/0003-fused-had-graph-capture.patch:17-40); here the caller owns them. */
+size_t exl3_gemv_workspace_size(int m, int k, int n, int K, int groups);
+
+/* Eligibility of the fused multi-row GEMV.
+ * Replaces `exl3_gemv_mr_supported(m, k, n, K, mcg, mul1)`
+ * (reference vllm_plugin/patches/exl3-fork/0002-gemv-multirow.patch:334-338).  Unlike the
+ * reference (mul1 only), every codebook is supported; 1 <= m <= 32, k and n multiples of 128. */
+int exl3_gemv_mr_supported(int m, int k, int n, int K, int mcg, int mul1);
+
+/* M == 1 EXL3 linear, y = fp16(H(fp16(H(x*suh)) . W) * svh) with fused input and output
+ * Hadamards.  m != 1 declines (returns 1) without touching y.
+ * Replaces `exl3_gemv(A, B, C, suh, A_had, svh, mcg, mul1)` (reference tests/test_gpu_parity.py:160)
+ * and the M == 1 route of `exl3_gemm` (reference ops.py:80-82).  A_had is accepted for
+ * signature parity; the rotated input lives in LDS and A_had is not written. */
+int exl3_gemv(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh, void* A_had,
+              const void* svh, int m, int k, int n, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
+              void* stream);
+
+/* 1 <= m <= 32 EXL3 linear, output rows with stride ldy.
+ * Replaces `exl3_gemv_mr(A, B, C, suh, A_had, svh, K, mcg, mul1)` (reference ops.py:85;
+ * 0002-gemv-multirow.patch:409-422). */
+int exl3_gemv_mr(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh, void* A_had,
+                 const void* svh, int m, int k, int n, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
+                 void* stream);
+
+/* Up to 4 groups sharing x (equal k, n, K): group i writes columns [i*n, (i+1)*n) of y.
+ * trellis / suh / svh are host arrays of device pointers.
+ * Replaces `exl3_gemv_mr_grouped(A, [B], C, [suh], A_had, [svh], K, mcg, mul1, bszm)`
+ * (reference ops.py:164-165; 0002-gemv-multirow.patch:424-440).  bszm_for_warps is accepted for
+ * signature parity: the split choice here never depends on it. */
+int exl3_gemv_mr_grouped(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
+                         const void* const* suh, void* A_had, const void* const* svh, int groups, int m, int k, int n,
+                         int K, int mcg, int mul1, int bszm_for_warps, void* workspace, size_t ws_bytes, void* stream);
+
+/* Grouped M == 1 linear over device int64 pointer tables (one entry per group), output
+ * (groups, 1, n) == the concatenated row.
+ * Replaces `exl3_mgemm(x, ptrs_trellis, y, ptrs_suh, xh, ptrs_svh, ...)` (reference ops.py:137-138). */
+int exl3_mgemm(const void* x, const int64_t* ptrs_trellis, void* y, const int64_t* ptrs_suh, void* xh,
+               const int64_t* ptrs_svh, int groups, int k, int n, int K, int mcg, int mul1, void* workspace,
+               size_t ws_bytes, void* stream);
+
+/* Dense fp16 GEMM y[m, n] = fp16(x[m, k] . W[k, n]) with fp32 accumulation (MFMA).
+ * Replaces `hgemm_recon(xh, W, y)` (reference ops.py:96), which accumulates in fp16. */
+int exl3_hgemm_recon(const void* x, int64_t ldx, const void* W, int64_t ldw, void* y, int64_t ldy, int m, int k, int n,
+                     void* stream);
+
+/* Prefill EXL3 linear for any m: the trellis is decoded into LDS tiles and fed to fp16 MFMA
+ * with fp32 accumulation; input and output Hadamards run as separate passes.  xh is an
+ * [m, k] fp16 scratch (the rotated input).
+ * Replaces the reconstruct + hgemm_recon route of `exl3rocm::linear` (reference ops.py:86-97). */
+int exl3_gemm_trellis(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh,
+                      void* xh, const void* svh, int m, int k, int n, int K, int mcg, int mul1, void* stream);
+
+/* Dispatcher by row count: m <= 32 -> fused GEMV, else the prefill GEMM.  Returns the route
+ * tag (1 = GEMV, 2 = prefill GEMM) or a negative error.
+ * Replaces `exl3_gemm(A, B, C, suh, A_had, svh, -1, mcg, mul1, 0) -> int` (reference ops.py:82). */
+int exl3_gemm(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh, void* A_had,
+              const void* svh, int m, int k, int n, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
+              void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXL3_MI355X_H */

@@ -1,0 +1,245 @@
+// exl3_device.h -- gfx950 (CDNA4, wave64) device building blocks for the EXL3 trellis linear.
+//
+//  * q-block trellis decoder: one lane turns the 32 consecutive ring positions of a tile's
+//    "q-block" (positions 32q .. 32q+31 == tile columns q and q+8, all 16 rows) into 16 packed
+//    fp16 pairs, specialised per bitrate at compile time (window extraction plan, codebook).
+//  * wave64 128-point Hadamard (2 elements per lane, float64 butterflies: exact for fp16 data).
+//  * float64 -> fp16 round-to-nearest-even.
+//
+// Format facts restated from the reference oracle (reference/exl3_oracle.py):
+//  * a tile is 16*bits little-endian u16 words == 8*bits u32 words, bits numbered MSB-first
+//    across the u32 ring (:149-153);
+//  * the state at position t is the 16-bit window ending at ring bit (t+1)*bits (:156-188);
+//  * position t -> (row, col): L = t>>3, i = t&7, row = 2(L%4) + (i&1) + 8((i>>1)&1),
+//    col = 2(L>>3) + ((L>>2)&1) + 8(i>>2) (:129-146);
+//  * codebooks (:67-119): mul1 v = fp16((1024 + bytesum(w*0x83DCD12D)) * k_inv + k_bias) with one
+//    rounding; mcg / 3inst: x = w*0xCBAC1FED or w*89226354 + 64248484, x' = (x & 0x8FFF8FFF) ^
+//    0x3B603B60, v = fp16(fp16(x'.lo) + fp16(x'.hi)).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace exl3 {
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr double R_SCALE = 0.088388347648;   // the Hadamard scale of every reference call site
+
+// ------------------------------------------------------------------------------------------
+// float64 -> fp16 bits, round to nearest even (exact single rounding; used by the Hadamards,
+// whose float64 butterflies are exact on fp16 data, so the result equals the oracle's).
+// ------------------------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t f64_to_f16_bits(double v)
+{
+    const uint64_t b = (uint64_t) __double_as_longlong(v);
+    const uint32_t sign = (uint32_t) (b >> 48) & 0x8000u;
+    const uint64_t mag = b & 0x7FFFFFFFFFFFFFFFull;
+    const int e16 = (int) (mag >> 52) - 1023;
+    if (e16 < -25) return sign;                        // below half the smallest subnormal
+    if (e16 >= 16) return sign | 0x7C00u;              // overflow (no NaN inputs on this path)
+    const uint64_t m = (mag & 0xFFFFFFFFFFFFFull) | (1ull << 52);
+    const int shift = e16 >= -14 ? 42 : 42 + (-14 - e16);
+    uint64_t kept = m >> shift;
+    const uint64_t rem = m & ((1ull << shift) - 1);
+    const uint64_t half = 1ull << (shift - 1);
+    if (rem > half || (rem == half && (kept & 1))) kept++;
+    uint32_t r = e16 >= -14 ? (uint32_t) (((e16 + 15) << 10) + (int) kept - 1024) : (uint32_t) kept;
+    if (r > 0x7C00u) r = 0x7C00u;
+    return sign | r;
+}
+
+__device__ __forceinline__ f16 bits_f16(uint32_t b) { return __builtin_bit_cast(f16, (uint16_t) b); }
+__device__ __forceinline__ uint32_t f16_bits(f16 h) { return (uint32_t) __builtin_bit_cast(uint16_t, h); }
+
+// ------------------------------------------------------------------------------------------
+// Wave64 Hadamard on 128 values: lane L holds elements 2L (v0) and 2L+1 (v1).  Natural-order
+// Sylvester H[i,j] = (-1)^popcount(i&j): stage bit 0 is in-lane, bits 1..6 are lane xor 1..32.
+// ------------------------------------------------------------------------------------------
+__device__ __forceinline__ double shfl_xor_f64(double v, int mask)
+{
+    const int lane = __lane_id();
+    const int src = (lane ^ mask) << 2;
+    uint64_t u = (uint64_t) __double_as_longlong(v);
+    uint32_t lo = (uint32_t) __builtin_amdgcn_ds_bpermute(src, (int) (uint32_t) u);
+    uint32_t hi = (uint32_t) __builtin_amdgcn_ds_bpermute(src, (int) (uint32_t) (u >> 32));
+    return __longlong_as_double((long long) (((uint64_t) hi << 32) | lo));
+}
+
+__device__ __forceinline__ void wht128_f64(double& v0, double& v1)
+{
+    const int lane = __lane_id();
+    double a = v0 + v1, b = v0 - v1;
+    v0 = a;
+    v1 = b;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const double p0 = shfl_xor_f64(v0, m), p1 = shfl_xor_f64(v1, m);
+        const bool upper = (lane & m) != 0;
+        v0 = upper ? p0 - v0 : v0 + p0;
+        v1 = upper ? p1 - v1 : v1 + p1;
+    }
+}
+
+// Full 128-block stage on a wave: in -> fp16(Had128(in [* pre]) * scale) [* post], fp16 bits.
+// pre / post may be null.  `in` and `out` are f16x2 views, lane L handles elements 2L, 2L+1.
+__device__ __forceinline__ uint32_t had128_pair(uint32_t in2, uint32_t pre2, bool has_pre, uint32_t post2,
+                                                bool has_post, double scale)
+{
+    f16x2 x = __builtin_bit_cast(f16x2, in2);
+    if (has_pre) x = x * __builtin_bit_cast(f16x2, pre2);       // one fp16 rounding per product
+    double v0 = (double) x[0], v1 = (double) x[1];
+    wht128_f64(v0, v1);
+    f16x2 y;
+    y[0] = bits_f16(f64_to_f16_bits(v0 * scale));
+    y[1] = bits_f16(f64_to_f16_bits(v1 * scale));
+    if (has_post) y = y * __builtin_bit_cast(f16x2, post2);
+    return __builtin_bit_cast(uint32_t, y);
+}
+
+// ------------------------------------------------------------------------------------------
+// Codebook constants
+// ------------------------------------------------------------------------------------------
+template <int CB> struct Codebook;
+template <> struct Codebook<2> { static constexpr uint32_t lo = 0xD12Du, hi = 0x83DCu, add = 0; };       // mul1
+template <> struct Codebook<1> { static constexpr uint32_t lo = 0x1FEDu, hi = 0xCBACu, add = 0; };       // mcg
+template <> struct Codebook<0> { static constexpr uint32_t lo = 0x7C72u, hi = 0x0551u, add = 64248484u; }; // 3inst
+
+// 32-bit hash of the 16-bit state held in half H (0 = lo, 1 = hi) of r, in two full-rate ops:
+//   q = (s*C_hi [+ add_hi]) << 16 [| add_lo]   (v_pk_mul_lo_u16 / v_pk_mad_u16, lo lane * 0)
+//   x = s*C_lo + q                              (v_mad_u32_u16)
+// Both read only the selected 16 bits of r, so window extraction never needs masking.
+template <int CB, int H>
+__device__ __forceinline__ uint32_t state_hash(uint32_t r, uint32_t k_hi, uint32_t k_add, uint32_t k_lo)
+{
+    uint32_t q, x;
+    if constexpr (CB == 0)
+        asm("v_pk_mad_u16 %0, %1, %2, %3 op_sel:[%4,0,0] op_sel_hi:[%4,1,1]"
+            : "=v"(q) : "v"(r), "s"(k_hi), "v"(k_add), "n"(H));
+    else
+        asm("v_pk_mul_lo_u16 %0, %1, %2 op_sel:[%3,0] op_sel_hi:[%3,1]" : "=v"(q) : "v"(r), "s"(k_hi), "n"(H));
+    asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[%4,0,0,0]" : "=v"(x) : "v"(r), "s"(k_lo), "v"(q), "n"(H));
+    return x;
+}
+
+// ------------------------------------------------------------------------------------------
+// q-block window plan.  A lane holds words w[-1 .. BITS-1] of its q-block (relative to the q-block's
+// first word; w[-1] is the ring predecessor) as W[0 .. BITS].  State p in [0, 32) is the window
+// ending at bit e = (p+1)*BITS.  It is read from a 32-bit register r, half H:
+//   e % 32 == 0            -> r = w[e/32 - 1], lo
+//   e % 32 == 16           -> r = w[e/32],     hi
+//   BITS | 16, e%32 < 16   -> r = R(e + 16),   hi    (one alignbit serves windows e and e+16)
+//   otherwise              -> r = R(e),        lo
+// where R(E) = the 32 ring bits ending at E = alignbit(w[E/32 - 1], w[E/32], 32*(E/32 + 1) - E).
+// ------------------------------------------------------------------------------------------
+struct WinSrc { int kind; int a; int b; int shift; int half; };   // kind 0: word a; kind 1: alignbit(a, b, shift)
+
+template <int BITS>
+__host__ __device__ constexpr WinSrc win_src(int p)
+{
+    const int e = (p + 1) * BITS;
+    if (e % 32 == 0) return {0, e / 32 - 1, 0, 0, 0};
+    if (e % 32 == 16) return {0, e / 32, 0, 0, 1};
+    int E = e, half = 0;
+    if ((16 % BITS) == 0 && (e % 32) < 16) { E = e + 16; half = 1; }
+    return {1, E / 32 - 1, E / 32, 32 * (E / 32 + 1) - E, half};
+}
+
+// Register for state p: W[] is indexed from word -1.
+template <int BITS, int P>
+__device__ __forceinline__ uint32_t win_reg(const uint32_t* W)
+{
+    constexpr WinSrc s = win_src<BITS>(P);
+    if constexpr (s.kind == 0) return W[s.a + 1];
+    else return __builtin_amdgcn_alignbit(W[s.a + 1], W[s.b + 1], (uint32_t) s.shift);
+}
+
+template <int BITS, int CB, int P>
+__device__ __forceinline__ uint32_t state_x(const uint32_t* W, uint32_t k_hi, uint32_t k_add, uint32_t k_lo)
+{
+    constexpr WinSrc s = win_src<BITS>(P);
+    return state_hash<CB, s.half>(win_reg<BITS, P>(W), k_hi, k_add, k_lo);
+}
+
+// Decode the pair of states (2I, 2I+1) of the q-block into one packed fp16 pair (lo = state 2I).
+template <int BITS, int CB, int I>
+__device__ __forceinline__ uint32_t decode_pair(const uint32_t* W, uint32_t k_hi, uint32_t k_add, uint32_t k_lo,
+                                                uint32_t c6400)
+{
+    const uint32_t x0 = state_x<BITS, CB, 2 * I>(W, k_hi, k_add, k_lo);
+    const uint32_t x1 = state_x<BITS, CB, 2 * I + 1>(W, k_hi, k_add, k_lo);
+    if constexpr (CB == 2) {
+        // 0x6400 + bytesum: the fp16 bit pattern of 1024 + s (exact for s <= 1020)
+        const uint32_t s0 = __builtin_amdgcn_udot4(x0, 0x01010101u, c6400, false);
+        const uint32_t s1 = __builtin_amdgcn_udot4(x1, 0x01010101u, c6400, false);
+        f16x2 h = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(s1, s0, 0x05040100u));
+        const f16x2 k_inv = {bits_f16(0x1EEEu), bits_f16(0x1EEEu)};
+        const f16x2 k_bias = {bits_f16(0xC931u), bits_f16(0xC931u)};
+        h = __builtin_elementwise_fma(h, k_inv, k_bias);           // v_pk_fma_f16: one rounding
+        return __builtin_bit_cast(uint32_t, h);
+    } else {
+        // gather lo halves and hi halves of the two hashes, then the mask/xor (half-symmetric
+        // constants commute with the byte permutation) and one packed fp16 add
+        uint32_t lo = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
+        uint32_t hi = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
+        lo = (lo & 0x8FFF8FFFu) ^ 0x3B603B60u;
+        hi = (hi & 0x8FFF8FFFu) ^ 0x3B603B60u;
+        const f16x2 r = __builtin_bit_cast(f16x2, lo) + __builtin_bit_cast(f16x2, hi);
+        return __builtin_bit_cast(uint32_t, r);
+    }
+}
+
+template <int BITS, int CB, int I>
+__device__ __forceinline__ void decode_pairs_rec(const uint32_t* W, uint32_t* P, uint32_t k_hi, uint32_t k_add,
+                                                 uint32_t k_lo, uint32_t c6400)
+{
+    if constexpr (I < 16) {
+        P[I] = decode_pair<BITS, CB, I>(W, k_hi, k_add, k_lo, c6400);
+        decode_pairs_rec<BITS, CB, I + 1>(W, P, k_hi, k_add, k_lo, c6400);
+    }
+}
+
+// Decode all 32 states of a q-block: P[i] = (state 2i, state 2i+1) as fp16 pairs.
+// State p of q-block q is tile position t = 32q + p: column q + 8*((p>>2)&1),
+// row 8*((p>>1)&1) + 2*(p>>3) + (p&1).
+template <int BITS, int CB>
+__device__ __forceinline__ void decode_qblock(const uint32_t* W, uint32_t* P)
+{
+    // constants live in SGPRs / one VGPR; the asm constraints keep them out of literals
+    const uint32_t k_hi = Codebook<CB>::hi << 16;
+    const uint32_t k_add = CB == 0 ? Codebook<0>::add : 0u;
+    const uint32_t k_lo = Codebook<CB>::lo;
+    const uint32_t c6400 = 0x6400u;
+    decode_pairs_rec<BITS, CB, 0>(W, P, k_hi, k_add, k_lo, c6400);
+}
+
+// Load the BITS+1 words a lane needs for q-block q of a tile (tile32 = tile base as u32 words).
+template <int BITS>
+__device__ __forceinline__ void load_qblock(const uint32_t* __restrict__ tile32, int q, uint32_t* W)
+{
+    const uint32_t* p = tile32 + q * BITS;
+    if constexpr (BITS % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < BITS / 4; ++i) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(p + 4 * i);
+            W[1 + 4 * i] = v[0]; W[2 + 4 * i] = v[1]; W[3 + 4 * i] = v[2]; W[4 + 4 * i] = v[3];
+        }
+    } else if constexpr (BITS % 2 == 0) {
+#pragma unroll
+        for (int i = 0; i < BITS / 2; ++i) {
+            const u32x2 v = *reinterpret_cast<const u32x2*>(p + 2 * i);
+            W[1 + 2 * i] = v[0]; W[2 + 2 * i] = v[1];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) W[1 + i] = p[i];
+    }
+    const int prev = q == 0 ? 8 * BITS - 1 : q * BITS - 1;
+    W[0] = tile32[prev];
+}
+
+}  // namespace exl3

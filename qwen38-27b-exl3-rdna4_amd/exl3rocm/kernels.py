@@ -1,0 +1,224 @@
+"""Tensor-level wrappers of the C ABI (one per reference extension call), on the current stream.
+
+Each function takes torch tensors, validates shapes the way the reference bindings do
+(TORCH_CHECK -> RuntimeError) and calls libexl3_mi355x.so.  Names follow the reference
+extension (`exllamav3_ext`): decode, reconstruct, reconstruct_slice, had_r_128, exl3_gemv,
+exl3_gemv_mr, exl3_gemv_mr_grouped, exl3_gemv_mr_supported, exl3_mgemm, hgemm_recon, exl3_gemm.
+"""
+from __future__ import annotations
+
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib as L
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _cb_flags(mcg: bool, mul1: bool):
+    return int(bool(mcg)), int(bool(mul1))
+
+
+def _need(cond: bool, msg: str):
+    if not cond:
+        raise RuntimeError(f"exl3rocm: {msg}")
+
+
+def _cuda(*ts):
+    for t in ts:
+        _need(t is None or t.is_cuda, "tensors must be on a GPU (no CPU path)")
+
+
+def _bits_of(trellis: torch.Tensor) -> int:
+    return trellis.shape[-1] // 16
+
+
+# ---------------------------------------------------------------------------------------------
+# workspace (GEMV split-K partials + completion counters), one per (device, stream)
+# ---------------------------------------------------------------------------------------------
+_workspaces: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int, stream: Optional[int] = None) -> torch.Tensor:
+    """Grow-only zeroed workspace for the current (or given) stream of `device`.  Reserve it at
+    load time (Exl3LinearMethod.process_weights_after_loading) so graph capture never allocates."""
+    device = torch.device(device)
+    if stream is None:
+        stream = torch.cuda.current_stream(device).cuda_stream
+    key = (device, stream)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        _need(not torch.cuda.is_current_stream_capturing(), "workspace must be reserved before graph capture")
+        buf = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
+        _workspaces[key] = buf
+    return buf
+
+
+def gemv_workspace_bytes(m: int, k: int, n: int, K: int, groups: int = 1) -> int:
+    return int(L.lib().exl3_gemv_workspace_size(m, k, n, K, groups))
+
+
+# ---------------------------------------------------------------------------------------------
+def decode(codes: torch.Tensor, out: torch.Tensor, mcg: bool, mul1: bool) -> None:
+    _cuda(codes, out)
+    _need(codes.dtype == torch.int16 and out.dtype == torch.float32 and codes.numel() == out.numel(),
+          "decode: int16 codes and a float32 output of the same size")
+    _need(codes.is_contiguous() and out.is_contiguous(), "decode: contiguous tensors")
+    L.check(L.lib().exl3_decode(codes.data_ptr(), out.data_ptr(), codes.numel(), *_cb_flags(mcg, mul1),
+                                _stream(codes)), "decode")
+
+
+def reconstruct(W: torch.Tensor, trellis: torch.Tensor, K: int, mcg: bool, mul1: bool) -> None:
+    _cuda(W, trellis)
+    k, n = trellis.shape[0] * 16, trellis.shape[1] * 16
+    _need(trellis.shape[2] == 16 * K, "reconstruct: trellis last dim must be 16*K")
+    _need(W.dtype == torch.float16 and tuple(W.shape) == (k, n) and W.is_contiguous(), "reconstruct: W [k, n] fp16")
+    L.check(L.lib().exl3_reconstruct(W.data_ptr(), trellis.data_ptr(), k, n, K, *_cb_flags(mcg, mul1),
+                                     _stream(W)), "reconstruct")
+
+
+def reconstruct_slice(W: torch.Tensor, trellis: torch.Tensor, K: int, mcg: bool, mul1: bool, n0: int) -> None:
+    _cuda(W, trellis)
+    k, n = trellis.shape[0] * 16, trellis.shape[1] * 16
+    _need(trellis.shape[2] == 16 * K, "reconstruct_slice: trellis last dim must be 16*K")
+    _need(W.dtype == torch.float16 and W.dim() == 2 and W.shape[0] == k and W.stride(1) == 1,
+          "reconstruct_slice: W [k, w] fp16 with unit column stride")
+    L.check(L.lib().exl3_reconstruct_slice(W.data_ptr(), W.stride(0), trellis.data_ptr(), k, n, K,
+                                           *_cb_flags(mcg, mul1), n0, W.shape[1], _stream(W)), "reconstruct_slice")
+
+
+def had_r_128(inp: torch.Tensor, out: torch.Tensor, pre: Optional[torch.Tensor], post: Optional[torch.Tensor],
+              scale: float) -> None:
+    """Blockwise Hadamard over the last dim (multiple of 128); 2-D operands may have any row stride."""
+    _cuda(inp, out, pre, post)
+    _need(inp.dtype == torch.float16 and out.dtype == torch.float16 and inp.shape == out.shape,
+          "had_r_128: fp16 tensors of equal shape")
+    _need(inp.stride(-1) == 1 and out.stride(-1) == 1, "had_r_128: unit stride rows")
+    cols = inp.shape[-1]
+
+    def as2d(t):
+        if t.dim() == 2:
+            return t
+        _need(t.is_contiguous(), "had_r_128: tensors above 2-D must be contiguous")
+        return t.view(-1, cols)
+
+    i2, o2 = as2d(inp), as2d(out)
+    rows = i2.shape[0]
+    L.check(L.lib().exl3_had_r_128(i2.data_ptr(), i2.stride(0) if rows > 1 else cols, o2.data_ptr(),
+                                   o2.stride(0) if rows > 1 else cols, rows, cols,
+                                   pre.data_ptr() if pre is not None else None,
+                                   post.data_ptr() if post is not None else None, float(scale), _stream(inp)),
+            "had_r_128")
+
+
+def _rows(x: torch.Tensor):
+    k = x.shape[-1]
+    x2 = x.reshape(-1, k)
+    _need(x2.dtype == torch.float16 and x2.stride(-1) == 1, "x must be fp16 with unit stride")
+    return x2, x2.shape[0], k
+
+
+def _ldy(y: torch.Tensor, n: int) -> int:
+    _need(y.dtype == torch.float16 and y.stride(-1) == 1, "output must be fp16 with unit column stride")
+    return y.stride(-2) if y.dim() >= 2 and y.shape[-2] > 1 else max(n, y.shape[-1])
+
+
+def exl3_gemv_mr_supported(m: int, k: int, n: int, K: int, mcg: bool, mul1: bool) -> bool:
+    return bool(L.lib().exl3_gemv_mr_supported(m, k, n, K, *_cb_flags(mcg, mul1)))
+
+
+def exl3_gemv(A, B, C, suh, A_had, svh, mcg: bool, mul1: bool) -> int:
+    """M == 1 linear; returns 0 (done) or 1 (declined, C untouched)."""
+    _cuda(A, B, C, suh, svh)
+    x2, m, k = _rows(A)
+    n = svh.shape[0]
+    K = _bits_of(B)
+    ws = workspace(A.device, gemv_workspace_bytes(max(m, 1), k, n, K))
+    return L.check(L.lib().exl3_gemv(x2.data_ptr(), x2.stride(0) if m > 1 else k, B.data_ptr(), C.data_ptr(),
+                                     _ldy(C, n), suh.data_ptr(), A_had.data_ptr() if A_had is not None else None,
+                                     svh.data_ptr(), m, k, n, K, *_cb_flags(mcg, mul1), ws.data_ptr(), ws.numel(),
+                                     _stream(A)), "exl3_gemv")
+
+
+def exl3_gemv_mr(A, B, C, suh, A_had, svh, K: int, mcg: bool, mul1: bool) -> int:
+    _cuda(A, B, C, suh, svh)
+    x2, m, k = _rows(A)
+    n = svh.shape[0]
+    _need(B.shape[-1] == 16 * K, "exl3_gemv_mr: trellis last dim must be 16*K")
+    ws = workspace(A.device, gemv_workspace_bytes(m, k, n, K))
+    return L.check(L.lib().exl3_gemv_mr(x2.data_ptr(), x2.stride(0) if m > 1 else k, B.data_ptr(), C.data_ptr(),
+                                        _ldy(C, n), suh.data_ptr(), None, svh.data_ptr(), m, k, n, K,
+                                        *_cb_flags(mcg, mul1), ws.data_ptr(), ws.numel(), _stream(A)),
+                   "exl3_gemv_mr")
+
+
+def exl3_gemv_mr_grouped(A, B: Sequence[torch.Tensor], C, suh: Sequence[torch.Tensor], A_had,
+                         svh: Sequence[torch.Tensor], K: int, mcg: bool, mul1: bool, bszm_for_warps: int = 1) -> int:
+    _cuda(A, C, *B, *suh, *svh)
+    x2, m, k = _rows(A)
+    g = len(B)
+    n = svh[0].shape[0]
+    _need(1 <= g <= L.MAX_GROUPS and len(suh) == g and len(svh) == g, "grouped: 1..4 groups with suh/svh each")
+    _need(all(s.shape[0] == n for s in svh), "grouped: groups must share n")
+    _need(C.shape[-1] >= g * n, "grouped: output narrower than groups * n")
+    ws = workspace(A.device, gemv_workspace_bytes(m, k, n, K, g))
+    pt, _a = L.ptr_array([b.data_ptr() for b in B])
+    ps, _b = L.ptr_array([s.data_ptr() for s in suh])
+    pv, _c = L.ptr_array([s.data_ptr() for s in svh])
+    return L.check(L.lib().exl3_gemv_mr_grouped(x2.data_ptr(), x2.stride(0) if m > 1 else k, pt, C.data_ptr(),
+                                                _ldy(C, g * n), ps, None, pv, g, m, k, n, K, *_cb_flags(mcg, mul1),
+                                                bszm_for_warps, ws.data_ptr(), ws.numel(), _stream(A)),
+                   "exl3_gemv_mr_grouped")
+
+
+def exl3_mgemm(x, ptrs_trellis, y, ptrs_suh, xh, ptrs_svh, K: int, mcg: bool, mul1: bool) -> int:
+    """Grouped M == 1 over int64 device pointer tables; y is (groups, 1, n)."""
+    _cuda(x, ptrs_trellis, y, ptrs_suh, ptrs_svh)
+    g = ptrs_trellis.numel()
+    k = x.shape[-1]
+    n = y.shape[-1]
+    _need(x.numel() == k and x.dtype == torch.float16 and x.is_contiguous(), "mgemm: x is one fp16 row")
+    _need(y.is_contiguous() and y.numel() == g * n, "mgemm: y (groups, 1, n) contiguous")
+    for t in (ptrs_trellis, ptrs_suh, ptrs_svh):
+        _need(t.dtype == torch.int64 and t.numel() == g and t.is_contiguous(), "mgemm: int64 pointer tables")
+    ws = workspace(x.device, gemv_workspace_bytes(1, k, n, K, g))
+    return L.check(L.lib().exl3_mgemm(x.data_ptr(), ptrs_trellis.data_ptr(), y.data_ptr(), ptrs_suh.data_ptr(),
+                                      xh.data_ptr() if xh is not None else None, ptrs_svh.data_ptr(), g, k, n, K,
+                                      *_cb_flags(mcg, mul1), ws.data_ptr(), ws.numel(), _stream(x)), "exl3_mgemm")
+
+
+def hgemm_recon(xh: torch.Tensor, W: torch.Tensor, y: torch.Tensor) -> None:
+    _cuda(xh, W, y)
+    x2, m, k = _rows(xh)
+    _need(W.dtype == torch.float16 and W.dim() == 2 and W.shape[0] == k and W.stride(1) == 1, "hgemm_recon: W [k, n]")
+    n = W.shape[1]
+    L.check(L.lib().exl3_hgemm_recon(x2.data_ptr(), x2.stride(0) if m > 1 else k, W.data_ptr(), W.stride(0),
+                                     y.data_ptr(), _ldy(y, n), m, k, n, _stream(xh)), "hgemm_recon")
+
+
+def exl3_gemm_trellis(A, B, C, suh, xh, svh, K: int, mcg: bool, mul1: bool) -> None:
+    _cuda(A, B, C, suh, xh, svh)
+    x2, m, k = _rows(A)
+    n = svh.shape[0]
+    _need(xh.numel() >= m * k and xh.dtype == torch.float16 and xh.is_contiguous(), "gemm: xh scratch [m, k] fp16")
+    L.check(L.lib().exl3_gemm_trellis(x2.data_ptr(), x2.stride(0) if m > 1 else k, B.data_ptr(), C.data_ptr(),
+                                      _ldy(C, n), suh.data_ptr(), xh.data_ptr(), svh.data_ptr(), m, k, n, K,
+                                      *_cb_flags(mcg, mul1), _stream(A)), "exl3_gemm_trellis")
+
+
+def exl3_gemm(A, B, C, suh, A_had, svh, force_shape_idx: int = -1, mcg: bool = False, mul1: bool = True,
+              force_kernel: int = 0) -> int:
+    """Row-count dispatcher; returns the route tag (1 = fused GEMV, 2 = prefill GEMM)."""
+    _cuda(A, B, C, suh, A_had, svh)
+    x2, m, k = _rows(A)
+    n = svh.shape[0]
+    K = _bits_of(B)
+    ws = workspace(A.device, gemv_workspace_bytes(min(max(m, 1), L.GEMV_MAX_ROWS), k, n, K)) \
+        if m <= L.GEMV_MAX_ROWS else None
+    return L.check(L.lib().exl3_gemm(x2.data_ptr(), x2.stride(0) if m > 1 else k, B.data_ptr(), C.data_ptr(),
+                                     _ldy(C, n), suh.data_ptr(), A_had.data_ptr(), svh.data_ptr(), m, k, n, K,
+                                     *_cb_flags(mcg, mul1), ws.data_ptr() if ws is not None else None,
+                                     ws.numel() if ws is not None else 0, _stream(A)), "exl3_gemm")

@@ -1,0 +1,164 @@
+"""
+EXL3 linear on MI355X as opaque torch custom ops, so torch.compile and HIP-graph capture treat
+each call as one node.  Same op names, schemas and routing contract as the reference plugin's
+ops (vllm_plugin/exl3rocm/ops.py:65-180); kernels come from libexl3_mi355x.so.
+
+One call computes one checkpoint tensor ("group"): y = had(had(x * suh) @ W_inner) * svh.
+Routing by rows M:
+  M <= EXL3_MR_MAX (32)  -> fused GEMV (input Hadamard, trellis decode + MFMA dot, split-K
+                            reduction and output Hadamard in one launch); every row is bitwise
+                            equal to the M == 1 call of that row
+  M  > EXL3_MR_MAX       -> prefill GEMM (trellis decoded into LDS, fp16 MFMA, fp32 accumulate)
+                            between standalone input / output Hadamards; EXL3_PREFILL=recon takes
+                            the reference's reconstruct + hgemm route instead
+"""
+from __future__ import annotations
+
+import os
+from typing import Optional
+
+import torch
+
+from . import _lib
+from . import kernels as E
+
+MR_MAX = min(int(os.environ.get("EXL3_MR_MAX", str(_lib.GEMV_MAX_ROWS))), _lib.GEMV_MAX_ROWS)
+# widest non-lm_head layer (17408): the shared reconstruction buffer of the `recon` prefill route
+RECON_SLICE_N = int(os.environ.get("EXL3_RECON_SLICE_N", "17408"))
+PREFILL_ROUTE = os.environ.get("EXL3_PREFILL", "fused")
+# timing-only debug switch: quantized linears return zeros without running kernels
+_DEBUG_SKIP = os.environ.get("EXL3_DEBUG_SKIP_LINEAR") == "1"
+
+_wbuf: dict = {}
+
+
+def ext():
+    """The loaded HIP library (raises if it is not built)."""
+    return _lib.lib()
+
+
+def reserve_weight_buffer(device, numel):
+    """Grow the shared reconstruction buffer (used by the `recon` prefill route) at load time,
+    so graph capture never allocates it (reference ops.py:52-57)."""
+    device = torch.device(device)
+    buf = _wbuf.get(device)
+    if buf is None or buf.numel() < numel:
+        _wbuf[device] = torch.empty(numel, dtype=torch.float16, device=device)
+
+
+def _weight_buffer(device, numel):
+    reserve_weight_buffer(device, numel)
+    return _wbuf[torch.device(device)][:numel]
+
+
+def reserve_workspace(device, k: int, n: int, K: int, groups: int = 1, m: int = MR_MAX):
+    """Reserve the GEMV workspace of the current stream for up to m rows (load time)."""
+    if m < 1:
+        return
+    E.workspace(torch.device(device), E.gemv_workspace_bytes(min(m, _lib.GEMV_MAX_ROWS), k, n, K, groups))
+
+
+def _prep(x: torch.Tensor):
+    k = x.shape[-1]
+    x2 = x.reshape(-1, k)
+    if x2.dtype != torch.float16:
+        x2 = x2.to(torch.float16)
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    return x2, k
+
+
+def _linear_into(x2, trellis, suh, svh, K, mcg, mul1, y):
+    """One group into y ([M, n] view, unit column stride, any row stride)."""
+    M, k = x2.shape
+    n = svh.shape[0]
+    if M <= MR_MAX:
+        rc = E.exl3_gemv_mr(x2, trellis, y, suh, None, svh, K, mcg, mul1)
+        if rc != 0:
+            raise RuntimeError(f"exl3rocm: GEMV declined shape m={M} k={k} n={n} K={K}")
+    elif PREFILL_ROUTE == "recon":
+        xh = torch.empty_like(x2)
+        E.had_r_128(x2, xh, suh, None, 1.0)
+        for n0 in range(0, n, RECON_SLICE_N):
+            n1 = min(n0 + RECON_SLICE_N, n)
+            w = _weight_buffer(x2.device, k * (n1 - n0)).view(k, n1 - n0)
+            if n0 == 0 and n1 == n:
+                E.reconstruct(w, trellis, K, mcg, mul1)
+            else:
+                E.reconstruct_slice(w, trellis, K, mcg, mul1, n0)
+            E.hgemm_recon(xh, w, y[:, n0:n1])
+        E.had_r_128(y, y, None, svh, 1.0)
+    else:
+        xh = torch.empty_like(x2)
+        E.exl3_gemm_trellis(x2, trellis, y, suh, xh, svh, K, mcg, mul1)
+
+
+@torch.library.custom_op("exl3rocm::linear", mutates_args=())
+def exl3_linear(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+                K: int, mcg: bool, mul1: bool) -> torch.Tensor:
+    x2, k = _prep(x)
+    n = svh.shape[0]
+    M = x2.shape[0]
+    y = torch.empty((M, n), dtype=torch.float16, device=x.device)
+    if M == 0 or _DEBUG_SKIP:
+        return y.zero_().view(*x.shape[:-1], n) if _DEBUG_SKIP else y.view(*x.shape[:-1], n)
+    _linear_into(x2, trellis, suh, svh, K, mcg, mul1, y)
+    return y.view(*x.shape[:-1], n)
+
+
+@exl3_linear.register_fake
+def _(x, trellis, suh, svh, K, mcg, mul1):
+    return x.new_empty((*x.shape[:-1], svh.shape[0]), dtype=torch.float16)
+
+
+@torch.library.custom_op("exl3rocm::linear_groups", mutates_args=())
+def exl3_linear_groups(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch.Tensor],
+                       svh: list[torch.Tensor], K: list[int], mcg: bool, mul1: bool,
+                       ptrs_trellis: Optional[torch.Tensor] = None, ptrs_suh: Optional[torch.Tensor] = None,
+                       ptrs_svh: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """A fused module made of several checkpoint tensors (e.g. gate_proj + up_proj), each with its
+    own K / suh / svh; the concatenation happens inside this opaque op (reference ops.py:106-175).
+
+    ptrs_* = int64 device tensors of per-group data pointers, given when all groups share K and
+    width: at M == 1 one grouped launch over the pointer tables computes every group."""
+    widths = [s.shape[0] for s in svh]
+    if _DEBUG_SKIP:
+        return torch.zeros((*x.shape[:-1], sum(widths)), dtype=torch.float16, device=x.device)
+    if len(trellis) == 1:
+        return exl3_linear(x, trellis[0], suh[0], svh[0], K[0], mcg, mul1)
+    x2, k = _prep(x)
+    M = x2.shape[0]
+    ng = len(trellis)
+    if M == 1 and ptrs_trellis is not None and ng <= _lib.MAX_GROUPS:
+        y = torch.empty((ng, 1, widths[0]), dtype=torch.float16, device=x.device)
+        E.exl3_mgemm(x2.view(1, 1, k), ptrs_trellis, y, ptrs_suh, None, ptrs_svh, K[0], mcg, mul1)
+        return y.view(*x.shape[:-1], ng * widths[0])
+    y = torch.empty((M, sum(widths)), dtype=torch.float16, device=x.device)
+    if M == 0:
+        return y.view(*x.shape[:-1], 0 if not widths else sum(widths))
+    if M <= MR_MAX:
+        # runs of consecutive groups with equal (K, width) share one grouped launch (gate/up, k/v),
+        # each written straight into its row-strided column slice
+        i, n0 = 0, 0
+        while i < ng:
+            j = i + 1
+            while j < ng and j - i < _lib.MAX_GROUPS and K[j] == K[i] and widths[j] == widths[i]:
+                j += 1
+            if j - i > 1:
+                E.exl3_gemv_mr_grouped(x2, list(trellis[i:j]), y[:, n0:], list(suh[i:j]), None, list(svh[i:j]),
+                                       K[i], mcg, mul1, j - i)
+            else:
+                _linear_into(x2, trellis[i], suh[i], svh[i], K[i], mcg, mul1, y[:, n0:n0 + widths[i]])
+            n0 += sum(widths[i:j])
+            i = j
+        return y.view(*x.shape[:-1], n0)
+    n0 = 0
+    for t, su, sv, kk, w in zip(trellis, suh, svh, K, widths):
+        _linear_into(x2, t, su, sv, kk, mcg, mul1, y[:, n0:n0 + w])
+        n0 += w
+    return y.view(*x.shape[:-1], n0)
+
+
+@exl3_linear_groups.register_fake
+def _(x, trellis, suh, svh, K, mcg, mul1, ptrs_trellis=None, ptrs_suh=None, ptrs_svh=None):
+    return x.new_empty((*x.shape[:-1], sum(s.shape[0] for s in svh)), dtype=torch.float16)

@@ -1,0 +1,96 @@
+"""CPU tests of the C-ABI library: it loads without a GPU, exports every symbol the header
+declares, and its host-only entry points (sizing, eligibility, argument validation that returns
+before any launch) behave as documented.  No kernel runs here."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from exl3rocm import _lib
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(REPO, "include", "exl3_mi355x.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:int|size_t)\s+(exl3_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_reference_entry_points():
+    names = declared_functions()
+    for want in ("exl3_decode", "exl3_reconstruct", "exl3_reconstruct_slice", "exl3_had_r_128", "exl3_gemv",
+                 "exl3_gemv_mr", "exl3_gemv_mr_grouped", "exl3_gemv_mr_supported", "exl3_mgemm",
+                 "exl3_hgemm_recon", "exl3_gemm"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert set(declared_functions()) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_loader_and_abi_version():
+    L = _lib.lib()
+    assert L.exl3_abi_version() == _lib.ABI_VERSION
+
+
+def test_split_choice_depends_only_on_shape():
+    L = _lib.lib()
+    assert L.exl3_gemv_splits(5120, 5120) == 20
+    assert L.exl3_gemv_splits(5120, 17408) == 4
+    assert L.exl3_gemv_splits(17408, 5120) == 17
+    assert L.exl3_gemv_splits(5120, 1024) == 40
+    for k, n in ((4096, 4096), (5120, 5120), (17408, 5120)):
+        s = L.exl3_gemv_splits(k, n)
+        assert (k // 128) % s == 0 and k // s <= 2048
+
+
+def test_workspace_sizes():
+    L = _lib.lib()
+    ws1 = L.exl3_gemv_workspace_size(1, 5120, 5120, 4, 1)
+    ws16 = L.exl3_gemv_workspace_size(16, 5120, 5120, 4, 1)
+    ws2g = L.exl3_gemv_workspace_size(1, 5120, 5120, 4, 2)
+    assert ws1 >= 40 * 20 * 128 * 4 and ws16 > ws1 and ws2g > ws1
+    assert L.exl3_gemv_workspace_size(33, 5120, 5120, 4, 1) == 0        # beyond the GEMV row limit
+    assert L.exl3_gemv_workspace_size(1, 5000, 5120, 4, 1) == 0         # k not a multiple of 128
+
+
+def test_mr_supported_predicate():
+    L = _lib.lib()
+    assert L.exl3_gemv_mr_supported(1, 5120, 5120, 4, 0, 1) == 1
+    assert L.exl3_gemv_mr_supported(32, 5120, 1024, 8, 1, 0) == 1
+    assert L.exl3_gemv_mr_supported(33, 5120, 1024, 8, 1, 0) == 0
+    assert L.exl3_gemv_mr_supported(4, 5120, 1000, 4, 0, 1) == 0
+    assert L.exl3_gemv_mr_supported(4, 5120, 1024, 9, 0, 1) == 0
+
+
+def test_invalid_arguments_return_before_any_launch():
+    L = _lib.lib()
+    dummy = ctypes.c_void_p(0x1000)
+    # bad shapes / null pointers are rejected with EINVAL, declines with DECLINED
+    assert L.exl3_reconstruct(dummy, dummy, 100, 128, 4, 0, 1, None) == _lib.EINVAL
+    assert L.exl3_reconstruct_slice(dummy, 128, dummy, 128, 128, 4, 0, 1, 8, 16, None) == _lib.EINVAL
+    assert L.exl3_had_r_128(dummy, 100, dummy, 100, 1, 100, None, None, 1.0, None) == _lib.EINVAL
+    assert L.exl3_decode(None, dummy, 16, 0, 1, None) == _lib.EINVAL
+    assert L.exl3_gemv(dummy, 128, dummy, dummy, 128, dummy, None, dummy, 2, 128, 128, 4, 0, 1, dummy, 1 << 20,
+                       None) == _lib.DECLINED
+    assert L.exl3_gemv_mr(dummy, 128, dummy, dummy, 128, dummy, None, dummy, 40, 128, 128, 4, 0, 1, dummy, 1 << 20,
+                          None) == _lib.DECLINED
+    assert L.exl3_gemv_mr(dummy, 128, dummy, dummy, 128, dummy, None, dummy, 1, 128, 128, 4, 0, 1, dummy, 0,
+                          None) == _lib.EWORKSPACE
+    assert L.exl3_hgemm_recon(dummy, 64, dummy, 100, dummy, 100, 4, 64, 100, None) == _lib.EINVAL
+    assert L.exl3_gemm_trellis(dummy, 128, dummy, dummy, 128, dummy, dummy, dummy, 64, 128, 128, 9, 0, 1,
+                               None) == _lib.EINVAL
+    assert L.exl3_mgemm(dummy, None, dummy, dummy, None, dummy, 2, 128, 128, 4, 0, 1, dummy, 1 << 20,
+                        None) == _lib.EINVAL
+
+
+def test_check_raises_on_errors():
+    with pytest.raises(_lib.Exl3Error):
+        _lib.check(_lib.EINVAL, "x")
+    assert _lib.check(_lib.DECLINED, "x") == _lib.DECLINED

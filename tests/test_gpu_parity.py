@@ -1,0 +1,327 @@
+"""GPU parity of the HIP kernels against the oracle restatement (run with -m gpu on an MI355X).
+
+Bars:
+  * decoded fp16 weights and codebook values: bit-exact;
+  * Hadamard stages: bit-exact (float64 butterflies on fp16 data are exact);
+  * linear outputs: rel-L2 <= 1e-3 against the oracle's faithful fp16 staging, plus the
+    reference's own gate family (tests/test_gpu_parity.py:41-70 of the reference);
+  * determinism: repeat / stream invariance, every row of an m-row call == its m == 1 call,
+    grouped == ungrouped, graph replay == eager.
+Expected values come from oracle/libexl3cpu.so (the C restatement pinned in test_oracle.py).
+"""
+import numpy as np
+import pytest
+import torch
+
+import cpu
+import exl3_oracle as O
+from exl3rocm import _lib, kernels as E, ops, synth  # noqa: F401
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU")]
+DEV = "cuda:0"
+REL_L2 = 1e-3
+
+
+def stats(got, ref):
+    got = np.asarray(got, dtype=np.float64).ravel()
+    ref = np.asarray(ref, dtype=np.float64).ravel()
+    diff = got - ref
+    scale = np.sqrt(np.mean(ref ** 2)) or 1.0
+    cos = float(got @ ref / ((np.linalg.norm(got) * np.linalg.norm(ref)) or 1.0))
+    bound = 4e-3 * scale + 2e-3 * np.abs(ref)
+    return {
+        "rel_l2": float(np.linalg.norm(diff) / (np.linalg.norm(ref) or 1.0)),
+        "normalized_max_abs_err": float(np.abs(diff).max() / scale),
+        "normalized_rms_err": float(np.sqrt(np.mean(diff ** 2)) / scale),
+        "cosine_similarity": cos,
+        "abs_rel_bound_ratio": float((np.abs(diff) / bound).max()),
+    }
+
+
+def assert_close(got, ref, what=""):
+    st = stats(got, ref)
+    assert st["rel_l2"] <= REL_L2, (what, st)
+    assert st["normalized_max_abs_err"] <= 3e-3, (what, st)
+    assert st["normalized_rms_err"] <= 2e-4, (what, st)
+    assert st["cosine_similarity"] >= 0.999999, (what, st)
+    assert st["abs_rel_bound_ratio"] <= 1.0, (what, st)
+    return st
+
+
+def layer(k, n, bits, tag="parity", heavy=False, m=1):
+    tr, su, sv = synth.layer(tag, f"{k}x{n}x{bits}", k, n, bits)
+    x = synth.activations(synth.key_of(tag, f"{k}x{n}x{bits}", "x", m), m, k, heavy_tail=heavy)
+    return x, tr, su, sv
+
+
+def to_dev(*arrs):
+    out = []
+    for a in arrs:
+        t = torch.from_numpy(np.ascontiguousarray(a))
+        if t.dtype == torch.uint16:
+            t = t.view(torch.int16)
+        out.append(t.to(DEV))
+    return out
+
+
+def gpu_linear(x, tr, su, sv, bits, cb):
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    y = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, cb == 1, cb == 2)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+# ---------------------------------------------------------------------------------- decode
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_decode_full_table_bitexact(cb):
+    codes = torch.arange(65536, dtype=torch.int32).to(torch.int16).to(DEV)
+    out = torch.empty(65536, dtype=torch.float32, device=DEV)
+    E.decode(codes, out, cb == 1, cb == 2)
+    want = O.codebook_f16(np.arange(65536), cb).astype(np.float32)
+    np.testing.assert_array_equal(out.cpu().numpy(), want)
+
+
+# ---------------------------------------------------------------------------------- reconstruct
+@pytest.mark.parametrize("bits", range(1, 9))
+@pytest.mark.parametrize("cb", [0, 1, 2])
+def test_reconstruct_bitexact(bits, cb):
+    tr = synth.trellis(synth.key_of("rec", bits, cb), 256, 640, bits)
+    T = to_dev(tr.view(np.int16))[0]
+    W = torch.empty(256, 640, dtype=torch.float16, device=DEV)
+    E.reconstruct(W, T, bits, cb == 1, cb == 2)
+    np.testing.assert_array_equal(W.cpu().numpy().view(np.uint16), cpu.reconstruct(tr, bits, cb).view(np.uint16))
+
+
+def test_reconstruct_slice_bitexact():
+    tr = synth.trellis(synth.key_of("slice"), 128, 1024, 3)
+    T = to_dev(tr.view(np.int16))[0]
+    full = cpu.reconstruct(tr, 3, 2)
+    for n0, w in ((0, 512), (384, 640), (1008, 16)):
+        buf = torch.full((128, w + 8), float("nan"), dtype=torch.float16, device=DEV)
+        E.reconstruct_slice(buf[:, :w], T, 3, False, True, n0)
+        got = buf.cpu().numpy()
+        np.testing.assert_array_equal(got[:, :w].view(np.uint16), full[:, n0:n0 + w].view(np.uint16))
+        assert np.isnan(got[:, w:]).all()           # nothing written past the slice
+
+
+@pytest.mark.parametrize("k,n,bits,cb", [(5120, 17408, 4, 2), (17408, 5120, 3, 2), (4096, 4096, 4, 1)])
+def test_reconstruct_full_size_bitexact(k, n, bits, cb):
+    tr = synth.trellis(synth.key_of("full", k, n, bits), k, n, bits)
+    T = to_dev(tr.view(np.int16))[0]
+    W = torch.empty(k, n, dtype=torch.float16, device=DEV)
+    E.reconstruct(W, T, bits, cb == 1, cb == 2)
+    np.testing.assert_array_equal(W.cpu().numpy().view(np.uint16), cpu.reconstruct(tr, bits, cb).view(np.uint16))
+
+
+# ---------------------------------------------------------------------------------- Hadamard
+def test_had_r_128_bitexact():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((5, 640)) * 2).astype(np.float16)
+    su = synth.scales(1, 640)
+    X, SU = to_dev(x, su)
+    out = torch.empty_like(X)
+    E.had_r_128(X, out, SU, None, 1.0)
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16), cpu.had_in(x, su).view(np.uint16))
+    E.had_r_128(X, X, None, SU, 1.0)                  # in place, post-scale
+    np.testing.assert_array_equal(X.cpu().numpy().view(np.uint16), cpu.had_out(x, su).view(np.uint16))
+    Y = to_dev(x)[0]
+    E.had_r_128(Y, Y, None, None, 2.0)
+    np.testing.assert_array_equal(Y.cpu().numpy().view(np.uint16),
+                                  O.to_f16(O.had128(x.astype(np.float64), O.R_SCALE * 2.0)).astype(np.float16)
+                                  .view(np.uint16))
+
+
+# ---------------------------------------------------------------------------------- GEMV
+GEMV_CASES = [
+    (256, 128, 3, 2), (512, 256, 3, 2), (1024, 512, 3, 2), (4096, 4096, 4, 1),
+    (5120, 5120, 2, 2), (5120, 5120, 4, 2), (5120, 1024, 4, 2), (5120, 17408, 3, 2), (17408, 5120, 3, 2),
+    (5120, 1024, 5, 2), (5120, 1024, 6, 2), (5120, 1024, 8, 2), (1024, 768, 7, 0), (1024, 512, 1, 1),
+    (5120, 5120, 4, 0), (5120, 5120, 4, 1),
+]
+
+
+@pytest.mark.parametrize("k,n,bits,cb", GEMV_CASES)
+def test_gemv_parity(k, n, bits, cb):
+    x, tr, su, sv = layer(k, n, bits)
+    got = gpu_linear(x, tr, su, sv, bits, cb)
+    ref = cpu.linear(x, tr, bits, su, sv, cb)
+    assert_close(got, ref, (k, n, bits, cb))
+
+
+def test_gemv_heavy_tail_parity():
+    for k, n in ((5120, 17408), (17408, 5120)):
+        x, tr, su, sv = layer(k, n, 4, heavy=True, m=4)
+        assert_close(gpu_linear(x, tr, su, sv, 4, 2), cpu.linear(x, tr, 4, su, sv, 2), (k, n))
+
+
+@pytest.mark.parametrize("k,n,bits", [(5120, 5120, 4), (17408, 5120, 3), (5120, 1024, 5)])
+def test_rows_bitwise_equal_to_m1(k, n, bits):
+    x, tr, su, sv = layer(k, n, bits, m=32)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    rows1 = torch.cat([torch.ops.exl3rocm.linear(X[r:r + 1], T, SU, SV, bits, False, True) for r in range(32)])
+    for m in (2, 3, 4, 8, 12, 16, 17, 24, 32):
+        ym = torch.ops.exl3rocm.linear(X[:m], T, SU, SV, bits, False, True)
+        assert torch.equal(ym.view(torch.int16), rows1[:m].view(torch.int16)), m
+    torch.cuda.synchronize()
+    assert_close(rows1.cpu().numpy(), cpu.linear(x, tr, bits, su, sv, 2), (k, n, bits))
+
+
+def test_grouped_equals_single_and_mgemm():
+    k, n, bits = 5120, 4096, 3
+    mats = [synth.layer("grp", i, k, n, bits) for i in range(2)]
+    x = synth.activations(synth.key_of("grp", "x"), 8, k)
+    X = to_dev(x)[0]
+    Ts = [to_dev(m[0].view(np.int16))[0] for m in mats]
+    SUs = [to_dev(m[1])[0] for m in mats]
+    SVs = [to_dev(m[2])[0] for m in mats]
+    for m in (1, 4, 8):
+        y = torch.empty(m, 2 * n, dtype=torch.float16, device=DEV)
+        E.exl3_gemv_mr_grouped(X[:m], Ts, y, SUs, None, SVs, bits, False, True, 2)
+        ref = torch.empty_like(y)
+        for i in range(2):
+            E.exl3_gemv_mr(X[:m], Ts[i], ref[:, i * n:(i + 1) * n], SUs[i], None, SVs[i], bits, False, True)
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16)), m
+    ptr = [torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=DEV) for ts in (Ts, SUs, SVs)]
+    y1 = torch.empty(2, 1, n, dtype=torch.float16, device=DEV)
+    E.exl3_mgemm(X[:1].contiguous(), ptr[0], y1, ptr[1], None, ptr[2], bits, False, True)
+    yg = torch.ops.exl3rocm.linear_groups(X[:1], Ts, SUs, SVs, [bits, bits], False, True)
+    assert torch.equal(y1.view(1, -1).view(torch.int16), yg.view(torch.int16))
+    torch.cuda.synchronize()
+    ref0 = cpu.linear(x[:1], mats[0][0], bits, mats[0][1], mats[0][2], 2)
+    assert_close(y1[0].cpu().numpy(), ref0)
+
+
+def test_linear_groups_mixed_bits_rows_equal():
+    """Fused mixed-bit module (q=2 / k,v=5 style): M=4 == four M=1 calls, bitwise."""
+    k = 5120
+    spec = [(2048, 2), (1024, 5), (1024, 5)]
+    mats = [synth.layer("mix", i, k, n, K) for i, (n, K) in enumerate(spec)]
+    Ts = [to_dev(m[0].view(np.int16))[0] for m in mats]
+    SUs = [to_dev(m[1])[0] for m in mats]
+    SVs = [to_dev(m[2])[0] for m in mats]
+    Ks = [K for _, K in spec]
+    X = to_dev(synth.activations(synth.key_of("mix", "x"), 4, k))[0]
+    y4 = torch.ops.exl3rocm.linear_groups(X, Ts, SUs, SVs, Ks, False, True)
+    y1 = torch.cat([torch.ops.exl3rocm.linear_groups(X[r:r + 1], Ts, SUs, SVs, Ks, False, True) for r in range(4)])
+    assert torch.equal(y4.view(torch.int16), y1.view(torch.int16))
+
+
+def test_determinism_repeat_and_streams():
+    x, tr, su, sv = layer(5120, 5120, 4)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    ref = torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True)
+    for _ in range(3):
+        assert torch.equal(torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True).view(torch.int16),
+                           ref.view(torch.int16))
+    for _ in range(2):
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            y = torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True)
+        s.synchronize()
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+
+
+def test_zero_input():
+    _, tr, su, sv = layer(5120, 1024, 4)
+    X, T, SU, SV = to_dev(np.zeros((1, 5120), np.float16), tr.view(np.int16), su, sv)
+    y = torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True)
+    assert torch.isfinite(y).all() and y.abs().max().item() == 0.0
+
+
+def test_ineligible_declines_without_modifying_outputs():
+    x, tr, su, sv = layer(256, 128, 3, m=2)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    C = torch.full((2, 128), float("nan"), dtype=torch.float16, device=DEV)
+    assert E.exl3_gemv(X, T, C, SU, None, SV, False, True) == _lib.DECLINED     # m = 2 is not the M=1 entry
+    torch.cuda.synchronize()
+    assert torch.isnan(C).all()
+    C2 = torch.full((1, 128), float("nan"), dtype=torch.float16, device=DEV)
+    with pytest.raises(RuntimeError):                # odd output stride: invalid, nothing launched
+        E.exl3_gemv_mr(X[:1], T, torch.empty(3, 129, dtype=torch.float16, device=DEV)[:, 1:], SU, None, SV, 3,
+                       False, True)
+    assert torch.isnan(C2).all()
+
+
+def test_graph_capture_replays_match_eager():
+    x, tr, su, sv = layer(5120, 5120, 4, m=4)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    eager1 = torch.ops.exl3rocm.linear(X[:1], T, SU, SV, 4, False, True)
+    eager4 = torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.reserve_workspace(DEV, 5120, 5120, 4)       # the capture stream's own workspace
+        torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        y1 = torch.ops.exl3rocm.linear(X[:1], T, SU, SV, 4, False, True)
+        y4 = torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True)
+    for _ in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y1.view(torch.int16), eager1.view(torch.int16))
+        assert torch.equal(y4.view(torch.int16), eager4.view(torch.int16))
+        torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True)     # eager work between replays
+        torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------------------------- prefill GEMM
+@pytest.mark.parametrize("m,k,n,bits,cb", [(33, 256, 128, 3, 2), (64, 512, 256, 4, 2), (300, 1024, 384, 2, 1),
+                                           (256, 5120, 1024, 4, 2), (130, 512, 640, 5, 0)])
+def test_prefill_gemm_parity(m, k, n, bits, cb):
+    x, tr, su, sv = layer(k, n, bits, m=m)
+    assert_close(gpu_linear(x, tr, su, sv, bits, cb), cpu.linear(x, tr, bits, su, sv, cb), (m, k, n, bits))
+
+
+def test_hgemm_recon_vs_fp32():
+    g = torch.Generator(device=DEV).manual_seed(4)
+    x = torch.randn(200, 1024, device=DEV, generator=g).half()
+    W = (torch.randn(1024, 384, device=DEV, generator=g) * 0.5).half()
+    y = torch.empty(200, 384, dtype=torch.float16, device=DEV)
+    E.hgemm_recon(x, W, y)
+    ref = (x.float() @ W.float()).half().float()
+    err = ((y.float() - ref).norm() / ref.norm()).item()
+    assert err < 1e-3, err
+
+
+def test_recon_route_matches_fused_route():
+    x, tr, su, sv = layer(1024, 512, 4, m=96)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    fused = torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True)
+    xh = torch.empty_like(X)
+    E.had_r_128(X, xh, SU, None, 1.0)
+    W = torch.empty(1024, 512, dtype=torch.float16, device=DEV)
+    E.reconstruct(W, T, 4, False, True)
+    y = torch.empty_like(fused)
+    E.hgemm_recon(xh, W, y)
+    E.had_r_128(y, y, None, SV, 1.0)
+    assert torch.equal(y.view(torch.int16), fused.view(torch.int16))
+
+
+# ---------------------------------------------------------------------------------- plugin surface
+def test_linear_method_end_to_end():
+    from exl3rocm import plugin
+    groups = [("gate", 4, 1024, 1536), ("up", 4, 1024, 1536)]
+    method = plugin.Exl3LinearMethod(plugin.Exl3Config("mul1"), groups)
+    lay = torch.nn.Module()
+    method.create_weights(lay, 1024, [1536, 1536], 1024, 3072, torch.float16)
+    lay.to(DEV)
+    mats = [synth.layer("plug", i, 1024, 1536, 4) for i in range(2)]
+    for i, (tr, su, sv) in enumerate(mats):
+        lay.trellis.weight_loader(lay.trellis, torch.from_numpy(tr.view(np.int16)), i)
+        lay.suh.weight_loader(lay.suh, torch.from_numpy(su), i)
+        lay.svh.weight_loader(lay.svh, torch.from_numpy(sv), i)
+        lay.mul1.weight_loader(lay.mul1, torch.tensor(0x83DCD12D), i)
+    method.process_weights_after_loading(lay)
+    assert lay.exl3_mgemm_ptrs is not None
+    x = synth.activations(synth.key_of("plug", "x"), 3, 1024)
+    X = to_dev(x)[0]
+    y3 = method.apply(lay, X)
+    y1 = method.apply(lay, X[:1])
+    assert torch.equal(y3[:1].view(torch.int16), y1.view(torch.int16))
+    ref = np.concatenate([cpu.linear(x, tr, 4, su, sv, 2) for tr, su, sv in mats], axis=1)
+    assert_close(y3.cpu().numpy(), ref)
+    yb = method.apply(lay, X.float(), bias=torch.ones(3072, device=DEV))
+    assert yb.dtype == torch.float32

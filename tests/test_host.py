@@ -1,0 +1,171 @@
+"""CPU tests of the host-side surface: checkpoint layout discovery, the linear-method weight
+loading contract, and the custom ops' fake (meta) implementations."""
+import json
+import os
+import struct
+
+import numpy as np
+import pytest
+import torch
+
+from exl3rocm import layout, plugin
+from exl3rocm import ops  # noqa: F401  (registers torch.ops.exl3rocm.*)
+
+
+def write_safetensors_header(path, tensors: dict):
+    """A header-only safetensors file (the layout reader never touches tensor data)."""
+    header, off = {}, 0
+    for name, (dtype, shape) in tensors.items():
+        nbytes = int(np.prod(shape)) * {"I16": 2, "F16": 2, "I32": 4, "F8_E4M3": 1}[dtype]
+        header[name] = {"dtype": dtype, "shape": list(shape), "data_offsets": [off, off + nbytes]}
+        off += nbytes
+    blob = json.dumps(header).encode()
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(blob)))
+        f.write(blob)
+
+
+@pytest.fixture
+def checkpoint(tmp_path):
+    pre = "model.language_model.layers.0"
+    t = {
+        f"{pre}.mlp.gate_proj.trellis": ("I16", (320, 1088, 64)),
+        f"{pre}.mlp.up_proj.trellis": ("I16", (320, 1088, 64)),
+        f"{pre}.mlp.down_proj.trellis": ("I16", (1088, 320, 48)),
+        f"{pre}.self_attn.q_proj.trellis": ("I16", (320, 320, 32)),
+        f"{pre}.self_attn.k_proj.trellis": ("I16", (320, 64, 80)),
+        f"{pre}.self_attn.v_proj.trellis": ("I16", (320, 64, 80)),
+        f"{pre}.mlp.gate_proj.suh": ("F16", (5120,)),
+        "model.language_model.embed_tokens.weight": ("F8_E4M3", (1000, 5120)),
+        "lm_head.trellis": ("I16", (320, 100, 64)),
+    }
+    write_safetensors_header(str(tmp_path / "model-00001.safetensors"), t)
+    return str(tmp_path)
+
+
+def test_norm_key():
+    assert layout.norm_key("model.language_model.layers.3.mlp.gate_proj") == "layers.3.mlp.gate_proj"
+    assert layout.norm_key("language_model.model.layers.3.mlp.gate_proj") == "layers.3.mlp.gate_proj"
+    assert layout.norm_key("model.mtp.layers.0.x") == "mtp.layers.0.x"
+    assert layout.norm_key("model.visual.blocks.0.mlp.linear_fc1") == "visual.blocks.0.mlp.linear_fc1"
+    assert layout.norm_key("lm_head") == "lm_head"
+
+
+def test_checkpoint_layout(checkpoint):
+    mods, dtypes, shapes = layout.read_checkpoint_layout(checkpoint)
+    assert mods["layers.0.mlp.gate_proj"] == (4, 5120, 17408)
+    assert mods["layers.0.mlp.down_proj"] == (3, 17408, 5120)
+    assert mods["layers.0.self_attn.k_proj"] == (5, 5120, 1024)
+    assert mods["lm_head"] == (4, 5120, 1600)
+    assert dtypes["model.language_model.embed_tokens.weight"] == "F8_E4M3"
+    assert shapes["model.language_model.layers.0.mlp.gate_proj.suh"] == (5120,)
+
+
+def test_groups_for_fused_modules(checkpoint):
+    mods, _, _ = layout.read_checkpoint_layout(checkpoint)
+    g = layout.groups_for(mods, "model.layers.0.mlp.gate_up_proj")
+    assert [m for m, *_ in g] == ["layers.0.mlp.gate_proj", "layers.0.mlp.up_proj"]
+    qkv = layout.groups_for(mods, "model.layers.0.self_attn.qkv_proj")
+    assert [x[1] for x in qkv] == [2, 5, 5]
+    assert layout.groups_for(mods, "model.layers.0.self_attn.o_proj") is None
+    with pytest.raises(AssertionError):
+        layout.groups_for({"layers.0.mlp.gate_proj": (4, 128, 128)}, "model.layers.0.mlp.gate_up_proj")
+
+
+def test_config_surface(checkpoint):
+    cfg = plugin.Exl3Config.from_config({"codebook": "mcg"})
+    assert cfg.get_name() == "exl3" and cfg.codebook == "mcg"
+    assert cfg.get_supported_act_dtypes() == [torch.float16]
+    cfg.maybe_update_config(checkpoint)
+    assert len(cfg.modules) == 7
+    with pytest.raises(NotImplementedError):
+        cfg.maybe_update_config(os.path.join(checkpoint, "missing"))
+    layer = plugin.LinearBase()
+    m = cfg.get_quant_method(layer, "model.layers.0.mlp.gate_up_proj")
+    assert isinstance(m, plugin.Exl3LinearMethod) and len(m.groups) == 2
+    assert isinstance(cfg.get_quant_method(layer, "model.layers.0.self_attn.o_proj"), plugin.UnquantizedLinearMethod)
+
+
+def make_layer(groups, codebook="mul1"):
+    cfg = plugin.Exl3Config(codebook)
+    method = plugin.Exl3LinearMethod(cfg, groups)
+    layer = torch.nn.Module()
+    k = groups[0][2]
+    method.create_weights(layer, k, [g[3] for g in groups], k, sum(g[3] for g in groups), torch.float16)
+    return method, layer
+
+
+def test_create_weights_and_loading():
+    groups = [("q", 2, 256, 256), ("k", 5, 256, 128), ("v", 5, 256, 128)]
+    method, layer = make_layer(groups)
+    assert layer.exl3_K == [2, 5, 5] and layer.exl3_n == [256, 128, 128]
+    assert tuple(layer.exl3_trellis_1.shape) == (16, 8, 80) and layer.exl3_trellis_1.dtype == torch.int16
+    assert "exl3_trellis_0" not in layer.state_dict()            # non-persistent buffers
+    for name in ("trellis", "suh", "svh", "mul1"):
+        assert layer._parameters[name].numel() == 0
+    rng = np.random.default_rng(0)
+    for sid, (_, K, k, n) in zip("qkv", groups):
+        tr = torch.from_numpy(rng.integers(-32768, 32767, (k // 16, n // 16, 16 * K), dtype=np.int16))
+        layer.trellis.weight_loader(layer.trellis, tr, sid)
+        layer.suh.weight_loader(layer.suh, torch.ones(k, dtype=torch.float16), sid)
+        layer.svh.weight_loader(layer.svh, torch.ones(n, dtype=torch.float16), sid)
+        layer.mul1.weight_loader(layer.mul1, torch.tensor(0x83DCD12D - (1 << 32), dtype=torch.int64), sid)
+    assert torch.equal(layer.exl3_trellis_2, tr)
+    with pytest.raises(AssertionError):
+        layer.trellis.weight_loader(layer.trellis, torch.zeros(1, dtype=torch.int16), "q")
+    with pytest.raises(AssertionError):
+        layer.mul1.weight_loader(layer.mul1, torch.tensor(7), "k")             # differs across groups
+    method.process_weights_after_loading(layer)
+    assert layer.exl3_is_mul1 and not layer.exl3_is_mcg
+    assert "trellis" not in layer._parameters and "mul1" not in layer._parameters
+    assert layer.exl3_mgemm_ptrs is None                                   # groups differ in K / width
+
+
+def test_partition_mapping_and_errors():
+    # one group spanning two output partitions (in_proj_qkv covers q, k, v of in_proj_qkvz)
+    method, layer = make_layer([("qkv", 4, 128, 384), ("z", 4, 128, 128)])
+    assert layer.exl3_part_to_group == [0, 1]
+    cfg = plugin.Exl3Config()
+    m = plugin.Exl3LinearMethod(cfg, [("a", 4, 128, 256)])
+    l2 = torch.nn.Module()
+    m.create_weights(l2, 128, [128, 128], 128, 256, torch.float16)
+    assert l2.exl3_part_to_group == [0, 0]
+    with pytest.raises(NotImplementedError):
+        m.create_weights(torch.nn.Module(), 64, [256], 128, 256, torch.float16)   # tensor parallel
+    with pytest.raises(AssertionError):
+        m.create_weights(torch.nn.Module(), 128, [200], 128, 200, torch.float16)  # does not tile
+    with pytest.raises(AssertionError):
+        plugin.Exl3LinearMethod._group_of(l2, (0, 1)) if len(set(l2.exl3_part_to_group)) > 1 else \
+            plugin.Exl3LinearMethod._group_of(layer, (0, 1))
+
+
+def test_missing_tensor_is_reported():
+    method, layer = make_layer([("a", 4, 128, 128)])
+    layer.trellis.weight_loader(layer.trellis, torch.zeros(8, 8, 64, dtype=torch.int16))
+    with pytest.raises(AssertionError, match="missing"):
+        method.process_weights_after_loading(layer)
+
+
+def test_codebook_scalar_check():
+    assert plugin.check_codebook_scalar("mul1", 0x83DCD12D)
+    assert plugin.check_codebook_scalar("mul1", 0x83DCD12D - (1 << 32))
+    assert not plugin.check_codebook_scalar("mcg", 0x83DCD12D)
+
+
+def test_fake_impls_shapes():
+    x = torch.empty(2, 3, 256, device="meta", dtype=torch.float16)
+    tr = torch.empty(16, 8, 64, device="meta", dtype=torch.int16)
+    su = torch.empty(256, device="meta", dtype=torch.float16)
+    sv = torch.empty(128, device="meta", dtype=torch.float16)
+    y = torch.ops.exl3rocm.linear(x, tr, su, sv, 4, False, True)
+    assert y.shape == (2, 3, 128) and y.dtype == torch.float16
+    yg = torch.ops.exl3rocm.linear_groups(x, [tr, tr], [su, su], [sv, sv], [4, 4], False, True)
+    assert yg.shape == (2, 3, 256)
+
+
+def test_cpu_tensors_fail_loudly():
+    x = torch.zeros(1, 128, dtype=torch.float16)
+    tr = torch.zeros(8, 8, 64, dtype=torch.int16)
+    s = torch.ones(128, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="GPU"):
+        torch.ops.exl3rocm.linear(x, tr, s, s, 4, False, True)
