@@ -20,8 +20,9 @@
  *   - All buffers are caller-owned.  Nothing here allocates device memory.  Launches are
  *     asynchronous on `stream`; no call synchronizes or reads back.  Calls are graph-capturable.
  *   - The GEMV entry points need a caller workspace of exl3_gemv_workspace_size() bytes whose
- *     first bytes (completion counters) are zero before the first call; every call leaves them
- *     zero again.  Calls that overlap on one workspace race: give concurrent streams their own.
+ *     first EXL3_GEMV_COUNTER_BYTES (completion counters) are zero before the first call; every
+ *     call leaves them zero again.  One workspace may serve calls of any shape in stream order;
+ *     calls that overlap on one workspace race: give concurrent streams their own.
  *   - Results are deterministic: repeat calls and different streams give bitwise-equal output,
  *     and each row of an m-row call equals the m == 1 call of that row.
  */
@@ -38,6 +39,7 @@ extern "C" {
 #define EXL3_ABI_VERSION 1
 #define EXL3_MAX_GROUPS 4       /* groups per grouped launch (reference EXL3_GEMV_MRG_MAX) */
 #define EXL3_GEMV_MAX_ROWS 32   /* rows handled by the fused GEMV */
+#define EXL3_GEMV_COUNTER_BYTES 65536  /* workspace head reserved for completion counters */
 
 #define EXL3_OK 0
 #define EXL3_DECLINED 1

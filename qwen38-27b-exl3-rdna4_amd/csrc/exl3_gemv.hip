@@ -365,14 +365,16 @@ int launch_gemv(const GemvArgs& a, int bits, int cb, int groups, hipStream_t s)
     }
 }
 
-size_t align256(size_t v) { return (v + 255) & ~(size_t) 255; }
+// workspace layout: [counters: fixed EXL3_GEMV_COUNTER_BYTES region][partials: groups*NB*S*M*128 f32].
+// The counter region has a fixed size so calls of different shapes sharing one workspace never
+// see another shape's partial sums where their counters live.
+constexpr size_t COUNTER_BYTES = EXL3_GEMV_COUNTER_BYTES;
 
-// workspace layout: [counters: groups*NB u32, 256-aligned][partials: groups*NB*S*M*128 f32]
 size_t gemv_ws_bytes(int m, int k, int n, int groups)
 {
     const int S = choose_splits(k, n), NB = n / 128;
-    if (S == 1) return align256((size_t) groups * NB * 4);
-    return align256((size_t) groups * NB * 4) + (size_t) groups * NB * S * m * 128 * 4;
+    if (S == 1) return COUNTER_BYTES;
+    return COUNTER_BYTES + (size_t) groups * NB * S * m * 128 * 4;
 }
 
 bool shape_ok(int m, int k, int n, int K)
@@ -413,8 +415,9 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, int groups, con
     a.S = choose_splits(k, n);
     a.ldy = ldy;
     const int NB = n / 128;
+    if ((size_t) groups * NB * 4 > COUNTER_BYTES) return EXL3_DECLINED;
     a.counters = (uint32_t*) ws;
-    a.part = (float*) ((char*) ws + align256((size_t) groups * NB * 4));
+    a.part = (float*) ((char*) ws + COUNTER_BYTES);
     a.xcd_remap = (NB * a.S) % 8 == 0 && NB % 8 == 0;
     return launch_gemv(a, K, codebook_of(mcg, mul1), groups, (hipStream_t) stream);
 }
