@@ -11,8 +11,8 @@
  * Conventions
  *   - fp16 tensors are IEEE binary16; the trellis is the checkpoint's (k/16, n/16, 16*K) int16
  *     tensor, read as little-endian 16-bit words; suh [k], svh [n] are fp16.
- *   - Alignment: trellis 16 bytes; x, y, suh, svh 4 bytes with even row strides (fp16 pairs
- *     move as 32-bit words); violations return EXL3_EINVAL before any launch.
+ *   - Alignment: trellis, x, y, suh, svh 16 bytes, row strides multiples of 8 elements (fp16
+ *     moves in 16-byte groups of 8); violations return EXL3_EINVAL before any launch.
  *   - Codebook flags: mul1 != 0 -> mul1 (cb 2), else mcg != 0 -> mcg (cb 1), else 3inst (cb 0).
  *   - K is the bitrate (bits per weight, 1..8).
  *   - Return status: 0 done; > 0 declined (ineligible but valid call, outputs untouched);
@@ -69,8 +69,9 @@ int exl3_reconstruct_slice(void* W, int64_t ldw, const void* trellis, int k, int
 int exl3_had_r_128(const void* in, int64_t ld_in, void* out, int64_t ld_out, int rows, int cols, const void* pre,
                    const void* post, float scale, void* stream);
 
-/* Split count the fused GEMV uses for a (k, n) layer (diagnostic). */
-int exl3_gemv_splits(int k, int n);
+/* Workgroups per group of the fused GEMV's stream-K grid for a (k, n) layer launched with
+ * `groups` groups (diagnostic; a function of the shape only, never of m). */
+int exl3_gemv_grid(int k, int n, int groups);
 
 /* Workspace bytes the fused GEMV needs for m rows and `groups` groups.
  * Has no reference counterpart: the reference fork allocates its counters inside the extension

@@ -30,6 +30,22 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr double R_SCALE = 0.088388347648;   // the Hadamard scale of every reference call site
 
+// Global-address-space views.  Pointers read from structs or pointer tables are generic, and
+// loads through generic pointers compile to flat_load, which also counts against lgkmcnt: every
+// LDS wait would then wait for in-flight HBM loads too.  Hot-path loads go through these.
+typedef __attribute__((address_space(1))) const uint32_t gc_u32;
+typedef __attribute__((address_space(1))) const uint16_t gc_u16;
+typedef __attribute__((address_space(1))) uint16_t g_u16;
+typedef __attribute__((address_space(1))) const u32x4 gc_u32x4;
+typedef __attribute__((address_space(1))) u32x4 g_u32x4;
+typedef __attribute__((address_space(1))) const u32x2 gc_u32x2;
+
+template <class T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* as_global(T* p)
+{
+    return (__attribute__((address_space(1))) T*) p;
+}
+
 // ------------------------------------------------------------------------------------------
 // float64 -> fp16 bits, round to nearest even (exact single rounding; used by the Hadamards,
 // whose float64 butterflies are exact on fp16 data, so the result equals the oracle's).
@@ -57,48 +73,93 @@ __device__ __forceinline__ f16 bits_f16(uint32_t b) { return __builtin_bit_cast(
 __device__ __forceinline__ uint32_t f16_bits(f16 h) { return (uint32_t) __builtin_bit_cast(uint16_t, h); }
 
 // ------------------------------------------------------------------------------------------
-// Wave64 Hadamard on 128 values: lane L holds elements 2L (v0) and 2L+1 (v1).  Natural-order
-// Sylvester H[i,j] = (-1)^popcount(i&j): stage bit 0 is in-lane, bits 1..6 are lane xor 1..32.
+// float64 -> fp16 through a round-to-odd float32 (two instructions plus a fix-up instead of the
+// integer path above): rounding to odd at 24 bits, then to nearest-even at 11 bits, equals a
+// single nearest-even rounding of the float64 value.
 // ------------------------------------------------------------------------------------------
-__device__ __forceinline__ double shfl_xor_f64(double v, int mask)
+__device__ __forceinline__ f16 f64_to_f16_rto(double v)
 {
-    const int lane = __lane_id();
-    const int src = (lane ^ mask) << 2;
-    uint64_t u = (uint64_t) __double_as_longlong(v);
-    uint32_t lo = (uint32_t) __builtin_amdgcn_ds_bpermute(src, (int) (uint32_t) u);
-    uint32_t hi = (uint32_t) __builtin_amdgcn_ds_bpermute(src, (int) (uint32_t) (u >> 32));
+    const float f = (float) v;
+    uint32_t fb = __float_as_uint(f);
+    const double back = (double) f;
+    if (back != v && !(fb & 1u)) fb += __builtin_fabs(back) < __builtin_fabs(v) ? 1u : 0xFFFFFFFFu;
+    return (f16) __uint_as_float(fb);
+}
+
+// ------------------------------------------------------------------------------------------
+// 128-point Hadamard, 16 lanes per block: lane r = lane & 15 holds elements 8r .. 8r+7, so a
+// wave transforms 4 blocks at once.  Natural-order Sylvester H[i,j] = (-1)^popcount(i&j):
+// element bits 0..2 are butterflies inside the lane, bits 3..6 are lane xor 1, 2, 4, 8 within
+// a 16-lane row, done with DPP moves (quad_perm, row_half_mirror, row_ror).  float64 sums of
+// fp16 data are exact, so the result does not depend on the butterfly order.
+// ------------------------------------------------------------------------------------------
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double x)
+{
+    const uint64_t u = (uint64_t) __double_as_longlong(x);
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_mov_dpp((int) (uint32_t) u, CTRL, 0xF, 0xF, true);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_mov_dpp((int) (uint32_t) (u >> 32), CTRL, 0xF, 0xF, true);
     return __longlong_as_double((long long) (((uint64_t) hi << 32) | lo));
 }
 
-__device__ __forceinline__ void wht128_f64(double& v0, double& v1)
+constexpr int DPP_QP_XOR1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int DPP_QP_XOR2 = 0x4E;     // quad_perm [2,3,0,1]
+constexpr int DPP_QP_REV = 0x1B;      // quad_perm [3,2,1,0]   (lane ^ 3)
+constexpr int DPP_HALF_MIRROR = 0x141; // lane ^ 7 within 8
+constexpr int DPP_ROR8 = 0x128;       // row_ror:8 == lane ^ 8 within 16
+
+// one cross-lane butterfly stage: lower lane a + b, upper lane a - b (fma with +-1 is exact
+// up to the single rounding of the sum, as the separate add / subtract would be)
+__device__ __forceinline__ void had_stage(double (&v)[8], const double (&p)[8], bool upper)
 {
-    const int lane = __lane_id();
-    double a = v0 + v1, b = v0 - v1;
-    v0 = a;
-    v1 = b;
+    const double s = upper ? -1.0 : 1.0;
 #pragma unroll
-    for (int m = 1; m < 64; m <<= 1) {
-        const double p0 = shfl_xor_f64(v0, m), p1 = shfl_xor_f64(v1, m);
-        const bool upper = (lane & m) != 0;
-        v0 = upper ? p0 - v0 : v0 + p0;
-        v1 = upper ? p1 - v1 : v1 + p1;
-    }
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_fma(s, v[i], p[i]);
 }
 
-// Full 128-block stage on a wave: in -> fp16(Had128(in [* pre]) * scale) [* post], fp16 bits.
-// pre / post may be null.  `in` and `out` are f16x2 views, lane L handles elements 2L, 2L+1.
-__device__ __forceinline__ uint32_t had128_pair(uint32_t in2, uint32_t pre2, bool has_pre, uint32_t post2,
-                                                bool has_post, double scale)
+__device__ __forceinline__ void wht128_x8(double (&v)[8])
 {
-    f16x2 x = __builtin_bit_cast(f16x2, in2);
-    if (has_pre) x = x * __builtin_bit_cast(f16x2, pre2);       // one fp16 rounding per product
-    double v0 = (double) x[0], v1 = (double) x[1];
-    wht128_f64(v0, v1);
-    f16x2 y;
-    y[0] = bits_f16(f64_to_f16_bits(v0 * scale));
-    y[1] = bits_f16(f64_to_f16_bits(v1 * scale));
-    if (has_post) y = y * __builtin_bit_cast(f16x2, post2);
-    return __builtin_bit_cast(uint32_t, y);
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (!(i & h)) {
+                const double a = v[i], b = v[i + h];
+                v[i] = a + b;
+                v[i + h] = a - b;
+            }
+    const int r = __lane_id() & 15;
+    double p[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = dpp_f64<DPP_QP_XOR1>(v[i]);
+    had_stage(v, p, r & 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = dpp_f64<DPP_QP_XOR2>(v[i]);
+    had_stage(v, p, r & 2);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = dpp_f64<DPP_QP_REV>(dpp_f64<DPP_HALF_MIRROR>(v[i]));
+    had_stage(v, p, r & 4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = dpp_f64<DPP_ROR8>(v[i]);
+    had_stage(v, p, r & 8);
+}
+
+// 8 fp16 in (16 B) -> 8 fp16 out: fp16(Had128(in [* pre]) * scale) [* post]; pre / post are the
+// matching 8 scale values (ignored when has_pre / has_post are false).  Each fp16 product is a
+// single rounding (packed fp16 multiplies), as in the reference kernels' hmul2 stages.
+__device__ __forceinline__ u32x4 had128_x8(u32x4 in, u32x4 pre, bool has_pre, u32x4 post, bool has_post, double scale)
+{
+    f16x8 x = __builtin_bit_cast(f16x8, in);
+    if (has_pre) x = x * __builtin_bit_cast(f16x8, pre);
+    double v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (double) x[i];
+    wht128_x8(v);
+    f16x8 y;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = f64_to_f16_rto(v[i] * scale);
+    if (has_post) y = y * __builtin_bit_cast(f16x8, post);
+    return __builtin_bit_cast(u32x4, y);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -217,21 +278,22 @@ __device__ __forceinline__ void decode_qblock(const uint32_t* W, uint32_t* P)
     decode_pairs_rec<BITS, CB, 0>(W, P, k_hi, k_add, k_lo, c6400);
 }
 
-// Load the BITS+1 words a lane needs for q-block q of a tile (tile32 = tile base as u32 words).
+// Load the BITS+1 words a lane needs for q-block q of a tile (tile32 = tile base as u32 words,
+// a global-address-space pointer).
 template <int BITS>
-__device__ __forceinline__ void load_qblock(const uint32_t* __restrict__ tile32, int q, uint32_t* W)
+__device__ __forceinline__ void load_qblock(gc_u32* __restrict__ tile32, int q, uint32_t* W)
 {
-    const uint32_t* p = tile32 + q * BITS;
+    gc_u32* p = tile32 + q * BITS;
     if constexpr (BITS % 4 == 0) {
 #pragma unroll
         for (int i = 0; i < BITS / 4; ++i) {
-            const u32x4 v = *reinterpret_cast<const u32x4*>(p + 4 * i);
+            const u32x4 v = *reinterpret_cast<gc_u32x4*>(p + 4 * i);
             W[1 + 4 * i] = v[0]; W[2 + 4 * i] = v[1]; W[3 + 4 * i] = v[2]; W[4 + 4 * i] = v[3];
         }
     } else if constexpr (BITS % 2 == 0) {
 #pragma unroll
         for (int i = 0; i < BITS / 2; ++i) {
-            const u32x2 v = *reinterpret_cast<const u32x2*>(p + 2 * i);
+            const u32x2 v = *reinterpret_cast<gc_u32x2*>(p + 2 * i);
             W[1 + 2 * i] = v[0]; W[2 + 2 * i] = v[1];
         }
     } else {

@@ -33,7 +33,7 @@ struct TrellisB {
     __device__ __forceinline__ void fetch(int kt0, int nt0, int t, uint32_t* W) const
     {
         const int ktl = t >> 6, ntl = (t >> 3) & 7, q = t & 7;
-        const uint32_t* tp = trellis + ((int64_t) (kt0 + ktl) * nt_total + nt0 + ntl) * (8 * BITS);
+        gc_u32* tp = as_global(trellis) + ((int64_t) (kt0 + ktl) * nt_total + nt0 + ntl) * (8 * BITS);
         load_qblock<BITS>(tp, q, W);
     }
     __device__ __forceinline__ void decode_store(const uint32_t* W, int t, char* bfrag) const

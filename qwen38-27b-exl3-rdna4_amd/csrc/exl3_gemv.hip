@@ -16,7 +16,7 @@
 
 #include <stdio.h>
 #include <stdlib.h>
-#include <mutex>
+#include <algorithm>
 
 using namespace exl3;
 
@@ -61,7 +61,7 @@ __global__ void __launch_bounds__(256) reconstruct_kernel(const uint32_t* __rest
     const int local_nt = t >> 3, q = t & 7;
     const int nts = min(32, nt_out - strip);
     if (local_nt < nts) {
-        const uint32_t* tp = trellis + ((int64_t) kt * nt_total + nt0 + strip + local_nt) * (8 * BITS);
+        gc_u32* tp = as_global(trellis) + ((int64_t) kt * nt_total + nt0 + strip + local_nt) * (8 * BITS);
         uint32_t Wd[BITS + 1];
         load_qblock<BITS>(tp, q, Wd);
         uint32_t P[16];
@@ -85,33 +85,46 @@ __global__ void __launch_bounds__(256) reconstruct_kernel(const uint32_t* __rest
 }
 
 // ============================================================================================
-// had_r_128: out = fp16(Had128(in [* pre]) * r * scale) [* post], one wave per 128-block
-// (reference binding `had_r_128`, vllm_plugin/exl3rocm/ops.py:88,97)
+// had_r_128: out = fp16(Had128(in [* pre]) * r * scale) [* post]; one 16-lane group per 128-block,
+// 4 blocks per wave (reference binding `had_r_128`, vllm_plugin/exl3rocm/ops.py:88,97)
 // ============================================================================================
-__global__ void __launch_bounds__(256) had_kernel(const uint32_t* __restrict__ in, int64_t ld_in, uint32_t* __restrict__ out,
-                                                  int64_t ld_out, int rows, int cols, const uint32_t* __restrict__ pre,
-                                                  const uint32_t* __restrict__ post, double scale)
+__global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ in, int64_t ld_in, uint16_t* __restrict__ out,
+                                                  int64_t ld_out, int rows, int cols, const uint16_t* __restrict__ pre,
+                                                  const uint16_t* __restrict__ post, double scale)
 {
     const int blocks_per_row = cols / 128;
-    const int64_t job = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (job >= (int64_t) rows * blocks_per_row) return;
-    const int lane = threadIdx.x & 63;
-    const int64_t row = job / blocks_per_row;
-    const int blk = (int) (job % blocks_per_row);
-    const int64_t e2 = (int64_t) blk * 64 + lane;      // index in half2 units within the row
-    const uint32_t v = in[row * (ld_in / 2) + e2];
-    const uint32_t r = had128_pair(v, pre ? pre[e2] : 0u, pre != nullptr, post ? post[e2] : 0u, post != nullptr,
-                                   R_SCALE * scale);
-    out[row * (ld_out / 2) + e2] = r;
+    const int64_t job = ((int64_t) blockIdx.x * 256 + threadIdx.x) >> 4;     // one 128-block per 16 lanes
+    const bool live = job < (int64_t) rows * blocks_per_row;
+    const int r = threadIdx.x & 15;
+    const int64_t row = live ? job / blocks_per_row : 0;
+    const int col = live ? (int) (job % blocks_per_row) * 128 + 8 * r : 0;
+    u32x4 v = {0u, 0u, 0u, 0u}, pv = v, qv = v;
+    if (live) {
+        v = *reinterpret_cast<const u32x4*>(in + row * ld_in + col);
+        if (pre) pv = *reinterpret_cast<const u32x4*>(pre + col);
+        if (post) qv = *reinterpret_cast<const u32x4*>(post + col);
+    }
+    // every lane takes part in the DPP exchanges; only live lanes store
+    const u32x4 res = had128_x8(v, pv, pre != nullptr, qv, post != nullptr, R_SCALE * scale);
+    if (live) *reinterpret_cast<u32x4*>(out + row * ld_out + col) = res;
 }
 
 // ============================================================================================
-// Fused GEMV
+// Fused GEMV with stream-K balancing
+//
+// Work unit: (128-column block cb, 128-row k slice ku) == two 64-row k steps == one Hadamard
+// block of the input; units are ordered cb-major, U in total, UPB = k / 128 per block.  The grid
+// has G workgroups (all resident); workgroup w owns units [w*U/G, (w+1)*U/G).  Wave i of a
+// workgroup covers n-tiles 2i, 2i+1 of the block; its lanes = (k-tile g of the step, n-tile,
+// q-block).  A workgroup keeps fp32 accumulators across consecutive units of one block and writes
+// one partial per block it touches; the block's completion counter counts the contributing
+// workgroups and the last one sums the partials in workgroup order (fixed for the shape, hence
+// deterministic), rounds C to fp16 and applies the output Hadamard and svh.
 // ============================================================================================
 struct GemvGroup {
     const uint32_t* trellis;   // tile words
-    const uint32_t* suh;       // fp16 pairs
-    const uint32_t* svh;       // fp16 pairs
+    const uint16_t* suh;
+    const uint16_t* svh;
     uint16_t* y;               // output columns of this group (row stride ldy)
 };
 
@@ -123,54 +136,49 @@ struct GemvArgs {
     const int64_t* tab_suh;
     const int64_t* tab_svh;
     int64_t group_col_stride;  // with tables: group i writes y + i * group_col_stride
-    int M, k, n, S;
+    int M, k, n;
+    int G, U, UPB, max_seg;    // grid, units, units per block, partial slots per workgroup
+    int chunk_units;           // units whose rotated input fits the LDS at once
     int64_t ldy;
-    float* part;               // [groups][NB][S][M][128] fp32 partials (S > 1)
+    float* part;               // [groups][G][max_seg][M][128] fp32 partials
     uint32_t* counters;        // [groups][NB], zero between calls
-    int xcd_remap;
 };
 
-template <int MT>
-__device__ __forceinline__ void gemv_load_a(const uint16_t* lds_a, int lda, int M, int j, int col, f16x8 (&A)[MT])
+constexpr int RED_BATCH = 16;                   // partial loads in flight per thread in the reduction
+constexpr int A_ROW = 136;                      // LDS row of one rotated 128-block (padded, halves)
+constexpr int LDS_BUDGET = 38 * 1024;           // per workgroup: 4 workgroups per CU
+
+// s_waitcnt vmcnt(0) (gfx9 encoding: expcnt / lgkmcnt left at their maxima), fenced against
+// compiler reordering: every vector-memory store of this wave has completed.
+__device__ __forceinline__ void wait_stores_complete()
 {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        const int m = mt * 16 + j;
-        f16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (m < M) v = *reinterpret_cast<const f16x8*>(lds_a + m * lda + col);
-        A[mt] = v;
-    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+__device__ __forceinline__ int wg_lo(int w, int U, int G) { return (int) ((int64_t) w * U / G); }
+// workgroup owning unit u: the largest w with floor(w*U/G) <= u
+__device__ __forceinline__ int wg_of_unit(int u, int U, int G) { return (int) (((int64_t) (u + 1) * G - 1) / U); }
+
+
+// Four workgroups (16 waves) per CU are resident at once: at most 128 VGPRs per lane.
 template <int BITS, int CB, int MT>
-__global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) gemv_kernel(GemvArgs a)
 {
     extern __shared__ __align__(16) uint16_t smem[];
     __shared__ int s_last;
-    const int NB = a.n / 128;
-    const int S = a.S;
-    int cb, sp;
-    {
-        const int b = blockIdx.x;
-        if (a.xcd_remap) {
-            const int per_xcd = (NB * S) / 8;
-            const int u = (b & 7) * per_xcd + (b >> 3);
-            cb = u / S;
-            sp = u % S;
-        } else {
-            cb = b / S;
-            sp = b % S;
-        }
-    }
-    const int grp = blockIdx.y;
+    const int w = blockIdx.x, grp = blockIdx.y;
+    const int G = a.G, U = a.U, UPB = a.UPB, M = a.M;
+    const int NB = a.n / 128, NT = a.n / 16;
     const uint32_t* trel;
-    const uint32_t* suh;
-    const uint32_t* svh;
+    const uint16_t* suh;
+    const uint16_t* svh;
     uint16_t* y;
     if (a.tab_trellis) {
         trel = reinterpret_cast<const uint32_t*>(a.tab_trellis[grp]);
-        suh = reinterpret_cast<const uint32_t*>(a.tab_suh[grp]);
-        svh = reinterpret_cast<const uint32_t*>(a.tab_svh[grp]);
+        suh = reinterpret_cast<const uint16_t*>(a.tab_suh[grp]);
+        svh = reinterpret_cast<const uint16_t*>(a.tab_svh[grp]);
         y = a.g[0].y + grp * a.group_col_stride;
     } else {
         trel = a.g[grp].trellis;
@@ -178,52 +186,186 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a)
         svh = a.g[grp].svh;
         y = a.g[grp].y;
     }
-    const int M = a.M;
-    const int KR = a.k / S;
-    const int k0 = sp * KR;
-    const int lda = KR + 8;                       // padded LDS row (halves): rows land on distinct banks
-    uint16_t* lds_a = smem;                       // [M][lda]
-    uint16_t* lds_c = smem + M * lda;             // [M][136]
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    gc_u32* const gtrel = as_global(trel);
+    gc_u16* const gsuh = as_global(suh);
+    gc_u16* const gsvh = as_global(svh);
+    gc_u16* const gx = as_global(a.x);
+    g_u16* const gy = as_global(y);
+    uint16_t* lds_a = smem;                                   // [chunk_units][M][A_ROW]
+    uint16_t* lds_c = smem + a.chunk_units * M * A_ROW;       // [M][A_ROW] fp16 C of one block
+    uint16_t* lds_zero = lds_c + M * A_ROW;                   // one zero row: A operand of rows >= M
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int g = lane >> 4, j = lane & 15, q = j & 7;
+    const int ulo = wg_lo(w, U, G), uhi = wg_lo(w + 1, U, G);
+    if (ulo >= uhi) return;                                   // uniform per workgroup
+    const int seg0_cb = ulo / UPB;
+    float* part_grp = a.part + (int64_t) grp * G * a.max_seg * M * 128;
 
-    // ---- prologue: rotated input slice ------------------------------------------------------
-    const int nblk = KR / 128;
-    for (int job = wave; job < M * nblk; job += 4) {
-        const int m = job / nblk, blk = job % nblk;
-        const uint32_t xv = reinterpret_cast<const uint32_t*>(a.x + (int64_t) m * a.ldx + k0 + blk * 128)[lane];
-        const uint32_t sv = suh[(k0 + blk * 128) / 2 + lane];
-        reinterpret_cast<uint32_t*>(lds_a + m * lda + blk * 128)[lane] = had128_pair(xv, sv, true, 0u, false, R_SCALE);
+    // step d (0, 1) of unit (cb, ku) for this lane: a per-lane base plus a uniform offset
+    gc_u32* lane_base = gtrel + ((int64_t) g * NT + wave * 2 + (j >> 3)) * (8 * BITS);
+    auto tile_at = [&](int cb, int ku, int d) -> gc_u32* {
+        return lane_base + ((int64_t) (2 * ku + d) * 4 * NT + cb * 8) * (8 * BITS);
+    };
+    auto tile_of = [&](int u, int d) -> gc_u32* {
+        const int cb = u / UPB;
+        return tile_at(cb, u - cb * UPB, d);
+    };
+    // rotated-input job i of a chunk starting at unit u0: (unit u0 + i / M, row i % M), 16 lanes each
+    auto job_src = [&](int u0, int i, int& m, int& col) {
+        const int u = u0 + i / M;
+        m = i - (i / M) * M;
+        col = (u - (u / UPB) * UPB) * 128 + 8 * (threadIdx.x & 15);
+    };
+
+    // The prologue and the completion phase sit on every workgroup's critical path while other
+    // workgroups on the same SIMDs run VALU-heavy decode loops: give them issue priority.
+    __builtin_amdgcn_s_setprio(2);
+
+    // ---- first input chunk: its x / suh loads go out before the trellis ring ----------------
+    const int nfirst = min(a.chunk_units, uhi - ulo) * M;
+    u32x4 px = {0u, 0u, 0u, 0u}, ps = px;
+    {
+        const int i = threadIdx.x >> 4;
+        if (i < nfirst) {
+            int m, col;
+            job_src(ulo, i, m, col);
+            px = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
+            ps = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+        }
     }
+    uint32_t W0[BITS + 1], W1[BITS + 1];
+    load_qblock<BITS>(tile_of(ulo, 0), q, W0);
+    load_qblock<BITS>(tile_of(ulo, 1), q, W1);
+    if (wave * 4 < nfirst) {                                  // waves without a job skip the transform
+        const int i = threadIdx.x >> 4;                       // whole 16-lane groups take part
+        const u32x4 r = had128_x8(px, ps, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
+        if (i < nfirst) {
+            int m, col;
+            job_src(ulo, i, m, col);
+            *reinterpret_cast<u32x4*>(lds_a + ((i / M) * M + m) * A_ROW + 8 * (threadIdx.x & 15)) = r;
+        }
+        for (int i2 = i + 16; i2 < nfirst; i2 += 16) {
+            int m, col;
+            job_src(ulo, i2, m, col);
+            const u32x4 xv = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
+            const u32x4 sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+            *reinterpret_cast<u32x4*>(lds_a + ((i2 / M) * M + m) * A_ROW + 8 * (threadIdx.x & 15)) =
+                had128_x8(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
+        }
+    }
+    if (threadIdx.x < A_ROW / 8) *reinterpret_cast<u32x4*>(lds_zero + 8 * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
 
-    // ---- main loop -----------------------------------------------------------------------------
-    const int g = lane >> 4, j = lane & 15, q = j & 7;
-    const int NT = a.n / 16;
-    const int nt = cb * 8 + wave * 2 + (j >> 3);
-    const int kt0 = (k0 >> 4) + g;
-    const int64_t tstride = (int64_t) 4 * NT * (8 * BITS);      // 4 k-tiles further
-    const uint32_t* tp = trel + ((int64_t) kt0 * NT + nt) * (8 * BITS);
-    const int steps = KR / 64;
+    // A operand rows of this lane: rows >= M read the zero row, so the step has no branches
+    int a_row[MT];
+    bool a_live[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        a_live[mt] = mt * 16 + j < M;
+        a_row[mt] = a_live[mt] ? (mt * 16 + j) * A_ROW : (int) (lds_zero - lds_a);
+    }
 
-    f32x4 acc[2][MT];
+    f32x4 acc[2][MT], pacc[2][MT];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < MT; ++mt) acc[h][mt] = pacc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    uint32_t Wn[BITS + 1];
-    load_qblock<BITS>(tp, q, Wn);
-    for (int st = 0; st < steps; ++st) {
-        uint32_t Wc[BITS + 1];
+    const int colb = wave * 32 + (j >> 3) * 16 + (j & 7);    // + 8h: column of this lane in the block
+    auto write_partial = [&](const f32x4 (&ac)[2][MT], int cb) {
+        float* slab = part_grp + ((int64_t) w * a.max_seg + (cb - seg0_cb)) * M * 128;
 #pragma unroll
-        for (int i = 0; i <= BITS; ++i) Wc[i] = Wn[i];
-        if (st + 1 < steps) load_qblock<BITS>(tp + (int64_t) (st + 1) * tstride, q, Wn);
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int m = mt * 16 + 4 * g + v;
+                    if (m < M)
+                        __hip_atomic_store(&slab[m * 128 + colb + 8 * h], ac[h][mt][v], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                }
+    };
+
+    // Partials of blocks cb_a (if >= 0) and cb_b are written: count this workgroup in and
+    // reduce every block it completed.  Uniform control flow (every thread calls it).
+    auto complete = [&](int cb_a, int cb_b) {
+        // The partials are device-scope (write-through) stores: once complete (vmcnt(0)) they
+        // are visible to device-scope loads from any XCD, so no cache-wide release is needed.
+        wait_stores_complete();
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int last = 0;
+            for (int i = 0; i < 2; ++i) {
+                const int cb = i == 0 ? cb_a : cb_b;
+                if (cb < 0) continue;
+                const int wf = wg_of_unit(cb * UPB, U, G), wl = wg_of_unit(cb * UPB + UPB - 1, U, G);
+                const uint32_t prev = __hip_atomic_fetch_add(&a.counters[grp * NB + cb], 1u, __ATOMIC_RELAXED,
+                                                             __HIP_MEMORY_SCOPE_AGENT);
+                if (prev == (uint32_t) (wl - wf)) last |= 1 << i;
+            }
+            s_last = last;
+        }
+        __syncthreads();
+        const int last = s_last;
+        for (int i = 0; i < 2; ++i) {
+            if (!(last & (1 << i))) continue;
+            const int cb = i == 0 ? cb_a : cb_b;
+            // contributor wf holds block cb in its segment cb - first_cb(wf); every later
+            // contributor starts inside cb, so its segment is 0.  Loads go out in batches of
+            // RED_BATCH; the sum runs in contributor order.
+            const int wf = wg_of_unit(cb * UPB, U, G), wl = wg_of_unit(cb * UPB + UPB - 1, U, G);
+            const int seg_f = cb - wg_lo(wf, U, G) / UPB;
+            const int nc = wl - wf + 1;
+            for (int e = threadIdx.x; e < M * 128; e += 256) {
+                float sum = 0.f;
+                for (int c0 = 0; c0 < nc; c0 += RED_BATCH) {
+                    float v[RED_BATCH];
+#pragma unroll
+                    for (int ii = 0; ii < RED_BATCH; ++ii) {
+                        const int c = c0 + ii;
+                        const int64_t slot = c == 0 ? (int64_t) wf * a.max_seg + seg_f : (int64_t) (wf + c) * a.max_seg;
+                        v[ii] = c < nc ? __hip_atomic_load(part_grp + slot * M * 128 + e, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT)
+                                       : 0.f;
+                    }
+#pragma unroll
+                    for (int ii = 0; ii < RED_BATCH; ++ii)
+                        if (c0 + ii < nc) sum += v[ii];
+                }
+                lds_c[(e >> 7) * A_ROW + (e & 127)] = f16_bits((f16) sum);
+            }
+            if (threadIdx.x == 0)                              // ready for the next call (stream order)
+                __hip_atomic_store(&a.counters[grp * NB + cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            // output Hadamard + svh: 16 lanes per row
+            const int rr = threadIdx.x & 15;
+            const u32x4 sv = *reinterpret_cast<gc_u32x4*>(gsvh + cb * 128 + 8 * rr);
+            for (int m0 = 0; m0 < M; m0 += 16) {
+                const int m = m0 + (threadIdx.x >> 4);
+                const bool live = m < M;
+                u32x4 c = {0u, 0u, 0u, 0u};
+                if (live) c = *reinterpret_cast<const u32x4*>(lds_c + m * A_ROW + 8 * rr);
+                const u32x4 r = had128_x8(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, R_SCALE);
+                if (live) *reinterpret_cast<g_u32x4*>(gy + (int64_t) m * a.ldy + cb * 128 + 8 * rr) = r;
+            }
+            __syncthreads();                                   // lds_c free for the next block
+        }
+    };
+
+    // one k step: decode the lane's q-block, refill the ring slot (the last unit reloads itself:
+    // in bounds and never used), two MFMAs per tile column half
+    auto step = [&](uint32_t (&Wr)[BITS + 1], int unit_off, int d, int cb_n, int ku_n) {
         uint32_t P[16];
-        decode_qblock<BITS, CB>(Wc, P);
-        const int col = (st * 4 + g) * 16;
+        decode_qblock<BITS, CB>(Wr, P);
+        load_qblock<BITS>(tile_at(cb_n, ku_n, d), q, Wr);
         f16x8 A0[MT], A1[MT];
-        gemv_load_a<MT>(lds_a, lda, M, j, col, A0);
-        gemv_load_a<MT>(lds_a, lda, M, j, col + 8, A1);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const uint16_t* ap = lds_a + (a_live[mt] ? unit_off : 0) + a_row[mt] + 64 * d + 16 * g;
+            A0[mt] = *reinterpret_cast<const f16x8*>(ap);
+            A1[mt] = *reinterpret_cast<const f16x8*>(ap + 8);
+        }
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const u32x4 B0 = {P[2 * h], P[4 + 2 * h], P[8 + 2 * h], P[12 + 2 * h]};
@@ -234,58 +376,63 @@ __global__ void __launch_bounds__(256) gemv_kernel(GemvArgs a)
                 acc[h][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[mt], __builtin_bit_cast(f16x8, B1), acc[h][mt], 0, 0, 0);
             }
         }
-    }
+    };
 
-    // ---- epilogue ------------------------------------------------------------------------------
-    // lane holds rows mt*16 + 4*g + v (v = 0..3) of MFMA column j; MFMA h covers tile columns +8h
-    const int colb = wave * 32 + (j >> 3) * 16 + (j & 7);        // + 8h
-    if (S == 1) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int m = mt * 16 + 4 * g + v;
-                    if (m < M) lds_c[m * 136 + colb + 8 * h] = f16_bits((f16) acc[h][mt][v]);
-                }
-    } else {
-        float* slab = a.part + ((int64_t) (grp * NB + cb) * S + sp) * M * 128;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int m = mt * 16 + 4 * g + v;
-                    if (m < M) slab[m * 128 + colb + 8 * h] = acc[h][mt][v];
-                }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            const uint32_t prev = __hip_atomic_fetch_add(&a.counters[grp * NB + cb], 1u, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-            s_last = prev == (uint32_t) (S - 1);
+    __builtin_amdgcn_s_setprio(0);
+    int cb_cur = seg0_cb, cb_prev = -1;
+    // the unit being processed (cb_u, ku_u) and the next one, walked without divisions
+    int cb_u = seg0_cb, ku_u = ulo - seg0_cb * UPB;
+    for (int c0 = ulo; c0 < uhi; c0 += a.chunk_units) {
+        const int c1 = min(c0 + a.chunk_units, uhi);
+        if (c0 != ulo) {                                      // later chunks (large M x long ranges)
+            __syncthreads();
+            for (int i = threadIdx.x >> 4; i < (c1 - c0) * M; i += 16) {
+                int m, col;
+                job_src(c0, i, m, col);
+                const u32x4 xv = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
+                const u32x4 sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+                *reinterpret_cast<u32x4*>(lds_a + ((i / M) * M + m) * A_ROW + 8 * (threadIdx.x & 15)) =
+                    had128_x8(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
+            }
+            __syncthreads();
         }
-        __syncthreads();
-        if (!s_last) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        const float* base = a.part + (int64_t) (grp * NB + cb) * S * M * 128;
-        for (int e = threadIdx.x; e < M * 128; e += 256) {
-            float s = 0.f;
-            for (int i = 0; i < S; ++i) s += __builtin_nontemporal_load(base + (int64_t) i * M * 128 + e);
-            lds_c[(e >> 7) * 136 + (e & 127)] = f16_bits((f16) s);
+        for (int u = c0; u < c1; ++u) {
+            const int cb = cb_u;
+            int cb_n = cb_u, ku_n = ku_u + 1;
+            if (ku_n == UPB) {
+                ku_n = 0;
+                ++cb_n;
+            }
+            if (u + 1 >= uhi) {                               // the last unit reloads itself
+                cb_n = cb_u;
+                ku_n = ku_u;
+            }
+            if (cb != cb_cur) {
+                if (cb_prev >= 0) {                           // a third block: settle the oldest now
+                    write_partial(pacc, cb_prev);
+                    complete(-1, cb_prev);
+                }
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        pacc[h][mt] = acc[h][mt];
+                        acc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
+                cb_prev = cb_cur;
+                cb_cur = cb;
+            }
+            const int unit_off = (u - c0) * M * A_ROW;
+            step(W0, unit_off, 0, cb_n, ku_n);
+            step(W1, unit_off, 1, cb_n, ku_n);
+            cb_u = cb_n;
+            ku_u = ku_n;
         }
-        if (threadIdx.x == 0) a.counters[grp * NB + cb] = 0u;    // ready for the next call (stream order)
     }
-    __syncthreads();
-    // output Hadamard + svh for every row of this 128-column block
-    const uint32_t sv = svh[cb * 64 + lane];
-    for (int m = wave; m < M; m += 4) {
-        const uint32_t c2 = reinterpret_cast<const uint32_t*>(lds_c + m * 136)[lane];
-        const uint32_t r = had128_pair(c2, 0u, false, sv, true, R_SCALE);
-        reinterpret_cast<uint32_t*>(y + (int64_t) m * a.ldy + cb * 128)[lane] = r;
-    }
+    __builtin_amdgcn_s_setprio(2);
+    if (cb_prev >= 0) write_partial(pacc, cb_prev);
+    write_partial(acc, cb_cur);
+    complete(cb_prev, cb_cur);
 }
 
 // ============================================================================================
@@ -301,37 +448,46 @@ int env_int(const char* name, int dflt)
 
 int codebook_of(int mcg, int mul1) { return mul1 ? 2 : (mcg ? 1 : 0); }
 
-// Split count over k: depends on (k, n) only (never on m or the group count), so rows and groups
-// stay bitwise equal to the single-row, single-group call.
-int choose_splits(int k, int n)
+// Stream-K grid: workgroups per group, from (k, n, groups) only -- never from m -- so every row
+// of an m-row call is bitwise equal to the m == 1 call, and a module's grouped launches agree
+// across row counts.  All workgroups of a launch are resident at once (4 per CU at the kernel's
+// register budget), each with at least two 64-row k steps.
+constexpr int RESIDENT_WGS = 768;      // 256 CUs x 3 (measured best of 256..1024 for the 5120 / 17408 layers)
+
+int choose_grid(int k, int n, int groups)
 {
-    const int kb = k / 128, nb = n / 128;
-    const int forced = env_int("EXL3_GEMV_SPLITS", 0);
-    if (forced > 0 && kb % forced == 0) return forced;
-    const int target = env_int("EXL3_GEMV_TARGET_WGS", 512);
-    int best = kb;
-    for (int d = 1; d <= kb; ++d) {
-        if (kb % d) continue;
-        if (kb / d > 16) continue;                 // k-slice <= 2048 (LDS budget at M = 32)
-        best = d;
-        if ((int64_t) nb * d >= target) break;
-    }
-    return best;
+    const int64_t UPB = k / 128, U = (int64_t) (n / 128) * UPB;
+    const int forced = env_int("EXL3_GEMV_GRID", 0);
+    // all workgroups resident; at most ~max_contrib workgroups sharing one block
+    const int max_contrib = env_int("EXL3_GEMV_MAX_CONTRIB", 32);
+    const int64_t min_units = std::max<int64_t>(1, (UPB + max_contrib - 1) / max_contrib);
+    int64_t G = forced > 0 ? forced : std::min<int64_t>(RESIDENT_WGS / std::max(groups, 1), U / min_units);
+    return (int) std::max<int64_t>(1, std::min<int64_t>(G, U));
 }
 
-size_t lds_bytes(int M, int KR) { return (size_t) M * (KR + 8) * 2 + (size_t) M * 136 * 2; }
+int max_segments(int k, int n, int G)
+{
+    const int64_t UPB = k / 128, U = (int64_t) (n / 128) * UPB;
+    const int64_t per = (U + G - 1) / G;
+    return (int) ((per + UPB - 1) / UPB + 1);
+}
+
+// units whose rotated input a workgroup stages at once (all of them when they fit)
+int chunk_units(int m, int k, int n, int G)
+{
+    const int64_t U = (int64_t) (n / 128) * (k / 128);
+    const int64_t per = (U + G - 1) / G;
+    const int64_t fit = std::max<int64_t>(1, (LDS_BUDGET / (2 * A_ROW) - m) / m);
+    return (int) std::max<int64_t>(1, std::min(per, fit));
+}
+
+size_t lds_bytes(int M, int cu) { return ((size_t) (cu + 1) * M + 1) * A_ROW * 2; }
 
 template <int BITS, int CB, int MT>
 int launch_gemv_t(const GemvArgs& a, int groups, hipStream_t stream)
 {
-    const int NB = a.n / 128;
-    const size_t lds = lds_bytes(a.M, a.k / a.S);
-    static std::once_flag once;
-    std::call_once(once, [] {
-        (void) hipFuncSetAttribute((const void*) gemv_kernel<BITS, CB, MT>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            150 * 1024);
-    });
-    hipLaunchKernelGGL((gemv_kernel<BITS, CB, MT>), dim3(NB * a.S, groups), dim3(256), lds, stream, a);
+    hipLaunchKernelGGL((gemv_kernel<BITS, CB, MT>), dim3(a.G, groups), dim3(256), lds_bytes(a.M, a.chunk_units),
+                       stream, a);
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 
@@ -365,16 +521,15 @@ int launch_gemv(const GemvArgs& a, int bits, int cb, int groups, hipStream_t s)
     }
 }
 
-// workspace layout: [counters: fixed EXL3_GEMV_COUNTER_BYTES region][partials: groups*NB*S*M*128 f32].
+// workspace layout: [counters: fixed EXL3_GEMV_COUNTER_BYTES region][partials: groups*G*max_seg*M*128 f32].
 // The counter region has a fixed size so calls of different shapes sharing one workspace never
 // see another shape's partial sums where their counters live.
 constexpr size_t COUNTER_BYTES = EXL3_GEMV_COUNTER_BYTES;
 
 size_t gemv_ws_bytes(int m, int k, int n, int groups)
 {
-    const int S = choose_splits(k, n), NB = n / 128;
-    if (S == 1) return COUNTER_BYTES;
-    return COUNTER_BYTES + (size_t) groups * NB * S * m * 128 * 4;
+    const int G = choose_grid(k, n, groups);
+    return COUNTER_BYTES + (size_t) groups * G * max_segments(k, n, G) * m * 128 * 4;
 }
 
 bool shape_ok(int m, int k, int n, int K)
@@ -387,16 +542,18 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, int groups, con
                 size_t ws_bytes, void* stream)
 {
     if (!x || groups < 1 || groups > EXL3_MAX_GROUPS || ldx < k || ldy < n) return EXL3_EINVAL;
-    // the kernel moves fp16 pairs: x rows, y rows, suh and svh must be 4-byte aligned
-    if ((ldx & 1) || (ldy & 1) || (((uintptr_t) x) & 3)) return EXL3_EINVAL;
+    // the kernel moves fp16 in 16-byte groups of 8: x rows, y rows, suh and svh 16-byte aligned
+    if ((ldx & 7) || (ldy & 7) || (((uintptr_t) x) & 15)) return EXL3_EINVAL;
     // with pointer tables only gs[0].y is given; the table entries are the caller's contract
     for (int i = 0; i < (tabs ? 1 : groups); ++i) {
-        if (!gs[i].y || (((uintptr_t) gs[i].y) & 3)) return EXL3_EINVAL;
-        if (!tabs && ((((uintptr_t) gs[i].suh) & 3) || (((uintptr_t) gs[i].svh) & 3) || (((uintptr_t) gs[i].trellis) & 15)))
+        if (!gs[i].y || (((uintptr_t) gs[i].y) & 15)) return EXL3_EINVAL;
+        if (!tabs && ((((uintptr_t) gs[i].suh) & 15) || (((uintptr_t) gs[i].svh) & 15) ||
+                      (((uintptr_t) gs[i].trellis) & 15)))
             return EXL3_EINVAL;
     }
     if (groups > 1 && !tabs && m > 1 && ldy < (int64_t) groups * n) return EXL3_EINVAL;
     if (!shape_ok(m, k, n, K)) return EXL3_DECLINED;
+    if ((size_t) groups * (n / 128) * 4 > COUNTER_BYTES) return EXL3_DECLINED;
     if (ws_bytes < gemv_ws_bytes(m, k, n, groups) || !ws) return EXL3_EWORKSPACE;
     GemvArgs a{};
     a.x = (const uint16_t*) x;
@@ -412,13 +569,14 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, int groups, con
     a.M = m;
     a.k = k;
     a.n = n;
-    a.S = choose_splits(k, n);
+    a.G = choose_grid(k, n, groups);
+    a.UPB = k / 128;
+    a.U = (n / 128) * a.UPB;
+    a.max_seg = max_segments(k, n, a.G);
+    a.chunk_units = chunk_units(m, k, n, a.G);
     a.ldy = ldy;
-    const int NB = n / 128;
-    if ((size_t) groups * NB * 4 > COUNTER_BYTES) return EXL3_DECLINED;
     a.counters = (uint32_t*) ws;
     a.part = (float*) ((char*) ws + COUNTER_BYTES);
-    a.xcd_remap = (NB * a.S) % 8 == 0 && NB % 8 == 0;
     return launch_gemv(a, K, codebook_of(mcg, mul1), groups, (hipStream_t) stream);
 }
 
@@ -431,7 +589,11 @@ extern "C" {
 
 int exl3_abi_version(void) { return EXL3_ABI_VERSION; }
 
-int exl3_gemv_splits(int k, int n) { return (k % 128 || k < 128) ? 0 : choose_splits(k, n); }
+int exl3_gemv_grid(int k, int n, int groups)
+{
+    return (k % 128 || k < 128 || n % 128 || n < 128 || groups < 1 || groups > EXL3_MAX_GROUPS) ? 0
+                                                                                               : choose_grid(k, n, groups);
+}
 
 size_t exl3_gemv_workspace_size(int m, int k, int n, int K, int groups)
 {
@@ -454,7 +616,7 @@ int exl3_gemv(const void* x, int64_t ldx, const void* trellis, void* y, int64_t 
     (void) A_had;
     if (!trellis || !y || !suh || !svh) return EXL3_EINVAL;
     if (m != 1) return EXL3_DECLINED;
-    GemvGroup g{(const uint32_t*) trellis, (const uint32_t*) suh, (const uint32_t*) svh, (uint16_t*) y};
+    GemvGroup g{(const uint32_t*) trellis, (const uint16_t*) suh, (const uint16_t*) svh, (uint16_t*) y};
     return gemv_common(x, ldx, &g, 1, nullptr, 0, ldy, m, k, n, K, mcg, mul1, workspace, ws_bytes, stream);
 }
 
@@ -464,7 +626,7 @@ int exl3_gemv_mr(const void* x, int64_t ldx, const void* trellis, void* y, int64
 {
     (void) A_had;
     if (!trellis || !y || !suh || !svh) return EXL3_EINVAL;
-    GemvGroup g{(const uint32_t*) trellis, (const uint32_t*) suh, (const uint32_t*) svh, (uint16_t*) y};
+    GemvGroup g{(const uint32_t*) trellis, (const uint16_t*) suh, (const uint16_t*) svh, (uint16_t*) y};
     return gemv_common(x, ldx, &g, 1, nullptr, 0, ldy, m, k, n, K, mcg, mul1, workspace, ws_bytes, stream);
 }
 
@@ -478,7 +640,7 @@ int exl3_gemv_mr_grouped(const void* x, int64_t ldx, const void* const* trellis,
     GemvGroup gs[EXL3_MAX_GROUPS];
     for (int i = 0; i < groups; ++i) {
         if (!trellis[i] || !suh[i] || !svh[i]) return EXL3_EINVAL;
-        gs[i] = {(const uint32_t*) trellis[i], (const uint32_t*) suh[i], (const uint32_t*) svh[i],
+        gs[i] = {(const uint32_t*) trellis[i], (const uint16_t*) suh[i], (const uint16_t*) svh[i],
                  (uint16_t*) y + (int64_t) i * n};
     }
     return gemv_common(x, ldx, gs, groups, nullptr, 0, ldy, m, k, n, K, mcg, mul1, workspace, ws_bytes, stream);
@@ -545,14 +707,14 @@ int exl3_decode(const void* states, void* out_f32, int64_t count, int mcg, int m
 int exl3_had_r_128(const void* in, int64_t ld_in, void* out, int64_t ld_out, int rows, int cols, const void* pre,
                    const void* post, float scale, void* stream)
 {
-    if (!in || !out || rows < 0 || cols % 128 || cols < 128 || ld_in < cols || ld_out < cols || ld_in % 2 || ld_out % 2 ||
-        (((uintptr_t) in) & 3) || (((uintptr_t) out) & 3) || (((uintptr_t) pre) & 3) || (((uintptr_t) post) & 3))
+    if (!in || !out || rows < 0 || cols % 128 || cols < 128 || ld_in < cols || ld_out < cols || ld_in % 8 || ld_out % 8 ||
+        (((uintptr_t) in) & 15) || (((uintptr_t) out) & 15) || (((uintptr_t) pre) & 15) || (((uintptr_t) post) & 15))
         return EXL3_EINVAL;
     if (rows == 0) return EXL3_OK;
-    const int64_t jobs = (int64_t) rows * (cols / 128);
-    hipLaunchKernelGGL(had_kernel, dim3((unsigned) ((jobs + 3) / 4)), dim3(256), 0, (hipStream_t) stream,
-                       (const uint32_t*) in, ld_in, (uint32_t*) out, ld_out, rows, cols, (const uint32_t*) pre,
-                       (const uint32_t*) post, (double) scale);
+    const int64_t jobs = (int64_t) rows * (cols / 128);           // 16 lanes each
+    hipLaunchKernelGGL(had_kernel, dim3((unsigned) ((jobs + 15) / 16)), dim3(256), 0, (hipStream_t) stream,
+                       (const uint16_t*) in, ld_in, (uint16_t*) out, ld_out, rows, cols, (const uint16_t*) pre,
+                       (const uint16_t*) post, (double) scale);
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 
