@@ -15,6 +15,10 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 OUT = os.path.join(HERE, "exl3rocm", "libexl3_mi355x.so")
 SOURCES = ["exl3_gemv.hip", "exl3_gemm.hip"]
+# Per-source extra flags.  The GEMV decode is long chains of packed-math (VOP3P) ops whose results
+# need extra wait states on gfx950; the ILP scheduler interleaves the independent chains so the
+# hazards are hidden instead of padded with s_nop.
+EXTRA = {"exl3_gemv.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
@@ -25,7 +29,7 @@ FLAGS = [
 
 def _compile(src: str, objdir: str) -> str:
     obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)

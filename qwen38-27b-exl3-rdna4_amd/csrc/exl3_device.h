@@ -39,6 +39,7 @@ typedef __attribute__((address_space(1))) uint16_t g_u16;
 typedef __attribute__((address_space(1))) const u32x4 gc_u32x4;
 typedef __attribute__((address_space(1))) u32x4 g_u32x4;
 typedef __attribute__((address_space(1))) const u32x2 gc_u32x2;
+typedef __attribute__((address_space(1))) const uint8_t gc_u8;
 
 template <class T>
 __device__ __forceinline__ __attribute__((address_space(1))) T* as_global(T* p)
@@ -302,6 +303,61 @@ __device__ __forceinline__ void load_qblock(gc_u32* __restrict__ tile32, int q, 
     }
     const int prev = q == 0 ? 8 * BITS - 1 : q * BITS - 1;
     W[0] = tile32[prev];
+}
+
+// The same q-block load from a uniform base plus per-lane byte offsets (32-bit): the loads then
+// use the scalar-base + vector-offset address form, with no per-step address arithmetic.
+// off_main addresses word q*BITS of the lane's tile, off_prev the ring predecessor word.
+template <int BITS>
+__device__ __forceinline__ void load_qblock_at(gc_u8* __restrict__ base, uint32_t off_main, uint32_t off_prev,
+                                               uint32_t* W)
+{
+    gc_u8* p = base + off_main;
+    if constexpr (BITS % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < BITS / 4; ++i) {
+            const u32x4 v = *reinterpret_cast<gc_u32x4*>(p + 16 * i);
+            W[1 + 4 * i] = v[0]; W[2 + 4 * i] = v[1]; W[3 + 4 * i] = v[2]; W[4 + 4 * i] = v[3];
+        }
+    } else if constexpr (BITS % 2 == 0) {
+#pragma unroll
+        for (int i = 0; i < BITS / 2; ++i) {
+            const u32x2 v = *reinterpret_cast<gc_u32x2*>(p + 8 * i);
+            W[1 + 2 * i] = v[0]; W[2 + 2 * i] = v[1];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) W[1 + i] = *reinterpret_cast<gc_u32*>(p + 4 * i);
+    }
+    W[0] = *reinterpret_cast<gc_u32*>(base + off_prev);
+}
+
+// Buffer-resource form: the trellis is one raw buffer (dword 3 of the resource: gfx9 raw 32-bit
+// format), the unit's byte offset a scalar, the lane's byte offsets fixed VGPRs.  No address
+// arithmetic per load, and the hardware range check turns any stray offset into zeros.
+constexpr int RAW_BUFFER_FLAGS = 0x00020000;
+
+template <int BITS>
+__device__ __forceinline__ void load_qblock_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t off_main, uint32_t off_prev,
+                                                uint32_t soff, uint32_t* W)
+{
+    if constexpr (BITS % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < BITS / 4; ++i) {
+            const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off_main + 16 * i, soff, 0));
+            W[1 + 4 * i] = v[0]; W[2 + 4 * i] = v[1]; W[3 + 4 * i] = v[2]; W[4 + 4 * i] = v[3];
+        }
+    } else if constexpr (BITS % 2 == 0) {
+#pragma unroll
+        for (int i = 0; i < BITS / 2; ++i) {
+            const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, off_main + 8 * i, soff, 0));
+            W[1 + 2 * i] = v[0]; W[2 + 2 * i] = v[1];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < BITS; ++i) W[1 + i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, off_main + 4 * i, soff, 0);
+    }
+    W[0] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, off_prev, soff, 0);
 }
 
 }  // namespace exl3

@@ -17,8 +17,17 @@
 #include <stdio.h>
 #include <stdlib.h>
 #include <algorithm>
+#include <utility>
 
 using namespace exl3;
+
+// f(integral_constant<int, I>) for I in the sequence: ring slots are indexed by constants in the
+// source, so the ring always lives in registers (a loop index here could leave it in scratch memory)
+template <class F, int... I>
+__device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&& f)
+{
+    (f(std::integral_constant<int, I>{}), ...);
+}
 
 // ============================================================================================
 // Codebook decode of raw states (reference binding `decode`, tests/test_gpu_parity.py:101-109)
@@ -146,7 +155,9 @@ struct GemvArgs {
 
 constexpr int RED_BATCH = 16;                   // partial loads in flight per thread in the reduction
 constexpr int A_ROW = 136;                      // LDS row of one rotated 128-block (padded, halves)
-constexpr int LDS_BUDGET = 38 * 1024;           // per workgroup: 4 workgroups per CU
+constexpr int LDS_BUDGET = 64 * 1024;           // per workgroup: 2 workgroups per CU
+constexpr int RING = 8;                         // 64-row k steps in flight per wave (even)
+constexpr int WAVES_PER_SIMD = 2;
 
 // s_waitcnt vmcnt(0) (gfx9 encoding: expcnt / lgkmcnt left at their maxima), fenced against
 // compiler reordering: every vector-memory store of this wave has completed.
@@ -162,12 +173,13 @@ __device__ __forceinline__ int wg_lo(int w, int U, int G) { return (int) ((int64
 __device__ __forceinline__ int wg_of_unit(int u, int U, int G) { return (int) (((int64_t) (u + 1) * G - 1) / U); }
 
 
-// Four workgroups (16 waves) per CU are resident at once: at most 128 VGPRs per lane.
+// Two workgroups (8 waves) per CU are resident at once: up to 256 registers per lane, enough for
+// a ring deep enough that one wave alone keeps its SIMD busy.
 template <int BITS, int CB, int MT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))) gemv_kernel(GemvArgs a)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_SIMD, WAVES_PER_SIMD))) gemv_kernel(GemvArgs a)
 {
     extern __shared__ __align__(16) uint16_t smem[];
-    __shared__ int s_last;
+    __shared__ int s_last[256];
     const int w = blockIdx.x, grp = blockIdx.y;
     const int G = a.G, U = a.U, UPB = a.UPB, M = a.M;
     const int NB = a.n / 128, NT = a.n / 16;
@@ -181,19 +193,27 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))
         svh = reinterpret_cast<const uint16_t*>(a.tab_svh[grp]);
         y = a.g[0].y + grp * a.group_col_stride;
     } else {
-        trel = a.g[grp].trellis;
-        suh = a.g[grp].suh;
-        svh = a.g[grp].svh;
-        y = a.g[grp].y;
+        // constant indices only: a runtime index into the kernel-argument struct would copy it to
+        // scratch memory, and every later read of it would be a vector-memory load
+        const GemvGroup gg = grp == 0 ? a.g[0] : grp == 1 ? a.g[1] : grp == 2 ? a.g[2] : a.g[3];
+        trel = gg.trellis;
+        suh = gg.suh;
+        svh = gg.svh;
+        y = gg.y;
     }
-    gc_u32* const gtrel = as_global(trel);
+    // the trellis as one raw buffer (layers of 4 GiB and more are declined on the host)
+    const uint64_t trel_bytes = (uint64_t) a.k * a.n * BITS / 8;
+    const __amdgpu_buffer_rsrc_t trsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(trel), 0, (int) (uint32_t) trel_bytes, RAW_BUFFER_FLAGS);
     gc_u16* const gsuh = as_global(suh);
     gc_u16* const gsvh = as_global(svh);
     gc_u16* const gx = as_global(a.x);
     g_u16* const gy = as_global(y);
-    uint16_t* lds_a = smem;                                   // [chunk_units][M][A_ROW]
-    uint16_t* lds_c = smem + a.chunk_units * M * A_ROW;       // [M][A_ROW] fp16 C of one block
-    uint16_t* lds_zero = lds_c + M * A_ROW;                   // one zero row: A operand of rows >= M
+    // LDS: the rotated input of a chunk of units, M rows per unit followed by one zero row (the A
+    // operand of MFMA rows >= M), then the fp16 C of one block for the output transform
+    const int UROWS = M + 1;
+    uint16_t* lds_a = smem;                                   // [chunk_units][M + 1][A_ROW]
+    uint16_t* lds_c = smem + a.chunk_units * UROWS * A_ROW;   // [M][A_ROW]
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int g = lane >> 4, j = lane & 15, q = j & 7;
     const int ulo = wg_lo(w, U, G), uhi = wg_lo(w + 1, U, G);
@@ -201,17 +221,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))
     const int seg0_cb = ulo / UPB;
     float* part_grp = a.part + (int64_t) grp * G * a.max_seg * M * 128;
 
-    // step d (0, 1) of unit (cb, ku) for this lane: a per-lane base plus a uniform offset
-    gc_u32* lane_base = gtrel + ((int64_t) g * NT + wave * 2 + (j >> 3)) * (8 * BITS);
-    auto tile_at = [&](int cb, int ku, int d) -> gc_u32* {
-        return lane_base + ((int64_t) (2 * ku + d) * 4 * NT + cb * 8) * (8 * BITS);
-    };
-    auto tile_of = [&](int u, int d) -> gc_u32* {
-        const int cb = u / UPB;
-        return tile_at(cb, u - cb * UPB, d);
-    };
+    // Trellis addressing.  Step d (0, 1) of unit (cb, ku) covers k-tiles 8ku + 4d .. +3 and n-tiles
+    // 8cb .. 8cb + 7; this lane reads q-block q of tile (k-tile + g, n-tile 8cb + 2 wave + (j >> 3)).
+    // A uniform byte offset walks the units; the lane adds fixed byte offsets.
+    const int tile_lane = (g * NT + wave * 2 + (j >> 3)) * (8 * BITS);            // words
+    const uint32_t off_main = (uint32_t) (tile_lane + q * BITS) * 4u;
+    const uint32_t off_prev = (uint32_t) (tile_lane + (q == 0 ? 8 * BITS - 1 : q * BITS - 1)) * 4u;
+    const uint32_t STEP_D = (uint32_t) (4 * NT * 8 * BITS * 4);   // bytes from step 0 to step 1 of a unit
+    const uint32_t STEP_KU = 2 * STEP_D;                          // to the next unit of the same block
+    const uint32_t STEP_CB = 8 * 8 * BITS * 4;                    // to the next block, same ku
+    const uint32_t STEP_WRAP = STEP_CB - (uint32_t) (UPB - 1) * STEP_KU;   // to ku 0 of the next block (mod 2^32)
+
     // rotated-input job i of a chunk starting at unit u0: (unit u0 + i / M, row i % M), 16 lanes each
-    auto job_src = [&](int u0, int i, int& m, int& col) {
+    auto job_src = [&](int u0, int i, int& m, int& col) __attribute__((always_inline)) {
         const int u = u0 + i / M;
         m = i - (i / M) * M;
         col = (u - (u / UPB) * UPB) * 128 + 8 * (threadIdx.x & 15);
@@ -233,46 +255,80 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))
             ps = *reinterpret_cast<gc_u32x4*>(gsuh + col);
         }
     }
-    uint32_t W0[BITS + 1], W1[BITS + 1];
-    load_qblock<BITS>(tile_of(ulo, 0), q, W0);
-    load_qblock<BITS>(tile_of(ulo, 1), q, W1);
-    if (wave * 4 < nfirst) {                                  // waves without a job skip the transform
-        const int i = threadIdx.x >> 4;                       // whole 16-lane groups take part
-        const u32x4 r = had128_x8(px, ps, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
-        if (i < nfirst) {
-            int m, col;
-            job_src(ulo, i, m, col);
-            *reinterpret_cast<u32x4*>(lds_a + ((i / M) * M + m) * A_ROW + 8 * (threadIdx.x & 15)) = r;
+    // ---- the trellis ring: RING steps in flight per wave ----------------------------------------
+    // Slot i always holds a step with d == i & 1.  The load cursor (ul, ku_l, lp) is the unit of the
+    // next refill; it stops at the last unit, whose steps are reloaded (in bounds, never used).
+    uint32_t Wr[RING][BITS + 1];
+    int ul = ulo, ku_l = ulo - seg0_cb * UPB;
+    uint32_t lp = (uint32_t) seg0_cb * STEP_CB + (uint32_t) ku_l * STEP_KU;
+    auto advance_load = [&]() __attribute__((always_inline)) {
+        if (ul + 1 < uhi) {
+            ++ul;
+            if (++ku_l == UPB) {
+                ku_l = 0;
+                lp += STEP_WRAP;
+            } else {
+                lp += STEP_KU;
+            }
         }
-        for (int i2 = i + 16; i2 < nfirst; i2 += 16) {
-            int m, col;
-            job_src(ulo, i2, m, col);
-            const u32x4 xv = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
-            const u32x4 sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
-            *reinterpret_cast<u32x4*>(lds_a + ((i2 / M) * M + m) * A_ROW + 8 * (threadIdx.x & 15)) =
-                had128_x8(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
+    };
+    static_for(std::make_integer_sequence<int, RING>{}, [&](auto I) __attribute__((always_inline)) {
+        constexpr int i = decltype(I)::value;
+        load_qblock_buf<BITS>(trsrc, off_main, off_prev, lp + (i & 1) * STEP_D, Wr[i]);
+        if (i & 1) advance_load();
+    });
+    // rotated input of units [c0, c1) -> LDS; the first 16-lane job of each lane uses (x0, s0)
+    auto rotate_chunk = [&](int c0, int c1, u32x4 x0, u32x4 s0, bool have_first) __attribute__((always_inline)) {
+        const int njobs = (c1 - c0) * M;
+        const int i = threadIdx.x >> 4;
+        if (i - (threadIdx.x & 63) / 16 < njobs) {            // waves with a job (whole 16-lane groups)
+            if (!have_first && i < njobs) {
+                int m, col;
+                job_src(c0, i, m, col);
+                x0 = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
+                s0 = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+            }
+            const u32x4 r = had128_x8(x0, s0, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
+            if (i < njobs) {
+                int m, col;
+                job_src(c0, i, m, col);
+                *reinterpret_cast<u32x4*>(lds_a + ((i / M) * UROWS + m) * A_ROW + 8 * (threadIdx.x & 15)) = r;
+            }
+            for (int i2 = i + 16; i2 - (threadIdx.x & 63) / 16 < njobs; i2 += 16) {
+                u32x4 xv = {0u, 0u, 0u, 0u}, sv = xv;
+                int m = 0, col = 0;
+                if (i2 < njobs) {
+                    job_src(c0, i2, m, col);
+                    xv = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
+                    sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+                }
+                const u32x4 r2 = had128_x8(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
+                if (i2 < njobs)
+                    *reinterpret_cast<u32x4*>(lds_a + ((i2 / M) * UROWS + m) * A_ROW + 8 * (threadIdx.x & 15)) = r2;
+            }
         }
-    }
-    if (threadIdx.x < A_ROW / 8) *reinterpret_cast<u32x4*>(lds_zero + 8 * threadIdx.x) = u32x4{0u, 0u, 0u, 0u};
+    };
+    int c0 = ulo, c1 = min(ulo + a.chunk_units, uhi);
+    rotate_chunk(c0, c1, px, ps, true);
+    // zero rows: never overwritten by later chunks
+    for (int t = threadIdx.x; t < a.chunk_units * (A_ROW / 8); t += 256)
+        *reinterpret_cast<u32x4*>(lds_a + ((t / (A_ROW / 8)) * UROWS + M) * A_ROW + 8 * (t % (A_ROW / 8))) =
+            u32x4{0u, 0u, 0u, 0u};
     __syncthreads();
 
-    // A operand rows of this lane: rows >= M read the zero row, so the step has no branches
-    int a_row[MT];
-    bool a_live[MT];
+    // A operand row of this lane (per MFMA row tile) within a unit: rows >= M read the zero row
+    int a_lane[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-        a_live[mt] = mt * 16 + j < M;
-        a_row[mt] = a_live[mt] ? (mt * 16 + j) * A_ROW : (int) (lds_zero - lds_a);
-    }
+    for (int mt = 0; mt < MT; ++mt) a_lane[mt] = (mt * 16 + j < M ? mt * 16 + j : M) * A_ROW + 16 * g;
 
-    f32x4 acc[2][MT], pacc[2][MT];
+    f32x4 acc[2][MT];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[h][mt] = pacc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < MT; ++mt) acc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     const int colb = wave * 32 + (j >> 3) * 16 + (j & 7);    // + 8h: column of this lane in the block
-    auto write_partial = [&](const f32x4 (&ac)[2][MT], int cb) {
+    auto write_partial = [&](int cb) __attribute__((always_inline)) {
         float* slab = part_grp + ((int64_t) w * a.max_seg + (cb - seg0_cb)) * M * 128;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
@@ -282,35 +338,106 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))
                 for (int v = 0; v < 4; ++v) {
                     const int m = mt * 16 + 4 * g + v;
                     if (m < M)
-                        __hip_atomic_store(&slab[m * 128 + colb + 8 * h], ac[h][mt][v], __ATOMIC_RELAXED,
+                        __hip_atomic_store(&slab[m * 128 + colb + 8 * h], acc[h][mt][v], __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
                 }
     };
 
-    // Partials of blocks cb_a (if >= 0) and cb_b are written: count this workgroup in and
-    // reduce every block it completed.  Uniform control flow (every thread calls it).
-    auto complete = [&](int cb_a, int cb_b) {
-        // The partials are device-scope (write-through) stores: once complete (vmcnt(0)) they
-        // are visible to device-scope loads from any XCD, so no cache-wide release is needed.
-        wait_stores_complete();
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            int last = 0;
-            for (int i = 0; i < 2; ++i) {
-                const int cb = i == 0 ? cb_a : cb_b;
-                if (cb < 0) continue;
-                const int wf = wg_of_unit(cb * UPB, U, G), wl = wg_of_unit(cb * UPB + UPB - 1, U, G);
-                const uint32_t prev = __hip_atomic_fetch_add(&a.counters[grp * NB + cb], 1u, __ATOMIC_RELAXED,
-                                                             __HIP_MEMORY_SCOPE_AGENT);
-                if (prev == (uint32_t) (wl - wf)) last |= 1 << i;
+    // one k step: decode the slot's q-block, refill the slot from the load cursor (when the ring
+    // still has steps to fetch), two MFMAs per tile column half
+    auto step = [&](uint32_t (&Wq)[BITS + 1], const uint16_t* unit_a, int d, bool refill) __attribute__((always_inline)) {
+        uint32_t P[16];
+        decode_qblock<BITS, CB>(Wq, P);
+        if (refill) load_qblock_buf<BITS>(trsrc, off_main, off_prev, lp + d * STEP_D, Wq);
+        f16x8 A0[MT], A1[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const uint16_t* ap = unit_a + a_lane[mt] + 64 * d;
+            A0[mt] = *reinterpret_cast<const f16x8*>(ap);
+            A1[mt] = *reinterpret_cast<const f16x8*>(ap + 8);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const u32x4 B0 = {P[2 * h], P[4 + 2 * h], P[8 + 2 * h], P[12 + 2 * h]};
+            const u32x4 B1 = {P[2 * h + 1], P[5 + 2 * h], P[9 + 2 * h], P[13 + 2 * h]};
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                acc[h][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0[mt], __builtin_bit_cast(f16x8, B0), acc[h][mt], 0, 0, 0);
+                acc[h][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[mt], __builtin_bit_cast(f16x8, B1), acc[h][mt], 0, 0, 0);
             }
-            s_last = last;
+        }
+    };
+
+    int cb_cur = seg0_cb;
+    int left = UPB - (ulo - seg0_cb * UPB);                   // units of block cb_cur still to come
+    // sub-step i of the ring turn starting at unit u0 (slot i, d = i & 1)
+    auto sub_step = [&](auto I, int u0, bool refill) __attribute__((always_inline)) {
+        constexpr int i = decltype(I)::value;
+        if (!(i & 1)) {
+            if (left == 0) {                                  // a new 128-column block starts
+                write_partial(cb_cur);
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                ++cb_cur;
+                left = UPB;
+            }
+            --left;
+        }
+        step(Wr[i], lds_a + (u0 + i / 2 - c0) * UROWS * A_ROW, i & 1, refill);
+        if ((i & 1) && refill) advance_load();
+    };
+    auto next_chunk = [&](int u0) __attribute__((always_inline)) {      // chunks hold whole ring turns
+        if (u0 == c1) {
+            c0 = c1;
+            c1 = min(c0 + a.chunk_units, uhi);
+            __syncthreads();
+            rotate_chunk(c0, c1, px, ps, false);
+            __syncthreads();
+        }
+    };
+
+    __builtin_amdgcn_s_setprio(0);
+    // Full ring turns run without per-step conditions (a conditional step would make the compiler
+    // wait for every load in flight); the last, partial turn only drains the ring.
+    const int S = 2 * (uhi - ulo);                            // 64-row k steps of this workgroup
+    const int S_full = S - S % RING;
+    int s0 = 0;
+    for (; s0 < S_full; s0 += RING) {
+        const int u0 = ulo + s0 / 2;
+        next_chunk(u0);
+        static_for(std::make_integer_sequence<int, RING>{}, [&](auto I) __attribute__((always_inline)) { sub_step(I, u0, true); });
+    }
+    if (s0 < S) {
+        const int u0 = ulo + s0 / 2;
+        next_chunk(u0);
+        static_for(std::make_integer_sequence<int, RING>{}, [&](auto I) __attribute__((always_inline)) {
+            if (s0 + decltype(I)::value < S) sub_step(I, u0, false);
+        });
+    }
+    __builtin_amdgcn_s_setprio(2);
+    write_partial(cb_cur);
+
+    // ---- completion: count this workgroup into every block it touched, reduce those it completed
+    // The partials are device-scope (write-through) stores: once complete (vmcnt(0)) they are
+    // visible to device-scope loads from any XCD, so no cache-wide release is needed.
+    wait_stores_complete();
+    __syncthreads();
+    const int nblk = cb_cur - seg0_cb + 1;
+    for (int b0 = 0; b0 < nblk; b0 += 256) {
+        const int nb = min(256, nblk - b0);
+        if ((int) threadIdx.x < nb) {                         // one counter per thread, all in flight
+            const int cb = seg0_cb + b0 + threadIdx.x;
+            const int wf = wg_of_unit(cb * UPB, U, G), wl = wg_of_unit(cb * UPB + UPB - 1, U, G);
+            const uint32_t prev = __hip_atomic_fetch_add(&a.counters[grp * NB + cb], 1u, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+            s_last[threadIdx.x] = prev == (uint32_t) (wl - wf) ? 1 : 0;
         }
         __syncthreads();
-        const int last = s_last;
-        for (int i = 0; i < 2; ++i) {
-            if (!(last & (1 << i))) continue;
-            const int cb = i == 0 ? cb_a : cb_b;
+        for (int bi = 0; bi < nb; ++bi) {
+            if (!__builtin_amdgcn_readfirstlane(s_last[bi])) continue;
+            const int cb = seg0_cb + b0 + bi;
             // contributor wf holds block cb in its segment cb - first_cb(wf); every later
             // contributor starts inside cb, so its segment is 0.  Loads go out in batches of
             // RED_BATCH; the sum runs in contributor order.
@@ -319,11 +446,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))
             const int nc = wl - wf + 1;
             for (int e = threadIdx.x; e < M * 128; e += 256) {
                 float sum = 0.f;
-                for (int c0 = 0; c0 < nc; c0 += RED_BATCH) {
+                for (int cc0 = 0; cc0 < nc; cc0 += RED_BATCH) {
                     float v[RED_BATCH];
 #pragma unroll
                     for (int ii = 0; ii < RED_BATCH; ++ii) {
-                        const int c = c0 + ii;
+                        const int c = cc0 + ii;
                         const int64_t slot = c == 0 ? (int64_t) wf * a.max_seg + seg_f : (int64_t) (wf + c) * a.max_seg;
                         v[ii] = c < nc ? __hip_atomic_load(part_grp + slot * M * 128 + e, __ATOMIC_RELAXED,
                                                            __HIP_MEMORY_SCOPE_AGENT)
@@ -331,7 +458,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))
                     }
 #pragma unroll
                     for (int ii = 0; ii < RED_BATCH; ++ii)
-                        if (c0 + ii < nc) sum += v[ii];
+                        if (cc0 + ii < nc) sum += v[ii];
                 }
                 lds_c[(e >> 7) * A_ROW + (e & 127)] = f16_bits((f16) sum);
             }
@@ -351,88 +478,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 4))
             }
             __syncthreads();                                   // lds_c free for the next block
         }
-    };
-
-    // one k step: decode the lane's q-block, refill the ring slot (the last unit reloads itself:
-    // in bounds and never used), two MFMAs per tile column half
-    auto step = [&](uint32_t (&Wr)[BITS + 1], int unit_off, int d, int cb_n, int ku_n) {
-        uint32_t P[16];
-        decode_qblock<BITS, CB>(Wr, P);
-        load_qblock<BITS>(tile_at(cb_n, ku_n, d), q, Wr);
-        f16x8 A0[MT], A1[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const uint16_t* ap = lds_a + (a_live[mt] ? unit_off : 0) + a_row[mt] + 64 * d + 16 * g;
-            A0[mt] = *reinterpret_cast<const f16x8*>(ap);
-            A1[mt] = *reinterpret_cast<const f16x8*>(ap + 8);
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const u32x4 B0 = {P[2 * h], P[4 + 2 * h], P[8 + 2 * h], P[12 + 2 * h]};
-            const u32x4 B1 = {P[2 * h + 1], P[5 + 2 * h], P[9 + 2 * h], P[13 + 2 * h]};
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                acc[h][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0[mt], __builtin_bit_cast(f16x8, B0), acc[h][mt], 0, 0, 0);
-                acc[h][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[mt], __builtin_bit_cast(f16x8, B1), acc[h][mt], 0, 0, 0);
-            }
-        }
-    };
-
-    __builtin_amdgcn_s_setprio(0);
-    int cb_cur = seg0_cb, cb_prev = -1;
-    // the unit being processed (cb_u, ku_u) and the next one, walked without divisions
-    int cb_u = seg0_cb, ku_u = ulo - seg0_cb * UPB;
-    for (int c0 = ulo; c0 < uhi; c0 += a.chunk_units) {
-        const int c1 = min(c0 + a.chunk_units, uhi);
-        if (c0 != ulo) {                                      // later chunks (large M x long ranges)
-            __syncthreads();
-            for (int i = threadIdx.x >> 4; i < (c1 - c0) * M; i += 16) {
-                int m, col;
-                job_src(c0, i, m, col);
-                const u32x4 xv = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
-                const u32x4 sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
-                *reinterpret_cast<u32x4*>(lds_a + ((i / M) * M + m) * A_ROW + 8 * (threadIdx.x & 15)) =
-                    had128_x8(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
-            }
-            __syncthreads();
-        }
-        for (int u = c0; u < c1; ++u) {
-            const int cb = cb_u;
-            int cb_n = cb_u, ku_n = ku_u + 1;
-            if (ku_n == UPB) {
-                ku_n = 0;
-                ++cb_n;
-            }
-            if (u + 1 >= uhi) {                               // the last unit reloads itself
-                cb_n = cb_u;
-                ku_n = ku_u;
-            }
-            if (cb != cb_cur) {
-                if (cb_prev >= 0) {                           // a third block: settle the oldest now
-                    write_partial(pacc, cb_prev);
-                    complete(-1, cb_prev);
-                }
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) {
-                        pacc[h][mt] = acc[h][mt];
-                        acc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    }
-                cb_prev = cb_cur;
-                cb_cur = cb;
-            }
-            const int unit_off = (u - c0) * M * A_ROW;
-            step(W0, unit_off, 0, cb_n, ku_n);
-            step(W1, unit_off, 1, cb_n, ku_n);
-            cb_u = cb_n;
-            ku_u = ku_n;
-        }
+        __syncthreads();                                       // s_last free for the next batch
     }
-    __builtin_amdgcn_s_setprio(2);
-    if (cb_prev >= 0) write_partial(pacc, cb_prev);
-    write_partial(acc, cb_cur);
-    complete(cb_prev, cb_cur);
 }
 
 // ============================================================================================
@@ -452,7 +499,7 @@ int codebook_of(int mcg, int mul1) { return mul1 ? 2 : (mcg ? 1 : 0); }
 // of an m-row call is bitwise equal to the m == 1 call, and a module's grouped launches agree
 // across row counts.  All workgroups of a launch are resident at once (4 per CU at the kernel's
 // register budget), each with at least two 64-row k steps.
-constexpr int RESIDENT_WGS = 768;      // 256 CUs x 3 (measured best of 256..1024 for the 5120 / 17408 layers)
+constexpr int RESIDENT_WGS = 256 * WAVES_PER_SIMD;   // 256 CUs x workgroups per CU
 
 int choose_grid(int k, int n, int groups)
 {
@@ -477,11 +524,12 @@ int chunk_units(int m, int k, int n, int G)
 {
     const int64_t U = (int64_t) (n / 128) * (k / 128);
     const int64_t per = (U + G - 1) / G;
-    const int64_t fit = std::max<int64_t>(1, (LDS_BUDGET / (2 * A_ROW) - m) / m);
+    // a chunk that is not the last one holds whole ring turns (RING / 2 units)
+    const int64_t fit = std::max<int64_t>(RING / 2, ((LDS_BUDGET / (2 * A_ROW) - m) / (m + 1)) / (RING / 2) * (RING / 2));
     return (int) std::max<int64_t>(1, std::min(per, fit));
 }
 
-size_t lds_bytes(int M, int cu) { return ((size_t) (cu + 1) * M + 1) * A_ROW * 2; }
+size_t lds_bytes(int M, int cu) { return ((size_t) cu * (M + 1) + M) * A_ROW * 2; }
 
 template <int BITS, int CB, int MT>
 int launch_gemv_t(const GemvArgs& a, int groups, hipStream_t stream)
@@ -553,6 +601,7 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, int groups, con
     }
     if (groups > 1 && !tabs && m > 1 && ldy < (int64_t) groups * n) return EXL3_EINVAL;
     if (!shape_ok(m, k, n, K)) return EXL3_DECLINED;
+    if ((uint64_t) k * n * K / 8 > 0xFFFFFFFFull) return EXL3_DECLINED;   // one raw buffer per trellis
     if ((size_t) groups * (n / 128) * 4 > COUNTER_BYTES) return EXL3_DECLINED;
     if (ws_bytes < gemv_ws_bytes(m, k, n, groups) || !ws) return EXL3_EWORKSPACE;
     GemvArgs a{};

@@ -41,8 +41,8 @@ def test_loader_and_abi_version():
 
 def test_grid_choice_depends_only_on_shape():
     L = _lib.lib()
-    assert L.exl3_gemv_grid(5120, 5120, 1) == 768           # 40 blocks x 40 units, all resident
-    assert L.exl3_gemv_grid(5120, 17408, 2) == 384           # two groups share the resident slots
+    assert L.exl3_gemv_grid(5120, 5120, 1) == 512           # 40 blocks x 40 units, all resident
+    assert L.exl3_gemv_grid(5120, 17408, 2) == 256           # two groups share the resident slots
     assert L.exl3_gemv_grid(5120, 1024, 1) == 160            # 320 units, <= 32 workgroups per block
     assert L.exl3_gemv_grid(256, 128, 1) == 2
     assert L.exl3_gemv_grid(5000, 128, 1) == 0
@@ -53,7 +53,7 @@ def test_workspace_sizes():
     ws1 = L.exl3_gemv_workspace_size(1, 5120, 5120, 4, 1)
     ws16 = L.exl3_gemv_workspace_size(16, 5120, 5120, 4, 1)
     ws2g = L.exl3_gemv_workspace_size(1, 5120, 5120, 4, 2)
-    assert ws1 >= 65536 + 768 * 2 * 128 * 4 and ws16 > ws1 and ws2g >= ws1
+    assert ws1 >= 65536 + 512 * 2 * 128 * 4 and ws16 > ws1 and ws2g >= ws1
     assert L.exl3_gemv_workspace_size(33, 5120, 5120, 4, 1) == 0        # beyond the GEMV row limit
     assert L.exl3_gemv_workspace_size(1, 5000, 5120, 4, 1) == 0         # k not a multiple of 128
 
