@@ -76,7 +76,7 @@ class LayerSet:
 
 
 def launches_per_step():
-    return 3 + 1 + 1 + 1      # q, k, v (differing widths) + o + gate/up grouped + down
+    return 1 + 1 + 1 + 1      # q/k/v grouped (mixed widths) + o + gate/up grouped + down
 
 
 def build_layers(torch, bits, copies, mul1=True, tag="config1"):

@@ -109,6 +109,19 @@ int exl3_gemv_mr_grouped(const void* x, int64_t ldx, const void* const* trellis,
                          const void* const* suh, void* A_had, const void* const* svh, int groups, int m, int k, int n,
                          int K, int mcg, int mul1, int bszm_for_warps, void* workspace, size_t ws_bytes, void* stream);
 
+/* Up to 4 groups sharing x and K but of any widths (q / k / v projections): group i writes the
+ * widths[i] columns of y that follow groups 0 .. i-1; rows ldy apart (ldy >= sum of widths).
+ * No counterpart in the reference: its linear_groups launches unequal widths one by one
+ * (reference ops.py:157-169).  Callers: exl3rocm's linear_groups for mixed-width runs.  The
+ * groups share one stream-K grid, so a module pays one launch, prologue and completion. */
+int exl3_gemv_mr_grouped_widths(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
+                                const void* const* suh, const void* const* svh, const int* widths, int groups, int m,
+                                int k, int K, int mcg, int mul1, void* workspace, size_t ws_bytes, void* stream);
+
+/* Workspace bytes exl3_gemv_mr_grouped_widths needs (0 for an ineligible shape).  No reference
+ * counterpart, as exl3_gemv_workspace_size. */
+size_t exl3_gemv_workspace_size_widths(int m, int k, const int* widths, int groups);
+
 /* Grouped M == 1 linear over device int64 pointer tables (one entry per group), output
  * (groups, 1, n) == the concatenated row.
  * Replaces `exl3_mgemm(x, ptrs_trellis, y, ptrs_suh, xh, ptrs_svh, ...)` (reference ops.py:137-138). */

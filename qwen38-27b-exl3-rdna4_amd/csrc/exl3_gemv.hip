@@ -135,22 +135,26 @@ struct GemvGroup {
     const uint16_t* suh;
     const uint16_t* svh;
     uint16_t* y;               // output columns of this group (row stride ldy)
+    int n;                     // width (columns)
+    int G;                     // workgroups of this group
+    int wg0;                   // its first workgroup in the flattened grid
+    int max_seg;               // partial slots per workgroup
+    int64_t part_off;          // first partial (floats) of this group
+    int cnt_off;               // first completion counter of this group
 };
 
 struct GemvArgs {
     const uint16_t* x;         // [M][ldx] fp16
     int64_t ldx;
     GemvGroup g[EXL3_MAX_GROUPS];
-    const int64_t* tab_trellis; // optional device pointer tables (grouped M=1 `mgemm` form)
-    const int64_t* tab_suh;
+    const int64_t* tab_trellis; // optional device pointer tables (grouped M=1 `mgemm` form): they
+    const int64_t* tab_suh;     // replace g[i].trellis / suh / svh
     const int64_t* tab_svh;
-    int64_t group_col_stride;  // with tables: group i writes y + i * group_col_stride
-    int M, k, n;
-    int G, U, UPB, max_seg;    // grid, units, units per block, partial slots per workgroup
+    int groups, M, k, UPB;
     int chunk_units;           // units whose rotated input fits the LDS at once
     int64_t ldy;
-    float* part;               // [groups][G][max_seg][M][128] fp32 partials
-    uint32_t* counters;        // [groups][NB], zero between calls
+    float* part;               // per group: [G][max_seg][M][128] fp32 partials
+    uint32_t* counters;        // per group: [n / 128], zero between calls
 };
 
 constexpr int RED_BATCH = 16;                   // partial loads in flight per thread in the reduction
@@ -180,29 +184,31 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
 {
     extern __shared__ __align__(16) uint16_t smem[];
     __shared__ int s_last[256];
-    const int w = blockIdx.x, grp = blockIdx.y;
-    const int G = a.G, U = a.U, UPB = a.UPB, M = a.M;
-    const int NB = a.n / 128, NT = a.n / 16;
-    const uint32_t* trel;
-    const uint16_t* suh;
-    const uint16_t* svh;
-    uint16_t* y;
+    __shared__ int s_list[256];
+    __shared__ int s_nred;
+    // the group of this workgroup: a flattened grid, each group its own range of workgroups
+    int grp = 0;
+    if (a.groups > 1 && (int) blockIdx.x >= a.g[1].wg0) grp = 1;
+    if (a.groups > 2 && (int) blockIdx.x >= a.g[2].wg0) grp = 2;
+    if (a.groups > 3 && (int) blockIdx.x >= a.g[3].wg0) grp = 3;
+    // constant indices only: a runtime index into the kernel-argument struct would copy it to
+    // scratch memory, and every later read of it would be a vector-memory load
+    const GemvGroup gg = grp == 0 ? a.g[0] : grp == 1 ? a.g[1] : grp == 2 ? a.g[2] : a.g[3];
+    const int w = blockIdx.x - gg.wg0;
+    const int G = gg.G, UPB = a.UPB, M = a.M;
+    const int NB = gg.n / 128, NT = gg.n / 16, U = NB * UPB;
+    const uint32_t* trel = gg.trellis;
+    const uint16_t* suh = gg.suh;
+    const uint16_t* svh = gg.svh;
+    uint16_t* y = gg.y;
     if (a.tab_trellis) {
         trel = reinterpret_cast<const uint32_t*>(a.tab_trellis[grp]);
         suh = reinterpret_cast<const uint16_t*>(a.tab_suh[grp]);
         svh = reinterpret_cast<const uint16_t*>(a.tab_svh[grp]);
-        y = a.g[0].y + grp * a.group_col_stride;
-    } else {
-        // constant indices only: a runtime index into the kernel-argument struct would copy it to
-        // scratch memory, and every later read of it would be a vector-memory load
-        const GemvGroup gg = grp == 0 ? a.g[0] : grp == 1 ? a.g[1] : grp == 2 ? a.g[2] : a.g[3];
-        trel = gg.trellis;
-        suh = gg.suh;
-        svh = gg.svh;
-        y = gg.y;
     }
+    uint32_t* const counters = a.counters + gg.cnt_off;
     // the trellis as one raw buffer (layers of 4 GiB and more are declined on the host)
-    const uint64_t trel_bytes = (uint64_t) a.k * a.n * BITS / 8;
+    const uint64_t trel_bytes = (uint64_t) a.k * gg.n * BITS / 8;
     const __amdgpu_buffer_rsrc_t trsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(trel), 0, (int) (uint32_t) trel_bytes, RAW_BUFFER_FLAGS);
     gc_u16* const gsuh = as_global(suh);
@@ -219,7 +225,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     const int ulo = wg_lo(w, U, G), uhi = wg_lo(w + 1, U, G);
     if (ulo >= uhi) return;                                   // uniform per workgroup
     const int seg0_cb = ulo / UPB;
-    float* part_grp = a.part + (int64_t) grp * G * a.max_seg * M * 128;
+    float* part_grp = a.part + gg.part_off;
 
     // Trellis addressing.  Step d (0, 1) of unit (cb, ku) covers k-tiles 8ku + 4d .. +3 and n-tiles
     // 8cb .. 8cb + 7; this lane reads q-block q of tile (k-tile + g, n-tile 8cb + 2 wave + (j >> 3)).
@@ -329,7 +335,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
 
     const int colb = wave * 32 + (j >> 3) * 16 + (j & 7);    // + 8h: column of this lane in the block
     auto write_partial = [&](int cb) __attribute__((always_inline)) {
-        float* slab = part_grp + ((int64_t) w * a.max_seg + (cb - seg0_cb)) * M * 128;
+        float* slab = part_grp + ((int64_t) w * gg.max_seg + (cb - seg0_cb)) * M * 128;
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -425,34 +431,44 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     wait_stores_complete();
     __syncthreads();
     const int nblk = cb_cur - seg0_cb + 1;
+    const int RB = M == 1 ? 2 : 1;                            // completed blocks reduced side by side
     for (int b0 = 0; b0 < nblk; b0 += 256) {
         const int nb = min(256, nblk - b0);
         if ((int) threadIdx.x < nb) {                         // one counter per thread, all in flight
             const int cb = seg0_cb + b0 + threadIdx.x;
             const int wf = wg_of_unit(cb * UPB, U, G), wl = wg_of_unit(cb * UPB + UPB - 1, U, G);
-            const uint32_t prev = __hip_atomic_fetch_add(&a.counters[grp * NB + cb], 1u, __ATOMIC_RELAXED,
+            const uint32_t prev = __hip_atomic_fetch_add(&counters[cb], 1u, __ATOMIC_RELAXED,
                                                          __HIP_MEMORY_SCOPE_AGENT);
             s_last[threadIdx.x] = prev == (uint32_t) (wl - wf) ? 1 : 0;
         }
         __syncthreads();
-        for (int bi = 0; bi < nb; ++bi) {
-            if (!__builtin_amdgcn_readfirstlane(s_last[bi])) continue;
-            const int cb = seg0_cb + b0 + bi;
+        if (threadIdx.x == 0) {
+            int c = 0;
+            for (int bi = 0; bi < nb; ++bi)
+                if (s_last[bi]) s_list[c++] = seg0_cb + b0 + bi;
+            s_nred = c;
+        }
+        __syncthreads();
+        const int nred = __builtin_amdgcn_readfirstlane(s_nred);
+        for (int r0 = 0; r0 < nred; r0 += RB) {
+            const int rb = min(RB, nred - r0);
             // contributor wf holds block cb in its segment cb - first_cb(wf); every later
             // contributor starts inside cb, so its segment is 0.  Loads go out in batches of
             // RED_BATCH; the sum runs in contributor order.
-            const int wf = wg_of_unit(cb * UPB, U, G), wl = wg_of_unit(cb * UPB + UPB - 1, U, G);
-            const int seg_f = cb - wg_lo(wf, U, G) / UPB;
-            const int nc = wl - wf + 1;
-            for (int e = threadIdx.x; e < M * 128; e += 256) {
+            for (int e = threadIdx.x; e < rb * M * 128; e += 256) {
+                const int r = e / (M * 128), el = e - r * (M * 128);
+                const int cb = s_list[r0 + r];
+                const int wf = wg_of_unit(cb * UPB, U, G), wl = wg_of_unit(cb * UPB + UPB - 1, U, G);
+                const int seg_f = cb - wg_lo(wf, U, G) / UPB;
+                const int nc = wl - wf + 1;
                 float sum = 0.f;
                 for (int cc0 = 0; cc0 < nc; cc0 += RED_BATCH) {
                     float v[RED_BATCH];
 #pragma unroll
                     for (int ii = 0; ii < RED_BATCH; ++ii) {
                         const int c = cc0 + ii;
-                        const int64_t slot = c == 0 ? (int64_t) wf * a.max_seg + seg_f : (int64_t) (wf + c) * a.max_seg;
-                        v[ii] = c < nc ? __hip_atomic_load(part_grp + slot * M * 128 + e, __ATOMIC_RELAXED,
+                        const int64_t slot = c == 0 ? (int64_t) wf * gg.max_seg + seg_f : (int64_t) (wf + c) * gg.max_seg;
+                        v[ii] = c < nc ? __hip_atomic_load(part_grp + slot * M * 128 + el, __ATOMIC_RELAXED,
                                                            __HIP_MEMORY_SCOPE_AGENT)
                                        : 0.f;
                     }
@@ -460,25 +476,29 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                     for (int ii = 0; ii < RED_BATCH; ++ii)
                         if (cc0 + ii < nc) sum += v[ii];
                 }
-                lds_c[(e >> 7) * A_ROW + (e & 127)] = f16_bits((f16) sum);
+                lds_c[(r * M + (el >> 7)) * A_ROW + (el & 127)] = f16_bits((f16) sum);
             }
-            if (threadIdx.x == 0)                              // ready for the next call (stream order)
-                __hip_atomic_store(&a.counters[grp * NB + cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((int) threadIdx.x < rb)                        // ready for the next call (stream order)
+                __hip_atomic_store(&counters[s_list[r0 + threadIdx.x]], 0u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
             __syncthreads();
-            // output Hadamard + svh: 16 lanes per row
-            const int rr = threadIdx.x & 15;
-            const u32x4 sv = *reinterpret_cast<gc_u32x4*>(gsvh + cb * 128 + 8 * rr);
-            for (int m0 = 0; m0 < M; m0 += 16) {
-                const int m = m0 + (threadIdx.x >> 4);
-                const bool live = m < M;
-                u32x4 c = {0u, 0u, 0u, 0u};
-                if (live) c = *reinterpret_cast<const u32x4*>(lds_c + m * A_ROW + 8 * rr);
-                const u32x4 r = had128_x8(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, R_SCALE);
-                if (live) *reinterpret_cast<g_u32x4*>(gy + (int64_t) m * a.ldy + cb * 128 + 8 * rr) = r;
+            // output Hadamard + svh: 16 lanes per (block, row)
+            const int l16 = threadIdx.x & 15;
+            for (int rr0 = 0; rr0 < rb * M; rr0 += 16) {
+                const int rr = rr0 + (threadIdx.x >> 4);
+                const bool live = rr < rb * M;
+                const int r = live ? rr / M : 0, m = live ? rr - r * M : 0;
+                const int cb = s_list[r0 + r];
+                u32x4 c = {0u, 0u, 0u, 0u}, sv = c;
+                if (live) {
+                    c = *reinterpret_cast<const u32x4*>(lds_c + rr * A_ROW + 8 * l16);
+                    sv = *reinterpret_cast<gc_u32x4*>(gsvh + cb * 128 + 8 * l16);
+                }
+                const u32x4 res = had128_x8(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, R_SCALE);
+                if (live) *reinterpret_cast<g_u32x4*>(gy + (int64_t) m * a.ldy + cb * 128 + 8 * l16) = res;
             }
-            __syncthreads();                                   // lds_c free for the next block
+            __syncthreads();                                   // lds_c free for the next blocks
         }
-        __syncthreads();                                       // s_last free for the next batch
     }
 }
 
@@ -495,89 +515,119 @@ int env_int(const char* name, int dflt)
 
 int codebook_of(int mcg, int mul1) { return mul1 ? 2 : (mcg ? 1 : 0); }
 
-// Stream-K grid: workgroups per group, from (k, n, groups) only -- never from m -- so every row
-// of an m-row call is bitwise equal to the m == 1 call, and a module's grouped launches agree
-// across row counts.  All workgroups of a launch are resident at once (4 per CU at the kernel's
-// register budget), each with at least two 64-row k steps.
+// Stream-K grid plan of one launch: workgroups per group from (k, widths) only -- never from m --
+// so every row of an m-row call is bitwise equal to the m == 1 call, and a module's grouped
+// launches agree across row counts.  The groups share the resident workgroup slots in proportion
+// to their units; each keeps its own workgroup range, partial slots and completion counters.
 constexpr int RESIDENT_WGS = 256 * WAVES_PER_SIMD;   // 256 CUs x workgroups per CU
 
-int choose_grid(int k, int n, int groups)
-{
-    const int64_t UPB = k / 128, U = (int64_t) (n / 128) * UPB;
-    const int forced = env_int("EXL3_GEMV_GRID", 0);
-    // all workgroups resident; at most ~max_contrib workgroups sharing one block
-    const int max_contrib = env_int("EXL3_GEMV_MAX_CONTRIB", 32);
-    const int64_t min_units = std::max<int64_t>(1, (UPB + max_contrib - 1) / max_contrib);
-    int64_t G = forced > 0 ? forced : std::min<int64_t>(RESIDENT_WGS / std::max(groups, 1), U / min_units);
-    return (int) std::max<int64_t>(1, std::min<int64_t>(G, U));
-}
+struct GridPlan {
+    int groups;
+    int G[EXL3_MAX_GROUPS], wg0[EXL3_MAX_GROUPS], max_seg[EXL3_MAX_GROUPS], cnt_off[EXL3_MAX_GROUPS];
+    int64_t slot_off[EXL3_MAX_GROUPS];   // first partial slot (one slot = m * 128 floats)
+    int total_wgs, counters;
+    int64_t slots;
+    int max_per;                         // most units any workgroup owns
+};
 
-int max_segments(int k, int n, int G)
+int max_segments(int UPB, int n, int G)
 {
-    const int64_t UPB = k / 128, U = (int64_t) (n / 128) * UPB;
+    const int64_t U = (int64_t) (n / 128) * UPB;
     const int64_t per = (U + G - 1) / G;
     return (int) ((per + UPB - 1) / UPB + 1);
 }
 
-// units whose rotated input a workgroup stages at once (all of them when they fit)
-int chunk_units(int m, int k, int n, int G)
+GridPlan plan_grid(int k, const int* widths, int groups)
 {
-    const int64_t U = (int64_t) (n / 128) * (k / 128);
-    const int64_t per = (U + G - 1) / G;
-    // a chunk that is not the last one holds whole ring turns (RING / 2 units)
-    const int64_t fit = std::max<int64_t>(RING / 2, ((LDS_BUDGET / (2 * A_ROW) - m) / (m + 1)) / (RING / 2) * (RING / 2));
-    return (int) std::max<int64_t>(1, std::min(per, fit));
+    GridPlan p{};
+    p.groups = groups;
+    const int UPB = k / 128;
+    int64_t Utot = 0;
+    for (int i = 0; i < groups; ++i) Utot += (int64_t) (widths[i] / 128) * UPB;
+    const int forced = env_int("EXL3_GEMV_GRID", 0);
+    // at most ~max_contrib workgroups sharing one block
+    const int max_contrib = env_int("EXL3_GEMV_MAX_CONTRIB", 32);
+    const int64_t min_units = std::max<int64_t>(1, (UPB + max_contrib - 1) / max_contrib);
+    int64_t Gt = forced > 0 ? (int64_t) forced * groups : std::min<int64_t>(RESIDENT_WGS, Utot / min_units);
+    Gt = std::max<int64_t>(Gt, groups);
+    int wg = 0, cnt = 0;
+    int64_t slots = 0;
+    for (int i = 0; i < groups; ++i) {
+        const int64_t Ui = (int64_t) (widths[i] / 128) * UPB;
+        const int64_t Gi = std::max<int64_t>(1, std::min<int64_t>(Ui, (Gt * Ui + Utot / 2) / Utot));
+        p.G[i] = (int) Gi;
+        p.wg0[i] = wg;
+        p.max_seg[i] = max_segments(UPB, widths[i], p.G[i]);
+        p.cnt_off[i] = cnt;
+        p.slot_off[i] = slots;
+        p.max_per = std::max<int>(p.max_per, (int) ((Ui + Gi - 1) / Gi));
+        wg += p.G[i];
+        cnt += widths[i] / 128;
+        slots += (int64_t) p.G[i] * p.max_seg[i];
+    }
+    p.total_wgs = wg;
+    p.counters = cnt;
+    p.slots = slots;
+    return p;
 }
 
-size_t lds_bytes(int M, int cu) { return ((size_t) cu * (M + 1) + M) * A_ROW * 2; }
+// units whose rotated input a workgroup stages at once (all of them when they fit); a chunk that
+// is not the last one holds whole ring turns (RING / 2 units)
+int chunk_units(int m, int max_per)
+{
+    const int64_t fit = std::max<int64_t>(RING / 2, ((LDS_BUDGET / (2 * A_ROW) - 2 * m) / (m + 1)) / (RING / 2) * (RING / 2));
+    return (int) std::max<int64_t>(1, std::min<int64_t>(max_per, fit));
+}
+
+// LDS: chunk_units x (m + 1) input rows, then the C rows of the blocks reduced side by side
+size_t lds_bytes(int M, int cu) { return ((size_t) cu * (M + 1) + (M == 1 ? 2 : M)) * A_ROW * 2; }
 
 template <int BITS, int CB, int MT>
-int launch_gemv_t(const GemvArgs& a, int groups, hipStream_t stream)
+int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t stream)
 {
-    hipLaunchKernelGGL((gemv_kernel<BITS, CB, MT>), dim3(a.G, groups), dim3(256), lds_bytes(a.M, a.chunk_units),
-                       stream, a);
+    hipLaunchKernelGGL((gemv_kernel<BITS, CB, MT>), dim3(wgs), dim3(256), lds_bytes(a.M, a.chunk_units), stream, a);
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 
 template <int BITS, int CB>
-int launch_gemv_m(const GemvArgs& a, int groups, hipStream_t s)
+int launch_gemv_m(const GemvArgs& a, int wgs, hipStream_t s)
 {
-    return a.M <= 16 ? launch_gemv_t<BITS, CB, 1>(a, groups, s) : launch_gemv_t<BITS, CB, 2>(a, groups, s);
+    return a.M <= 16 ? launch_gemv_t<BITS, CB, 1>(a, wgs, s) : launch_gemv_t<BITS, CB, 2>(a, wgs, s);
 }
 
 template <int BITS>
-int launch_gemv_cb(const GemvArgs& a, int cb, int groups, hipStream_t s)
+int launch_gemv_cb(const GemvArgs& a, int cb, int wgs, hipStream_t s)
 {
     switch (cb) {
-        case 0: return launch_gemv_m<BITS, 0>(a, groups, s);
-        case 1: return launch_gemv_m<BITS, 1>(a, groups, s);
-        default: return launch_gemv_m<BITS, 2>(a, groups, s);
+        case 0: return launch_gemv_m<BITS, 0>(a, wgs, s);
+        case 1: return launch_gemv_m<BITS, 1>(a, wgs, s);
+        default: return launch_gemv_m<BITS, 2>(a, wgs, s);
     }
 }
 
-int launch_gemv(const GemvArgs& a, int bits, int cb, int groups, hipStream_t s)
+int launch_gemv(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s)
 {
     switch (bits) {
-        case 1: return launch_gemv_cb<1>(a, cb, groups, s);
-        case 2: return launch_gemv_cb<2>(a, cb, groups, s);
-        case 3: return launch_gemv_cb<3>(a, cb, groups, s);
-        case 4: return launch_gemv_cb<4>(a, cb, groups, s);
-        case 5: return launch_gemv_cb<5>(a, cb, groups, s);
-        case 6: return launch_gemv_cb<6>(a, cb, groups, s);
-        case 7: return launch_gemv_cb<7>(a, cb, groups, s);
-        default: return launch_gemv_cb<8>(a, cb, groups, s);
+        case 1: return launch_gemv_cb<1>(a, cb, wgs, s);
+        case 2: return launch_gemv_cb<2>(a, cb, wgs, s);
+        case 3: return launch_gemv_cb<3>(a, cb, wgs, s);
+        case 4: return launch_gemv_cb<4>(a, cb, wgs, s);
+        case 5: return launch_gemv_cb<5>(a, cb, wgs, s);
+        case 6: return launch_gemv_cb<6>(a, cb, wgs, s);
+        case 7: return launch_gemv_cb<7>(a, cb, wgs, s);
+        default: return launch_gemv_cb<8>(a, cb, wgs, s);
     }
 }
 
-// workspace layout: [counters: fixed EXL3_GEMV_COUNTER_BYTES region][partials: groups*G*max_seg*M*128 f32].
+// workspace layout: [counters: fixed EXL3_GEMV_COUNTER_BYTES region][partials: slots * m * 128 f32].
 // The counter region has a fixed size so calls of different shapes sharing one workspace never
 // see another shape's partial sums where their counters live.
 constexpr size_t COUNTER_BYTES = EXL3_GEMV_COUNTER_BYTES;
 
-size_t gemv_ws_bytes(int m, int k, int n, int groups)
+size_t gemv_ws_bytes(int m, int k, const int* widths, int groups)
 {
-    const int G = choose_grid(k, n, groups);
-    return COUNTER_BYTES + (size_t) groups * G * max_segments(k, n, G) * m * 128 * 4;
+    const GridPlan p = plan_grid(k, widths, groups);
+    return COUNTER_BYTES + (size_t) p.slots * m * 128 * 4;
 }
 
 bool shape_ok(int m, int k, int n, int K)
@@ -585,48 +635,58 @@ bool shape_ok(int m, int k, int n, int K)
     return m >= 1 && m <= EXL3_GEMV_MAX_ROWS && k >= 128 && n >= 128 && k % 128 == 0 && n % 128 == 0 && K >= 1 && K <= 8;
 }
 
-int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, int groups, const int64_t* const* tabs,
-                int64_t col_stride, int64_t ldy, int m, int k, int n, int K, int mcg, int mul1, void* ws,
+// gs[i].y: group i's first output column (rows ldy apart); with pointer tables only gs[i].y is
+// read from gs, the table entries are the caller's contract
+int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widths, int groups,
+                const int64_t* const* tabs, int64_t ldy, int m, int k, int K, int mcg, int mul1, void* ws,
                 size_t ws_bytes, void* stream)
 {
-    if (!x || groups < 1 || groups > EXL3_MAX_GROUPS || ldx < k || ldy < n) return EXL3_EINVAL;
+    if (!x || groups < 1 || groups > EXL3_MAX_GROUPS || ldx < k) return EXL3_EINVAL;
     // the kernel moves fp16 in 16-byte groups of 8: x rows, y rows, suh and svh 16-byte aligned
     if ((ldx & 7) || (ldy & 7) || (((uintptr_t) x) & 15)) return EXL3_EINVAL;
-    // with pointer tables only gs[0].y is given; the table entries are the caller's contract
-    for (int i = 0; i < (tabs ? 1 : groups); ++i) {
+    int64_t total = 0;
+    for (int i = 0; i < groups; ++i) {
         if (!gs[i].y || (((uintptr_t) gs[i].y) & 15)) return EXL3_EINVAL;
-        if (!tabs && ((((uintptr_t) gs[i].suh) & 15) || (((uintptr_t) gs[i].svh) & 15) ||
-                      (((uintptr_t) gs[i].trellis) & 15)))
+        if (!tabs && (!gs[i].trellis || !gs[i].suh || !gs[i].svh || (((uintptr_t) gs[i].suh) & 15) ||
+                      (((uintptr_t) gs[i].svh) & 15) || (((uintptr_t) gs[i].trellis) & 15)))
             return EXL3_EINVAL;
+        if (widths[i] < 1) return EXL3_EINVAL;
+        total += widths[i];
     }
-    if (groups > 1 && !tabs && m > 1 && ldy < (int64_t) groups * n) return EXL3_EINVAL;
-    if (!shape_ok(m, k, n, K)) return EXL3_DECLINED;
-    if ((uint64_t) k * n * K / 8 > 0xFFFFFFFFull) return EXL3_DECLINED;   // one raw buffer per trellis
-    if ((size_t) groups * (n / 128) * 4 > COUNTER_BYTES) return EXL3_DECLINED;
-    if (ws_bytes < gemv_ws_bytes(m, k, n, groups) || !ws) return EXL3_EWORKSPACE;
+    if (ldy < widths[0] || (m > 1 && ldy < total)) return EXL3_EINVAL;
+    for (int i = 0; i < groups; ++i) {
+        if (!shape_ok(m, k, widths[i], K)) return EXL3_DECLINED;
+        if ((uint64_t) k * widths[i] * K / 8 > 0xFFFFFFFFull) return EXL3_DECLINED;   // one raw buffer per trellis
+    }
+    const GridPlan p = plan_grid(k, widths, groups);
+    if ((size_t) p.counters * 4 > COUNTER_BYTES) return EXL3_DECLINED;
+    if (!ws || ws_bytes < COUNTER_BYTES + (size_t) p.slots * m * 128 * 4) return EXL3_EWORKSPACE;
     GemvArgs a{};
     a.x = (const uint16_t*) x;
     a.ldx = ldx;
-    for (int i = 0; i < groups && !tabs; ++i) a.g[i] = gs[i];
+    for (int i = 0; i < groups; ++i) {
+        a.g[i] = gs[i];
+        a.g[i].n = widths[i];
+        a.g[i].G = p.G[i];
+        a.g[i].wg0 = p.wg0[i];
+        a.g[i].max_seg = p.max_seg[i];
+        a.g[i].part_off = p.slot_off[i] * m * 128;
+        a.g[i].cnt_off = p.cnt_off[i];
+    }
     if (tabs) {
         a.tab_trellis = tabs[0];
         a.tab_suh = tabs[1];
         a.tab_svh = tabs[2];
-        a.g[0].y = gs[0].y;
-        a.group_col_stride = col_stride;
     }
+    a.groups = groups;
     a.M = m;
     a.k = k;
-    a.n = n;
-    a.G = choose_grid(k, n, groups);
     a.UPB = k / 128;
-    a.U = (n / 128) * a.UPB;
-    a.max_seg = max_segments(k, n, a.G);
-    a.chunk_units = chunk_units(m, k, n, a.G);
+    a.chunk_units = chunk_units(m, p.max_per);
     a.ldy = ldy;
     a.counters = (uint32_t*) ws;
     a.part = (float*) ((char*) ws + COUNTER_BYTES);
-    return launch_gemv(a, K, codebook_of(mcg, mul1), groups, (hipStream_t) stream);
+    return launch_gemv(a, K, codebook_of(mcg, mul1), p.total_wgs, (hipStream_t) stream);
 }
 
 }  // namespace
@@ -640,15 +700,25 @@ int exl3_abi_version(void) { return EXL3_ABI_VERSION; }
 
 int exl3_gemv_grid(int k, int n, int groups)
 {
-    return (k % 128 || k < 128 || n % 128 || n < 128 || groups < 1 || groups > EXL3_MAX_GROUPS) ? 0
-                                                                                               : choose_grid(k, n, groups);
+    if (k % 128 || k < 128 || n % 128 || n < 128 || groups < 1 || groups > EXL3_MAX_GROUPS) return 0;
+    const int widths[EXL3_MAX_GROUPS] = {n, n, n, n};
+    return plan_grid(k, widths, groups).G[0];
 }
 
 size_t exl3_gemv_workspace_size(int m, int k, int n, int K, int groups)
 {
     (void) K;
     if (!shape_ok(m, k, n, 1) || groups < 1 || groups > EXL3_MAX_GROUPS) return 0;
-    return gemv_ws_bytes(m, k, n, groups);
+    const int widths[EXL3_MAX_GROUPS] = {n, n, n, n};
+    return gemv_ws_bytes(m, k, widths, groups);
+}
+
+size_t exl3_gemv_workspace_size_widths(int m, int k, const int* widths, int groups)
+{
+    if (!widths || groups < 1 || groups > EXL3_MAX_GROUPS) return 0;
+    for (int i = 0; i < groups; ++i)
+        if (!shape_ok(m, k, widths[i], 1)) return 0;
+    return gemv_ws_bytes(m, k, widths, groups);
 }
 
 int exl3_gemv_mr_supported(int m, int k, int n, int K, int mcg, int mul1)
@@ -666,7 +736,7 @@ int exl3_gemv(const void* x, int64_t ldx, const void* trellis, void* y, int64_t 
     if (!trellis || !y || !suh || !svh) return EXL3_EINVAL;
     if (m != 1) return EXL3_DECLINED;
     GemvGroup g{(const uint32_t*) trellis, (const uint16_t*) suh, (const uint16_t*) svh, (uint16_t*) y};
-    return gemv_common(x, ldx, &g, 1, nullptr, 0, ldy, m, k, n, K, mcg, mul1, workspace, ws_bytes, stream);
+    return gemv_common(x, ldx, &g, &n, 1, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream);
 }
 
 int exl3_gemv_mr(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh, void* A_had,
@@ -676,7 +746,7 @@ int exl3_gemv_mr(const void* x, int64_t ldx, const void* trellis, void* y, int64
     (void) A_had;
     if (!trellis || !y || !suh || !svh) return EXL3_EINVAL;
     GemvGroup g{(const uint32_t*) trellis, (const uint16_t*) suh, (const uint16_t*) svh, (uint16_t*) y};
-    return gemv_common(x, ldx, &g, 1, nullptr, 0, ldy, m, k, n, K, mcg, mul1, workspace, ws_bytes, stream);
+    return gemv_common(x, ldx, &g, &n, 1, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream);
 }
 
 int exl3_gemv_mr_grouped(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
@@ -687,12 +757,28 @@ int exl3_gemv_mr_grouped(const void* x, int64_t ldx, const void* const* trellis,
     (void) bszm_for_warps;
     if (!trellis || !suh || !svh || !y || groups < 1 || groups > EXL3_MAX_GROUPS) return EXL3_EINVAL;
     GemvGroup gs[EXL3_MAX_GROUPS];
+    int widths[EXL3_MAX_GROUPS];
     for (int i = 0; i < groups; ++i) {
-        if (!trellis[i] || !suh[i] || !svh[i]) return EXL3_EINVAL;
         gs[i] = {(const uint32_t*) trellis[i], (const uint16_t*) suh[i], (const uint16_t*) svh[i],
                  (uint16_t*) y + (int64_t) i * n};
+        widths[i] = n;
     }
-    return gemv_common(x, ldx, gs, groups, nullptr, 0, ldy, m, k, n, K, mcg, mul1, workspace, ws_bytes, stream);
+    return gemv_common(x, ldx, gs, widths, groups, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream);
+}
+
+int exl3_gemv_mr_grouped_widths(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
+                                const void* const* suh, const void* const* svh, const int* widths, int groups, int m,
+                                int k, int K, int mcg, int mul1, void* workspace, size_t ws_bytes, void* stream)
+{
+    if (!trellis || !suh || !svh || !y || !widths || groups < 1 || groups > EXL3_MAX_GROUPS) return EXL3_EINVAL;
+    GemvGroup gs[EXL3_MAX_GROUPS];
+    int64_t n0 = 0;
+    for (int i = 0; i < groups; ++i) {
+        gs[i] = {(const uint32_t*) trellis[i], (const uint16_t*) suh[i], (const uint16_t*) svh[i], (uint16_t*) y + n0};
+        n0 += widths[i];
+    }
+    if (ldy < n0) return EXL3_EINVAL;
+    return gemv_common(x, ldx, gs, widths, groups, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream);
 }
 
 int exl3_mgemm(const void* x, const int64_t* ptrs_trellis, void* y, const int64_t* ptrs_suh, void* xh,
@@ -701,9 +787,14 @@ int exl3_mgemm(const void* x, const int64_t* ptrs_trellis, void* y, const int64_
 {
     (void) xh;
     if (!ptrs_trellis || !ptrs_suh || !ptrs_svh || !y || groups < 1 || groups > EXL3_MAX_GROUPS) return EXL3_EINVAL;
-    GemvGroup g{nullptr, nullptr, nullptr, (uint16_t*) y};
+    GemvGroup gs[EXL3_MAX_GROUPS];
+    int widths[EXL3_MAX_GROUPS];
+    for (int i = 0; i < groups; ++i) {
+        gs[i] = {nullptr, nullptr, nullptr, (uint16_t*) y + (int64_t) i * n};
+        widths[i] = n;
+    }
     const int64_t* tabs[3] = {ptrs_trellis, ptrs_suh, ptrs_svh};
-    return gemv_common(x, k, &g, groups, tabs, n, (int64_t) groups * n, 1, k, n, K, mcg, mul1, workspace, ws_bytes,
+    return gemv_common(x, k, gs, widths, groups, tabs, (int64_t) groups * n, 1, k, K, mcg, mul1, workspace, ws_bytes,
                        stream);
 }
 

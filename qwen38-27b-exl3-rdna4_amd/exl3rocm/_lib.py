@@ -18,6 +18,7 @@ ABI_VERSION = 1
 
 _p, _i, _i64, _sz, _f = C.c_void_p, C.c_int, C.c_int64, C.c_size_t, C.c_float
 _pp = C.POINTER(C.c_void_p)
+_ip = C.POINTER(C.c_int)
 
 # name -> (restype, argtypes); mirrors include/exl3_mi355x.h
 SIGNATURES = {
@@ -33,6 +34,9 @@ SIGNATURES = {
     "exl3_gemv_mr": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "exl3_gemv_mr_grouped": (_i, [_p, _i64, _pp, _p, _i64, _pp, _p, _pp, _i, _i, _i, _i, _i, _i, _i, _i, _p, _sz,
                                   _p]),
+    "exl3_gemv_mr_grouped_widths": (_i, [_p, _i64, _pp, _p, _i64, _pp, _pp, _ip, _i, _i, _i, _i, _i, _i, _p, _sz,
+                                         _p]),
+    "exl3_gemv_workspace_size_widths": (_sz, [_i, _i, _ip, _i]),
     "exl3_mgemm": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "exl3_hgemm_recon": (_i, [_p, _i64, _p, _i64, _p, _i64, _i, _i, _i, _p]),
     "exl3_gemm_trellis": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),

@@ -3,10 +3,12 @@
 Each function takes torch tensors, validates shapes the way the reference bindings do
 (TORCH_CHECK -> RuntimeError) and calls libexl3_mi355x.so.  Names follow the reference
 extension (`exllamav3_ext`): decode, reconstruct, reconstruct_slice, had_r_128, exl3_gemv,
-exl3_gemv_mr, exl3_gemv_mr_grouped, exl3_gemv_mr_supported, exl3_mgemm, hgemm_recon, exl3_gemm.
+exl3_gemv_mr, exl3_gemv_mr_grouped, exl3_gemv_mr_supported, exl3_mgemm, hgemm_recon, exl3_gemm
+(plus exl3_gemv_mr_grouped_widths, which has no reference counterpart).
 """
 from __future__ import annotations
 
+from ctypes import c_int as C_int
 from typing import Optional, Sequence
 
 import torch
@@ -172,6 +174,27 @@ def exl3_gemv_mr_grouped(A, B: Sequence[torch.Tensor], C, suh: Sequence[torch.Te
                                                 _ldy(C, g * n), ps, None, pv, g, m, k, n, K, *_cb_flags(mcg, mul1),
                                                 bszm_for_warps, ws.data_ptr(), ws.numel(), _stream(A)),
                    "exl3_gemv_mr_grouped")
+
+
+def exl3_gemv_mr_grouped_widths(A, B: Sequence[torch.Tensor], C, suh: Sequence[torch.Tensor],
+                                svh: Sequence[torch.Tensor], K: int, mcg: bool, mul1: bool) -> int:
+    """Groups of any widths sharing x and K (q/k/v) in one launch; group i writes the columns after
+    groups 0..i-1 of C.  No counterpart in the reference extension (it launches these one by one)."""
+    _cuda(A, C, *B, *suh, *svh)
+    x2, m, k = _rows(A)
+    g = len(B)
+    widths = [int(s.shape[0]) for s in svh]
+    _need(1 <= g <= L.MAX_GROUPS and len(suh) == g and len(svh) == g, "grouped: 1..4 groups with suh/svh each")
+    _need(C.shape[-1] >= sum(widths), "grouped: output narrower than the groups")
+    wa = (C_int * g)(*widths)
+    ws = workspace(A.device, int(L.lib().exl3_gemv_workspace_size_widths(m, k, wa, g)))
+    pt, _a = L.ptr_array([b.data_ptr() for b in B])
+    ps, _b = L.ptr_array([s.data_ptr() for s in suh])
+    pv, _c = L.ptr_array([s.data_ptr() for s in svh])
+    return L.check(L.lib().exl3_gemv_mr_grouped_widths(x2.data_ptr(), x2.stride(0) if m > 1 else k, pt, C.data_ptr(),
+                                                       _ldy(C, sum(widths)), ps, pv, wa, g, m, k, K,
+                                                       *_cb_flags(mcg, mul1), ws.data_ptr(), ws.numel(), _stream(A)),
+                   "exl3_gemv_mr_grouped_widths")
 
 
 def exl3_mgemm(x, ptrs_trellis, y, ptrs_suh, xh, ptrs_svh, K: int, mcg: bool, mul1: bool) -> int:

@@ -137,16 +137,20 @@ def exl3_linear_groups(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[t
     if M == 0:
         return y.view(*x.shape[:-1], 0 if not widths else sum(widths))
     if M <= MR_MAX:
-        # runs of consecutive groups with equal (K, width) share one grouped launch (gate/up, k/v),
-        # each written straight into its row-strided column slice
+        # runs of consecutive groups with equal K share one launch, each group written straight into
+        # its row-strided column slice: equal widths (gate/up, k/v) through the reference's grouped
+        # entry point, mixed widths (q/k/v) through the widths form
         i, n0 = 0, 0
         while i < ng:
             j = i + 1
-            while j < ng and j - i < _lib.MAX_GROUPS and K[j] == K[i] and widths[j] == widths[i]:
+            while j < ng and j - i < _lib.MAX_GROUPS and K[j] == K[i]:
                 j += 1
-            if j - i > 1:
+            if j - i > 1 and all(w == widths[i] for w in widths[i:j]):
                 E.exl3_gemv_mr_grouped(x2, list(trellis[i:j]), y[:, n0:], list(suh[i:j]), None, list(svh[i:j]),
                                        K[i], mcg, mul1, j - i)
+            elif j - i > 1:
+                E.exl3_gemv_mr_grouped_widths(x2, list(trellis[i:j]), y[:, n0:], list(suh[i:j]), list(svh[i:j]),
+                                              K[i], mcg, mul1)
             else:
                 _linear_into(x2, trellis[i], suh[i], svh[i], K[i], mcg, mul1, y[:, n0:n0 + widths[i]])
             n0 += sum(widths[i:j])

@@ -58,6 +58,21 @@ def test_workspace_sizes():
     assert L.exl3_gemv_workspace_size(1, 5000, 5120, 4, 1) == 0         # k not a multiple of 128
 
 
+def test_widths_workspace_sizes():
+    L = _lib.lib()
+    eq = (ctypes.c_int * 2)(4096, 4096)
+    assert L.exl3_gemv_workspace_size_widths(4, 5120, eq, 2) == L.exl3_gemv_workspace_size(4, 5120, 4096, 4, 2)
+    qkv = (ctypes.c_int * 3)(5120, 1024, 1024)
+    assert L.exl3_gemv_workspace_size_widths(1, 5120, qkv, 3) > 65536
+    bad = (ctypes.c_int * 2)(5120, 1000)
+    assert L.exl3_gemv_workspace_size_widths(1, 5120, bad, 2) == 0
+    dummy = ctypes.c_void_p(0x1000)
+    arr = (ctypes.c_void_p * 3)(0x1000, 0x1000, 0x1000)
+    # output row narrower than the groups' total width
+    assert L.exl3_gemv_mr_grouped_widths(dummy, 5120, arr, dummy, 5120, arr, arr, qkv, 3, 2, 5120, 4, 0, 1, dummy,
+                                         1 << 30, None) == _lib.EINVAL
+
+
 def test_mr_supported_predicate():
     L = _lib.lib()
     assert L.exl3_gemv_mr_supported(1, 5120, 5120, 4, 0, 1) == 1

@@ -206,6 +206,50 @@ def test_grouped_rows_and_pointer_table_form():
     assert_close(rows1.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("widths,bits,cb", [((2048, 512, 512), 4, 2), ((1024, 256, 384, 128), 3, 1)])
+def test_grouped_widths_parity_and_rows(widths, bits, cb):
+    """Mixed-width groups sharing x (q/k/v) in one launch: every group's columns match the
+    oracle to the parity bar, every row of an m-row call == its m = 1 call bitwise, and
+    linear_groups routes the module through this form."""
+    k, m = 2048, 6
+    mats = [synth.layer("wid", i, k, n, bits) for i, n in enumerate(widths)]
+    x = synth.activations(synth.key_of("wid", "x", bits), m, k)
+    X = to_dev(x)[0]
+    Ts = [to_dev(t[0].view(np.int16))[0] for t in mats]
+    SUs = [to_dev(t[1])[0] for t in mats]
+    SVs = [to_dev(t[2])[0] for t in mats]
+    total = sum(widths)
+    rows1 = []
+    for r in range(m):
+        y1 = torch.empty(1, total, dtype=torch.float16, device=DEV)
+        assert E.exl3_gemv_mr_grouped_widths(X[r:r + 1].contiguous(), Ts, y1, SUs, SVs, bits, cb == 1, cb == 2) == 0
+        rows1.append(y1)
+    rows1 = torch.cat(rows1)
+    ym = torch.empty(m, total, dtype=torch.float16, device=DEV)
+    assert E.exl3_gemv_mr_grouped_widths(X, Ts, ym, SUs, SVs, bits, cb == 1, cb == 2) == 0
+    assert torch.equal(ym.view(torch.int16), rows1.view(torch.int16))
+    ref = np.concatenate([cpu.linear(x, t[0], bits, t[1], t[2], cb) for t in mats], axis=1)
+    assert_close(ym.cpu().numpy(), ref)
+    yg = torch.ops.exl3rocm.linear_groups(X, Ts, SUs, SVs, [bits] * len(widths), cb == 1, cb == 2)
+    assert torch.equal(yg.view(torch.int16), ym.view(torch.int16))
+
+
+def test_grouped_widths_equal_widths_match_grouped_form():
+    """With equal widths the widths form and the reference's grouped form plan the same grid:
+    bitwise equal outputs."""
+    k, n, bits, m = 1024, 512, 4, 3
+    mats = [synth.layer("wideq", i, k, n, bits) for i in range(3)]
+    X = to_dev(synth.activations(synth.key_of("wideq", "x"), m, k))[0]
+    Ts = [to_dev(t[0].view(np.int16))[0] for t in mats]
+    SUs = [to_dev(t[1])[0] for t in mats]
+    SVs = [to_dev(t[2])[0] for t in mats]
+    yw = torch.empty(m, 3 * n, dtype=torch.float16, device=DEV)
+    yg = torch.empty(m, 3 * n, dtype=torch.float16, device=DEV)
+    E.exl3_gemv_mr_grouped_widths(X, Ts, yw, SUs, SVs, bits, False, True)
+    E.exl3_gemv_mr_grouped(X, Ts, yg, SUs, None, SVs, bits, False, True, 3)
+    assert torch.equal(yw.view(torch.int16), yg.view(torch.int16))
+
+
 def test_linear_groups_mixed_bits_rows_equal():
     """Fused mixed-bit module (q=2 / k,v=5 style): M=4 == four M=1 calls, bitwise."""
     k = 5120
