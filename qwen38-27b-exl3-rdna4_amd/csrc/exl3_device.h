@@ -235,10 +235,11 @@ __device__ __forceinline__ uint32_t decode_pair(const uint32_t* W, uint32_t k_hi
     const uint32_t x0 = state_x<BITS, CB, 2 * I>(W, k_hi, k_add, k_lo);
     const uint32_t x1 = state_x<BITS, CB, 2 * I + 1>(W, k_hi, k_add, k_lo);
     if constexpr (CB == 2) {
-        // 0x6400 + bytesum: the fp16 bit pattern of 1024 + s (exact for s <= 1020)
-        const uint32_t s0 = __builtin_amdgcn_udot4(x0, 0x01010101u, c6400, false);
-        const uint32_t s1 = __builtin_amdgcn_udot4(x1, 0x01010101u, c6400, false);
-        f16x2 h = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(s1, s0, 0x05040100u));
+        // 0x6400 + bytesum is the fp16 bit pattern of 1024 + s (exact for s <= 1020).  Byte sums
+        // of differences against zero: v_sad_u8 adds s0 to 0x64006400, v_sad_hi_u8 adds s1 << 16,
+        // which packs the pair (1024 + s1, 1024 + s0) in two ops with no carry between halves.
+        const uint32_t lo = __builtin_amdgcn_sad_u8(x0, 0u, c6400);
+        f16x2 h = __builtin_bit_cast(f16x2, __builtin_amdgcn_sad_hi_u8(x1, 0u, lo));
         const f16x2 k_inv = {bits_f16(0x1EEEu), bits_f16(0x1EEEu)};
         const f16x2 k_bias = {bits_f16(0xC931u), bits_f16(0xC931u)};
         h = __builtin_elementwise_fma(h, k_inv, k_bias);           // v_pk_fma_f16: one rounding
@@ -275,7 +276,7 @@ __device__ __forceinline__ void decode_qblock(const uint32_t* W, uint32_t* P)
     const uint32_t k_hi = Codebook<CB>::hi << 16;
     const uint32_t k_add = CB == 0 ? Codebook<0>::add : 0u;
     const uint32_t k_lo = Codebook<CB>::lo;
-    const uint32_t c6400 = 0x6400u;
+    const uint32_t c6400 = 0x64006400u;
     decode_pairs_rec<BITS, CB, 0>(W, P, k_hi, k_add, k_lo, c6400);
 }
 
