@@ -344,13 +344,24 @@ def test_hgemm_recon_vs_fp32():
     assert err < 1e-3, err
 
 
-def test_recon_route_matches_fused_route():
-    x, tr, su, sv = layer(1024, 512, 4, m=96)
+def test_prefill_wide_ragged_parity():
+    """A wide layer (512 column tiles) with a ragged last row tile against the oracle: the fused
+    output transform writes only the valid rows."""
+    m, k, n, bits = 600, 256, 65536, 3
+    x, tr, su, sv = layer(k, n, bits, m=m)
+    assert_close(gpu_linear(x, tr, su, sv, bits, 2), cpu.linear(x, tr, bits, su, sv, 2), (m, k, n, bits))
+
+
+@pytest.mark.parametrize("m,k,n", [(96, 1024, 512), (512, 256, 65536)])
+def test_recon_route_matches_fused_route(m, k, n):
+    """reconstruct + hgemm_recon + output transform == the fused prefill route, bitwise (same
+    MFMA accumulation order), on a small and a wide layer."""
+    x, tr, su, sv = layer(k, n, 4, m=m)
     X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
     fused = torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True)
     xh = torch.empty_like(X)
     E.had_r_128(X, xh, SU, None, 1.0)
-    W = torch.empty(1024, 512, dtype=torch.float16, device=DEV)
+    W = torch.empty(k, n, dtype=torch.float16, device=DEV)
     E.reconstruct(W, T, 4, False, True)
     y = torch.empty_like(fused)
     E.hgemm_recon(xh, W, y)
