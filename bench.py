@@ -6,7 +6,8 @@ Qwen-27B-shaped decoder layer (q, k, v, o 5120-wide attention projections and th
 5120 -> 17408 -> 5120 MLP) at 4 bpw, mul1 codebook, with the plugin's own routing (q/k/v as one
 fused module, gate/up through the grouped pointer-table launch).  One *step* = one layer's
 linears on one token.  Steps cycle over 8 distinct copies of the layer's weights (1.3 GB, ~5x the
-256 MB Infinity Cache) and are replayed from HIP graphs, so weights stream from HBM as in decode.
+256 MB Infinity Cache) and are replayed from one HIP graph holding a step per copy (an 8-layer
+stack), so weights stream from HBM as in decode.
 
   value        = whole-job trellis + x + suh + svh + y bytes / elapsed time  (GB/s)
   roofline     = the dominant kernel (the M=1 4-bpw GEMV): algorithmic bytes per launch / mean
@@ -17,6 +18,7 @@ Extras: configuration 4 prefill (M = 2048 through a 64-layer stack, TFLOPS vs 2.
 configuration 3 small-batch crossover, configuration 2 bitrate sweep.
 
   python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-sweep] [--no-cpu]
+  python bench.py --traffic-probe      (what the PMC traffic passes profile)
 """
 from __future__ import annotations
 
@@ -107,19 +109,30 @@ def capture_steps(torch, sets, x5120, x17408):
         with torch.cuda.graph(g, stream=s):
             ls.step(x5120, x17408)
         graphs.append(g)
+    # all copies' steps in one graph (one step per layer of an 8-layer stack), so host launches
+    # between replays are rare
+    stack = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(stack, stream=s):
+        for ls in sets:
+            ls.step(x5120, x17408)
     torch.cuda.synchronize()
-    return graphs
+    return graphs, stack
 
 
 def time_graphs(torch, graphs, steps, warmup):
+    """Exactly `steps` steps: steps // copies replays of the stack graph, then single-step graphs."""
+    per, stack = graphs
+    n = len(per)
     for i in range(warmup):
-        graphs[i % len(graphs)].replay()
+        per[i % n].replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record()
-    for i in range(steps):
-        graphs[i % len(graphs)].replay()
+    for _ in range(steps // n):
+        stack.replay()
+    for i in range(steps % n):
+        per[i].replay()
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -258,6 +271,43 @@ def small_batch(torch, sets, ms=(1, 4, 8, 16, 32)):
     return res
 
 
+def traffic_probe(torch, bits=4, copies=8):
+    """--traffic-probe: the dispatches two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE)
+    read for roofline.traffic: a 256 MiB device copy (calibration: it reads and writes a known
+    byte count) and one eager pass of the configuration-1 step over every weight copy."""
+    n = 256 << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    from exl3rocm import synth
+    _, sets = build_layers(torch, bits, copies)
+    x5120 = torch.from_numpy(synth.activations(synth.key_of("config1", "x", HIDDEN), 1, HIDDEN)).cuda()
+    x17408 = torch.from_numpy(synth.activations(synth.key_of("config1", "x", INTER), 1, INTER)).cuda()
+    for ls in sets:
+        ls.step(x5120, x17408)
+    torch.cuda.synchronize()
+    step_bytes = sum(algo_bytes(1, k, n_, bits) for _, k, n_ in LAYER)
+    print(json.dumps({"copy_bytes": n, "copies": copies, "launches_per_step": launches_per_step(),
+                      "step_algorithmic_bytes": step_bytes}), flush=True)
+    return 0
+
+
+def measured_traffic():
+    """HBM bytes per GEMV launch of the configuration-1 step, from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter on a copy of known size);
+    None when that summary is absent."""
+    path = os.path.join(REPO, "profiles", "gemv_traffic_config1.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -267,6 +317,7 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true", help="only the dispatches the PMC traffic passes read")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this engine runs on one GPU; multi-GPU runs are not part of this build "
@@ -277,6 +328,8 @@ def main() -> int:
     from exl3rocm import _lib, ops  # noqa: F401
     _lib.lib()
     bits = 4
+    if args.traffic_probe:
+        return traffic_probe(torch, bits, args.copies)
     log("building layer set (4 bpw, mul1) x %d copies" % args.copies)
     base, sets = build_layers(torch, bits, args.copies)
     from exl3rocm import synth
@@ -291,8 +344,11 @@ def main() -> int:
     lps = launches_per_step()
     avg_launch_us = ms_per_step * 1e3 / lps
     achieved = step_bytes / lps / avg_launch_us / 1e3
+    traffic = measured_traffic()
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": round(traffic) if traffic is not None else None,
+                "traffic_source": "profiles/gemv_traffic_config1.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
                 "kernel": "gemv_kernel<4,2,1> (every M=1 launch of the step)",
                 "bytes_per_launch": step_bytes / lps, "mean_launch_us": round(avg_launch_us, 3)}
     extra = {"launches_per_step": lps, "step_bytes": step_bytes, "wall_s": round(wall, 3)}
