@@ -224,10 +224,17 @@ def prefill_chunk(torch, layers=64, m=2048, bits=4, iters=2):
     xb = torch.randn(m, INTER, device="cuda", dtype=torch.float16, generator=g)
     ops = torch.ops.exl3rocm
 
+    # the plugin's module grouping: q/k/v and gate/up are fused modules (one linear_groups call,
+    # one GEMM launch each), o and down single linears
     def chunk():
         for lw in stack:
-            for name, k, n in LAYER:
-                ops.linear(xb if k == INTER else xa, *lw[name], bits, False, True)
+            for names in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
+                x = xb if names[0] == "down" else xa
+                if len(names) == 1:
+                    ops.linear(x, *lw[names[0]], bits, False, True)
+                else:
+                    ops.linear_groups(x, [lw[nm][0] for nm in names], [lw[nm][1] for nm in names],
+                                      [lw[nm][2] for nm in names], [bits] * len(names), False, True)
 
     chunk()
     torch.cuda.synchronize()

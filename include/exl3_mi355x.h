@@ -141,6 +141,17 @@ int exl3_hgemm_recon(const void* x, int64_t ldx, const void* W, int64_t ldw, voi
 int exl3_gemm_trellis(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh,
                       void* xh, const void* svh, int m, int k, int n, int K, int mcg, int mul1, void* stream);
 
+/* Prefill EXL3 linear of up to 4 groups sharing x and K but of any widths (the checkpoint tensors
+ * of a fused module: q / k / v, gate / up): group i writes the widths[i] columns of y that follow
+ * groups 0 .. i-1 (rows ldy apart, ldy >= sum of widths).  xh is an fp16 scratch of groups * m * k
+ * elements (each group's rotated input).  No counterpart in the reference: its linear_groups runs
+ * one prefill per group (reference vllm_plugin/exl3rocm/ops.py:171-175).  Callers: exl3rocm's
+ * linear_groups for M > 32.  All groups' output tiles share one GEMM launch, so a module fills the
+ * GPU as one layer would. */
+int exl3_gemm_trellis_grouped(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
+                              const void* const* suh, void* xh, const void* const* svh, const int* widths, int groups,
+                              int m, int k, int K, int mcg, int mul1, void* stream);
+
 /* Dispatcher by row count: m <= 32 -> fused GEMV, else the prefill GEMM.  Returns the route
  * tag (1 = GEMV, 2 = prefill GEMM) or a negative error.
  * Replaces `exl3_gemm(A, B, C, suh, A_had, svh, -1, mcg, mul1, 0) -> int` (reference ops.py:82). */

@@ -278,21 +278,355 @@ int launch_gemm(const uint16_t* xh, int64_t ldx, BSRC b, const uint16_t* Wd, int
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 
-template <int BITS, int CB>
-int launch_trellis_gemm(const uint16_t* xh, int64_t ldx, const void* trellis, uint16_t* y, int64_t ldy,
-                        const uint16_t* svh, int M, int K, int N, hipStream_t s)
+// ============================================================================================
+// Producer / consumer prefill GEMM (trellis B).  Tile 256 x 128, K step 64, one workgroup of
+// 8 waves per CU:
+//   waves 0-3 (consumers, one per SIMD): wave w owns rows 64w .. 64w+63 of the tile, all 128
+//     columns (4 x 8 MFMA tiles of 16 x 16, fp32 accumulators in registers); it only reads A and B
+//     fragments from LDS and issues v_mfma_f32_16x16x32_f16;
+//   waves 4-7 (producers, one per SIMD) decode the trellis tiles of the next K step (one q-block
+//     per lane) into LDS in B-fragment order and stage its xh rows into LDS in A-fragment order.
+// Every SIMD pairs one MFMA wave with one VALU wave for the whole loop, so matrix and vector work
+// overlap by construction.
+// xh rows are read with whole 128-byte lines per instruction (8 lanes per row: 8 rows x 64 k per
+// wave load), which halves the memory-pipeline line requests of a fragment-shaped load (16 rows x
+// 64 bytes); the row tile's 2 KB of LDS holds (row r, 16-byte chunk c) in slot
+// (r >> 1) * 16 + 8 (r & 1) + (c ^ (r >> 1)), so both the producers' row-chunk stores and the
+// consumers' fragment reads (16 rows of one chunk) hit 16 distinct 16-byte bank groups.
+// Pipeline: two LDS stages and one workgroup barrier B_s per K step.  Between B_{s-1} and B_s the
+// producers stage step s + 1 (its trellis words and xh rows were requested two intervals earlier
+// into register rings) and request step s + 3; the consumers run the step's four 16-MFMA
+// sub-blocks on stage s & 1, each sub-block's fragments read during the previous sub-block, and
+// pass B_s before the last sub-block so that the first fragments of step s + 1 are read under its
+// MFMAs.
+// Groups (the checkpoint tensors of a fused module: one x, a rotated input per group) are
+// flattened into one tile list, so a module pays one GEMM launch and fills the GPU as one.  Each output element sees the MFMA sequence of gemm_kernel (k
+// steps in order, two k-substeps each) on the same operands: both kernels give bitwise-equal C.
+// ============================================================================================
+struct PcGroup {
+    const uint16_t* xh;         // [M][ldx] rotated input of the group (M * ldx * 2 < 2^31)
+    const uint32_t* trellis;
+    const uint16_t* svh;
+    uint16_t* y;                // first output column of the group (rows ldy apart)
+    int n;                      // columns
+    int tile0;                  // first tile of the group in the flattened tile list
+};
+
+struct PcArgs {
+    int64_t ldx, ldy;
+    int M, K, groups, total, xcd_remap;
+    PcGroup g[EXL3_MAX_GROUPS];
+};
+
+struct PC {
+    static constexpr int MT = 256, THREADS = 512;
+    static constexpr int RT_BYTES = 16 * 128;          // one row tile of xh for one K step (2 KB)
+    static constexpr int A_BYTES = (MT / 16) * RT_BYTES;   // 32 KB
+    static constexpr int B_BYTES = 2 * 8 * FRAG;       // 16 KB
+    static constexpr int BUF = A_BYTES + B_BYTES;      // one stage
+    static constexpr int STAGES = 2;
+    static constexpr int C_ROW = 136;                  // LDS row (halves) of the epilogue's C tile
+    static constexpr int LDS = STAGES * BUF > MT * C_ROW * 2 ? STAGES * BUF : MT * C_ROW * 2;
+};
+
+// byte offset of (row r, 16-byte chunk c) inside a row tile's 2 KB of A
+__device__ __forceinline__ int a_slot(int r, int c) { return ((r >> 1) * 16 + 8 * (r & 1) + (c ^ (r >> 1))) * 16; }
+
+// Workgroup barrier after this wave's LDS writes completed (lgkmcnt(0)), with no global-memory
+// wait (prefetches stay in flight across it) and no instruction moved across it by the scheduler.
+__device__ __forceinline__ void barrier_lds()
 {
-    TrellisB<BITS, CB> b{(const uint32_t*) trellis, N / 16};
-    return launch_gemm<TrellisB<BITS, CB>, false, GEMM_MT, true>(xh, ldx, b, nullptr, 0, y, ldy, svh, M, K, N, s);
+    __builtin_amdgcn_sched_barrier(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);                // lgkmcnt(0), vmcnt / expcnt not waited
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int BITS, int CB>
+__global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
+{
+    extern __shared__ __align__(16) char lds[];
+    const int t = threadIdx.x;
+    int u = blockIdx.x;
+    if (a.xcd_remap) u = (u & 7) * (a.total / 8) + (u >> 3);    // consecutive tiles share an XCD
+    // constant indices only into the kernel-argument struct (a runtime index copies it to scratch)
+    int gi = 0;
+    if (a.groups > 1 && u >= a.g[1].tile0) gi = 1;
+    if (a.groups > 2 && u >= a.g[2].tile0) gi = 2;
+    if (a.groups > 3 && u >= a.g[3].tile0) gi = 3;
+    const PcGroup gg = gi == 0 ? a.g[0] : gi == 1 ? a.g[1] : gi == 2 ? a.g[2] : a.g[3];
+    const int tiles_n = gg.n / NT_COLS, v = u - gg.tile0;
+    const int tm = v / tiles_n, tn = v - tm * tiles_n;
+    const int row0 = tm * PC::MT, col0 = tn * NT_COLS;
+    const int steps = a.K / KSTEP, M = a.M;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
+    auto stage = [&](int s) __attribute__((always_inline)) { return lds + (s & 1) * PC::BUF; };
+
+    if (wave < 4) {
+        // ---- consumer ---------------------------------------------------------------------
+        f32x4 acc[4][8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // A fragments of k-substep ks: row tiles 4 wave + i, lane (g, r) = (row r, chunk 4 ks + g)
+        const int a_lane = a_slot(lane & 15, lane >> 4);           // chunk g of k-substep 0
+        const int a_lane1 = a_slot(lane & 15, 4 + (lane >> 4));    // chunk g of k-substep 1
+        auto rd_a = [&](const char* stg, int ks, f16x8* A) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                A[i] = *reinterpret_cast<const f16x8*>(stg + (4 * wave + i) * PC::RT_BYTES + (ks ? a_lane1 : a_lane));
+        };
+        // B fragments of sub-block (ks, jh): column tiles 4 jh .. 4 jh + 3 of k-substep ks
+        auto rd_b = [&](const char* stg, int ks, int jh, f16x8* B) __attribute__((always_inline)) {
+            const char* bf = stg + PC::A_BYTES;
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int j = 4 * jh + jj;
+                B[jj] = *reinterpret_cast<const f16x8*>(bf + ((ks * 8 + j) * 64 + (lane ^ bswz(j))) * 16);
+            }
+        };
+        auto mm = [&](const f16x8* A, int jh, const f16x8* B) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj)
+                    acc[i][4 * jh + jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B[jj], acc[i][4 * jh + jj], 0, 0, 0);
+        };
+        f16x8 A0[4], A1[4], B0[4], B1[4];
+        barrier_lds();                                     // B_-1: stage 0 staged
+        rd_a(stage(0), 0, A0);
+        rd_b(stage(0), 0, 0, B0);
+        // sched_barrier pins the issue order: the reads of the next sub-block go out before the
+        // MFMAs that hide them, and nothing crosses the workgroup barrier
+        for (int s = 0; s < steps; ++s) {
+            const char* stg = stage(s);
+            rd_b(stg, 0, 1, B1);
+            rd_a(stg, 1, A1);
+            __builtin_amdgcn_sched_barrier(0);
+            mm(A0, 0, B0);
+            __builtin_amdgcn_sched_barrier(0);
+            rd_b(stg, 1, 0, B0);
+            __builtin_amdgcn_sched_barrier(0);
+            mm(A0, 1, B1);
+            __builtin_amdgcn_sched_barrier(0);
+            rd_b(stg, 1, 1, B1);
+            __builtin_amdgcn_sched_barrier(0);
+            mm(A1, 0, B0);
+            barrier_lds();                                 // B_s: stage s read, stage s + 1 staged
+            if (s + 1 < steps) {
+                rd_a(stage(s + 1), 0, A0);
+                rd_b(stage(s + 1), 0, 0, B0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mm(A1, 1, B1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // C = fp16(acc) into LDS: every read and write of the stages finished before the last B_s
+        uint16_t* ct = reinterpret_cast<uint16_t*>(lds);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = wave * 64 + i * 16 + 4 * (lane >> 4) + e;
+                    const int c = j * 16 + (lane & 15);
+                    ct[r * PC::C_ROW + c] = f16_bits((f16) acc[i][j][e]);
+                }
+    } else {
+        // ---- producer ---------------------------------------------------------------------
+        // the producer is the longer path of a step: its VALU issue goes first (measured faster)
+        __builtin_amdgcn_s_setprio(3);
+        const int pw = wave - 4, pt = t - 256;
+        // xh rows 64 pw + 8 i + (lane >> 3), 16-byte chunk lane & 7 (whole 128-byte lines); rows
+        // past M read row M - 1 (their outputs are never stored, and rows do not interact)
+        const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(gg.xh), 0, (int) ((uint32_t) M * (uint32_t) a.ldx * 2u), RAW_BUFFER_FLAGS);
+        uint32_t aoff[8];
+        int adst[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int r = 64 * pw + 8 * i + (lane >> 3);                // row in the tile
+            const int gr = min(row0 + r, M - 1);
+            aoff[i] = ((uint32_t) gr * (uint32_t) a.ldx + (lane & 7) * 8) * 2u;
+            adst[i] = (r >> 4) * PC::RT_BYTES + a_slot(r & 15, lane & 7);
+        }
+        auto load_a = [&](int st, u32x4* A) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                A[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, aoff[i], st * (KSTEP * 2), 0));
+        };
+        auto store_a = [&](char* stg, const u32x4* A) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(stg + adst[i]) = A[i];
+        };
+        const int ktl = pt >> 6, ntl = (pt >> 3) & 7, q = pt & 7;
+        const int nt_total = gg.n / 16;
+        // the trellis as one raw buffer (k * n * K / 8 < 2^31 on the host): a step advances the
+        // scalar offset by 4 k-tile rows; the lane's q-block and ring-predecessor word offsets are fixed
+        const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint32_t*>(gg.trellis), 0, (int) ((uint32_t) (a.K / 16) * (uint32_t) nt_total * 32u * BITS),
+            RAW_BUFFER_FLAGS);
+        const uint32_t tile_w = (uint32_t) (ktl * nt_total + col0 / 16 + ntl) * (8 * BITS);
+        const uint32_t off_main = (tile_w + q * BITS) * 4u;
+        const uint32_t off_prev = (tile_w + (q == 0 ? 8 * BITS - 1 : q * BITS - 1)) * 4u;
+        const uint32_t step_bytes = (uint32_t) nt_total * 4u * 32u * BITS;   // 4 k-tile rows
+        auto fetch = [&](int st, uint32_t* W) __attribute__((always_inline)) {
+            load_qblock_buf<BITS>(trs, off_main, off_prev, (uint32_t) st * step_bytes, W);
+        };
+        // B fragment tile ks * 8 + ntl, lanes XOR-swizzled by n-tile (conflict-free stores)
+        auto decode_store = [&](const uint32_t* W, char* stg) __attribute__((always_inline)) {
+            uint32_t P[16];
+            decode_qblock<BITS, CB>(W, P);
+            char* bf = stg + PC::A_BYTES;
+            const int ks = ktl >> 1;
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int rh = 0; rh < 2; ++rh) {
+                    const int ln = ((2 * (ktl & 1) + rh) * 16 + q + 8 * h) ^ bswz(ntl);
+                    const u32x4 val = {P[2 * h + rh], P[4 + 2 * h + rh], P[8 + 2 * h + rh], P[12 + 2 * h + rh]};
+                    *reinterpret_cast<u32x4*>(bf + ((ks * 8 + ntl) * 64 + ln) * 16) = val;
+                }
+        };
+        // step j's xh rows and trellis words live in register ring slot j % 3 (compile-time slot
+        // indices: the loop is unrolled by 3), requested two intervals before they are staged
+        u32x4 X0[8], X1[8], X2[8];
+        uint32_t R0[BITS + 1], R1[BITS + 1], R2[BITS + 1];
+        load_a(0, X0);
+        fetch(0, R0);
+        load_a(min(1, steps - 1), X1);
+        fetch(min(1, steps - 1), R1);
+        load_a(min(2, steps - 1), X2);
+        fetch(min(2, steps - 1), R2);
+        decode_store(R0, stage(0));
+        store_a(stage(0), X0);
+        barrier_lds();                                     // B_-1
+        // interval s (between B_s-1 and B_s): stage step s + 1, then request step s + 3 into the
+        // freed slot; the last intervals stage the last step again into a stage no longer read
+        auto interval = [&](int s, const uint32_t* Wd, const u32x4* Xd, uint32_t* Wf, u32x4* Xf) __attribute__((always_inline)) {
+            decode_store(Wd, stage(s + 1));
+            store_a(stage(s + 1), Xd);
+            __builtin_amdgcn_sched_barrier(0);
+            const int s3 = min(s + 3, steps - 1);
+            load_a(s3, Xf);
+            fetch(s3, Wf);
+            barrier_lds();                                 // B_s
+        };
+        int s = 0;
+        for (; s + 2 < steps; s += 3) {
+            interval(s, R1, X1, R0, X0);
+            interval(s + 1, R2, X2, R1, X1);
+            interval(s + 2, R0, X0, R2, X2);
+        }
+        if (s < steps) interval(s, R1, X1, R0, X0);
+        if (s + 1 < steps) interval(s + 1, R2, X2, R1, X1);
+        __builtin_amdgcn_s_setprio(0);
+    }
+    __syncthreads();                                       // C tile complete in LDS
+
+    // ---- epilogue: y = fp16(fp16(Had128(C)) * svh), 16 lanes per row, 16-byte stores -------------
+    const uint16_t* ct = reinterpret_cast<const uint16_t*>(lds);
+    const int l16 = t & 15;
+    const u32x4 sv = *reinterpret_cast<gc_u32x4*>(as_global(gg.svh) + col0 + 8 * l16);
+    g_u16* const gy = as_global(gg.y);
+    for (int r0 = 0; r0 < PC::MT; r0 += PC::THREADS / 16) {
+        const int r = r0 + (t >> 4);
+        const u32x4 c = *reinterpret_cast<const u32x4*>(ct + r * PC::C_ROW + 8 * l16);
+        const u32x4 res = had128_x8(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, R_SCALE);
+        if (row0 + r < M) *reinterpret_cast<g_u32x4*>(gy + (int64_t) (row0 + r) * a.ldy + col0 + 8 * l16) = res;
+    }
+}
+
+template <int BITS, int CB>
+int launch_gemm_pc(const PcArgs& a, hipStream_t s)
+{
+    auto kern = gemm_pc_kernel<BITS, CB>;
+    static bool attr_set = false;            // dynamic LDS above 64 KB must be enabled per kernel
+    if (!attr_set) {
+        if (hipFuncSetAttribute((const void*) kern, hipFuncAttributeMaxDynamicSharedMemorySize, PC::LDS) != hipSuccess)
+            return EXL3_ELAUNCH;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL(kern, dim3(a.total), dim3(PC::THREADS), PC::LDS, s, a);
+    return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
+}
+
+// One GEMM launch over `groups` groups sharing M and K: group i reads xh[i] and writes widths[i]
+// columns at y[i] (rows ldy apart).  Operands too large for 32-bit raw-buffer offsets take the
+// 128 x 128 kernel, one launch per group.
+template <int BITS, int CB>
+int launch_trellis_gemm(const uint16_t* const* xh, int64_t ldx, const void* const* trellis, uint16_t* const* y,
+                        int64_t ldy, const uint16_t* const* svh, const int* widths, int groups, int M, int K,
+                        hipStream_t s)
+{
+    bool fits = (uint64_t) M * (uint64_t) ldx * 2 < (1ull << 31);
+    for (int i = 0; i < groups; ++i) fits = fits && (uint64_t) K * widths[i] * BITS / 8 < (1ull << 31);
+    const char* e = getenv("EXL3_GEMM_KERNEL");              // "tile": the 128 x 128 kernel (comparison)
+    if (!fits || (e && e[0] == 't')) {
+        for (int i = 0; i < groups; ++i) {
+            TrellisB<BITS, CB> b{(const uint32_t*) trellis[i], widths[i] / 16};
+            const int rc = launch_gemm<TrellisB<BITS, CB>, false, GEMM_MT, true>(xh[i], ldx, b, nullptr, 0, y[i], ldy,
+                                                                                 svh[i], M, K, widths[i], s);
+            if (rc) return rc;
+        }
+        return EXL3_OK;
+    }
+    PcArgs a{};
+    a.ldx = ldx;
+    a.ldy = ldy;
+    a.M = M;
+    a.K = K;
+    a.groups = groups;
+    const int tiles_m = (M + PC::MT - 1) / PC::MT;
+    int tiles = 0;
+    for (int i = 0; i < groups; ++i) {
+        a.g[i] = {xh[i], (const uint32_t*) trellis[i], svh[i], y[i], widths[i], tiles};
+        tiles += tiles_m * (widths[i] / NT_COLS);
+    }
+    a.total = tiles;
+    a.xcd_remap = a.total % 8 == 0;
+    return launch_gemm_pc<BITS, CB>(a, s);
 }
 
 template <int BITS>
-int launch_trellis_gemm_cb(int cb, const uint16_t* xh, int64_t ldx, const void* tr, uint16_t* y, int64_t ldy,
-                           const uint16_t* svh, int M, int K, int N, hipStream_t s)
+int launch_trellis_gemm_cb(int cb, const uint16_t* const* xh, int64_t ldx, const void* const* tr, uint16_t* const* y,
+                           int64_t ldy, const uint16_t* const* svh, const int* widths, int groups, int M, int K,
+                           hipStream_t s)
 {
-    if (cb == 0) return launch_trellis_gemm<BITS, 0>(xh, ldx, tr, y, ldy, svh, M, K, N, s);
-    if (cb == 1) return launch_trellis_gemm<BITS, 1>(xh, ldx, tr, y, ldy, svh, M, K, N, s);
-    return launch_trellis_gemm<BITS, 2>(xh, ldx, tr, y, ldy, svh, M, K, N, s);
+    if (cb == 0) return launch_trellis_gemm<BITS, 0>(xh, ldx, tr, y, ldy, svh, widths, groups, M, K, s);
+    if (cb == 1) return launch_trellis_gemm<BITS, 1>(xh, ldx, tr, y, ldy, svh, widths, groups, M, K, s);
+    return launch_trellis_gemm<BITS, 2>(xh, ldx, tr, y, ldy, svh, widths, groups, M, K, s);
+}
+
+// x -> per-group xh (input Hadamards), then one GEMM launch over every group's tiles
+int gemm_trellis_common(const void* x, int64_t ldx, const void* const* trellis, uint16_t* const* y, int64_t ldy,
+                        const void* const* suh, uint16_t* xh, const void* const* svh, const int* widths, int groups,
+                        int m, int k, int K, int mcg, int mul1, hipStream_t s)
+{
+    const uint16_t* xhs[EXL3_MAX_GROUPS];
+    const uint16_t* svs[EXL3_MAX_GROUPS];
+    for (int i = 0; i < groups; ++i) {
+        uint16_t* xi = xh + (int64_t) i * m * k;
+        const int rc = exl3_had_r_128(x, ldx, xi, k, m, k, suh[i], nullptr, 1.0f, s);
+        if (rc) return rc;
+        xhs[i] = xi;
+        svs[i] = (const uint16_t*) svh[i];
+    }
+    const int cb = codebook_of(mcg, mul1);
+    switch (K) {
+        case 1: return launch_trellis_gemm_cb<1>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
+        case 2: return launch_trellis_gemm_cb<2>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
+        case 3: return launch_trellis_gemm_cb<3>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
+        case 4: return launch_trellis_gemm_cb<4>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
+        case 5: return launch_trellis_gemm_cb<5>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
+        case 6: return launch_trellis_gemm_cb<6>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
+        case 7: return launch_trellis_gemm_cb<7>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
+        default: return launch_trellis_gemm_cb<8>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
+    }
 }
 
 }  // namespace
@@ -320,23 +654,32 @@ int exl3_gemm_trellis(const void* x, int64_t ldx, const void* trellis, void* y, 
         (((uintptr_t) svh) & 15) || (((uintptr_t) trellis) & 15))
         return EXL3_EINVAL;
     if (m == 0) return EXL3_OK;
-    int rc = exl3_had_r_128(x, ldx, xh, k, m, k, suh, nullptr, 1.0f, stream);
-    if (rc) return rc;
-    const int cb = codebook_of(mcg, mul1);
-    hipStream_t s = (hipStream_t) stream;
-    const uint16_t* xhp = (const uint16_t*) xh;
     uint16_t* yp = (uint16_t*) y;
-    const uint16_t* sv = (const uint16_t*) svh;
-    switch (K) {
-        case 1: return launch_trellis_gemm_cb<1>(cb, xhp, k, trellis, yp, ldy, sv, m, k, n, s);
-        case 2: return launch_trellis_gemm_cb<2>(cb, xhp, k, trellis, yp, ldy, sv, m, k, n, s);
-        case 3: return launch_trellis_gemm_cb<3>(cb, xhp, k, trellis, yp, ldy, sv, m, k, n, s);
-        case 4: return launch_trellis_gemm_cb<4>(cb, xhp, k, trellis, yp, ldy, sv, m, k, n, s);
-        case 5: return launch_trellis_gemm_cb<5>(cb, xhp, k, trellis, yp, ldy, sv, m, k, n, s);
-        case 6: return launch_trellis_gemm_cb<6>(cb, xhp, k, trellis, yp, ldy, sv, m, k, n, s);
-        case 7: return launch_trellis_gemm_cb<7>(cb, xhp, k, trellis, yp, ldy, sv, m, k, n, s);
-        default: return launch_trellis_gemm_cb<8>(cb, xhp, k, trellis, yp, ldy, sv, m, k, n, s);
+    return gemm_trellis_common(x, ldx, &trellis, &yp, ldy, &suh, (uint16_t*) xh, &svh, &n, 1, m, k, K, mcg, mul1,
+                               (hipStream_t) stream);
+}
+
+int exl3_gemm_trellis_grouped(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
+                              const void* const* suh, void* xh, const void* const* svh, const int* widths, int groups,
+                              int m, int k, int K, int mcg, int mul1, void* stream)
+{
+    if (!x || !trellis || !y || !suh || !xh || !svh || !widths || groups < 1 || groups > EXL3_MAX_GROUPS || m < 0 ||
+        K < 1 || K > 8 || k % 128 || k < 128 || ldx < k || ldx % 8 || ldy % 8 || (((uintptr_t) xh) & 15) ||
+        (((uintptr_t) y) & 15))
+        return EXL3_EINVAL;
+    int64_t total = 0;
+    uint16_t* ys[EXL3_MAX_GROUPS];
+    for (int i = 0; i < groups; ++i) {
+        if (!trellis[i] || !suh[i] || !svh[i] || widths[i] < 128 || widths[i] % 128 || (((uintptr_t) svh[i]) & 15) ||
+            (((uintptr_t) trellis[i]) & 15))
+            return EXL3_EINVAL;
+        ys[i] = (uint16_t*) y + total;
+        total += widths[i];
     }
+    if (ldy < total) return EXL3_EINVAL;
+    if (m == 0) return EXL3_OK;
+    return gemm_trellis_common(x, ldx, trellis, ys, ldy, suh, (uint16_t*) xh, svh, widths, groups, m, k, K, mcg, mul1,
+                               (hipStream_t) stream);
 }
 
 int exl3_gemm(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh, void* A_had,

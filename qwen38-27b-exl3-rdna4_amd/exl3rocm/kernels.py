@@ -4,7 +4,7 @@ Each function takes torch tensors, validates shapes the way the reference bindin
 (TORCH_CHECK -> RuntimeError) and calls libexl3_mi355x.so.  Names follow the reference
 extension (`exllamav3_ext`): decode, reconstruct, reconstruct_slice, had_r_128, exl3_gemv,
 exl3_gemv_mr, exl3_gemv_mr_grouped, exl3_gemv_mr_supported, exl3_mgemm, hgemm_recon, exl3_gemm
-(plus exl3_gemv_mr_grouped_widths, which has no reference counterpart).
+(plus exl3_gemv_mr_grouped_widths and exl3_gemm_trellis_grouped, which have no reference counterpart).
 """
 from __future__ import annotations
 
@@ -230,6 +230,28 @@ def exl3_gemm_trellis(A, B, C, suh, xh, svh, K: int, mcg: bool, mul1: bool) -> N
     L.check(L.lib().exl3_gemm_trellis(x2.data_ptr(), x2.stride(0) if m > 1 else k, B.data_ptr(), C.data_ptr(),
                                       _ldy(C, n), suh.data_ptr(), xh.data_ptr(), svh.data_ptr(), m, k, n, K,
                                       *_cb_flags(mcg, mul1), _stream(A)), "exl3_gemm_trellis")
+
+
+def exl3_gemm_trellis_grouped(A, B: Sequence[torch.Tensor], C, suh: Sequence[torch.Tensor], xh,
+                              svh: Sequence[torch.Tensor], K: int, mcg: bool, mul1: bool) -> None:
+    """Prefill of groups of any widths sharing x and K (q/k/v, gate/up) with one GEMM launch; group i
+    writes the columns after groups 0..i-1 of C.  xh: fp16 scratch of groups * m * k elements.
+    No counterpart in the reference extension (its linear_groups runs one prefill per group)."""
+    _cuda(A, C, xh, *B, *suh, *svh)
+    x2, m, k = _rows(A)
+    g = len(B)
+    widths = [int(s.shape[0]) for s in svh]
+    _need(1 <= g <= L.MAX_GROUPS and len(suh) == g and len(svh) == g, "grouped: 1..4 groups with suh/svh each")
+    _need(C.shape[-1] >= sum(widths), "grouped: output narrower than the groups")
+    _need(xh.numel() >= g * m * k and xh.dtype == torch.float16 and xh.is_contiguous(),
+          "grouped gemm: xh scratch [groups, m, k] fp16")
+    wa = (C_int * g)(*widths)
+    pt, _a = L.ptr_array([b.data_ptr() for b in B])
+    ps, _b = L.ptr_array([s.data_ptr() for s in suh])
+    pv, _c = L.ptr_array([s.data_ptr() for s in svh])
+    L.check(L.lib().exl3_gemm_trellis_grouped(x2.data_ptr(), x2.stride(0) if m > 1 else k, pt, C.data_ptr(),
+                                              _ldy(C, sum(widths)), ps, xh.data_ptr(), pv, wa, g, m, k, K,
+                                              *_cb_flags(mcg, mul1), _stream(A)), "exl3_gemm_trellis_grouped")
 
 
 def exl3_gemm(A, B, C, suh, A_had, svh, force_shape_idx: int = -1, mcg: bool = False, mul1: bool = True,

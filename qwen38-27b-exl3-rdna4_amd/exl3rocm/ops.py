@@ -8,8 +8,9 @@ Routing by rows M:
   M <= EXL3_MR_MAX (32)  -> fused GEMV (input Hadamard, trellis decode + MFMA dot, split-K
                             reduction and output Hadamard in one launch); every row is bitwise
                             equal to the M == 1 call of that row
-  M  > EXL3_MR_MAX       -> prefill GEMM (trellis decoded into LDS, fp16 MFMA, fp32 accumulate)
-                            between standalone input / output Hadamards; EXL3_PREFILL=recon takes
+  M  > EXL3_MR_MAX       -> input Hadamard pass, then the prefill GEMM (trellis decoded into LDS,
+                            fp16 MFMA, fp32 accumulate, output Hadamard and svh in its epilogue);
+                            a fused module's groups share one GEMM launch; EXL3_PREFILL=recon takes
                             the reference's reconstruct + hgemm route instead
 """
 from __future__ import annotations
@@ -156,10 +157,23 @@ def exl3_linear_groups(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[t
             n0 += sum(widths[i:j])
             i = j
         return y.view(*x.shape[:-1], n0)
-    n0 = 0
-    for t, su, sv, kk, w in zip(trellis, suh, svh, K, widths):
-        _linear_into(x2, t, su, sv, kk, mcg, mul1, y[:, n0:n0 + w])
-        n0 += w
+    # prefill: runs of consecutive groups with equal K share one GEMM launch (each group its own
+    # rotated input); the recon route keeps the reference's one-group-at-a-time path
+    i, n0 = 0, 0
+    while i < ng:
+        j = i + 1
+        while j < ng and j - i < _lib.MAX_GROUPS and K[j] == K[i]:
+            j += 1
+        if j - i > 1 and PREFILL_ROUTE != "recon":
+            xh = torch.empty((j - i, M, k), dtype=torch.float16, device=x.device)
+            E.exl3_gemm_trellis_grouped(x2, list(trellis[i:j]), y[:, n0:], list(suh[i:j]), xh, list(svh[i:j]),
+                                        K[i], mcg, mul1)
+        else:
+            for g in range(i, j):
+                _linear_into(x2, trellis[g], suh[g], svh[g], K[g], mcg, mul1, y[:, n0 + sum(widths[i:g]):
+                                                                               n0 + sum(widths[i:g + 1])])
+        n0 += sum(widths[i:j])
+        i = j
     return y.view(*x.shape[:-1], n0)
 
 

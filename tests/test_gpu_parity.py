@@ -352,6 +352,45 @@ def test_prefill_wide_ragged_parity():
     assert_close(gpu_linear(x, tr, su, sv, bits, 2), cpu.linear(x, tr, bits, su, sv, 2), (m, k, n, bits))
 
 
+@pytest.mark.parametrize("widths,bits,cb", [((512, 128, 128), 4, 2), ((256, 256), 3, 1), ((128, 384, 256, 128), 5, 0)])
+def test_prefill_grouped_widths_parity(widths, bits, cb):
+    """One grouped prefill launch over groups of mixed widths (q/k/v shape) with a ragged row count:
+    every group's columns match the oracle, and are bitwise equal to that group's own prefill."""
+    m, k = 300, 512
+    mats = [synth.layer("pfg", i, k, n, bits) for i, n in enumerate(widths)]
+    x = synth.activations(synth.key_of("pfg", "x", m), m, k)
+    X = to_dev(x)[0]
+    Ts = [to_dev(t.view(np.int16))[0] for t, _, _ in mats]
+    SUs = [to_dev(su)[0] for _, su, _ in mats]
+    SVs = [to_dev(sv)[0] for _, _, sv in mats]
+    y = torch.empty(m, sum(widths) + 64, dtype=torch.float16, device=DEV)[:, :sum(widths)]   # row stride > width
+    xh = torch.empty(len(widths), m, k, dtype=torch.float16, device=DEV)
+    E.exl3_gemm_trellis_grouped(X, Ts, y, SUs, xh, SVs, bits, cb == 1, cb == 2)
+    n0 = 0
+    for (tr, su, sv), T, SU, SV, n in zip(mats, Ts, SUs, SVs, widths):
+        single = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, cb == 1, cb == 2)
+        assert torch.equal(y[:, n0:n0 + n].view(torch.int16), single.view(torch.int16)), (widths, n0)
+        assert_close(y[:, n0:n0 + n].cpu().numpy(), cpu.linear(x, tr, bits, su, sv, cb), (widths, n0))
+        n0 += n
+
+
+def test_linear_groups_prefill_matches_per_group_linear():
+    """linear_groups at M > 32 (one grouped GEMM launch per equal-K run, mixed bitrates split into
+    runs) == the concatenation of per-group linear calls, bitwise."""
+    k, m = 1024, 80
+    spec = [(512, 4), (256, 4), (256, 4), (384, 3)]
+    mats = [synth.layer("pfl", i, k, n, K) for i, (n, K) in enumerate(spec)]
+    Ts = [to_dev(t.view(np.int16))[0] for t, _, _ in mats]
+    SUs = [to_dev(su)[0] for _, su, _ in mats]
+    SVs = [to_dev(sv)[0] for _, _, sv in mats]
+    Ks = [K for _, K in spec]
+    X = to_dev(synth.activations(synth.key_of("pfl", "x"), m, k))[0]
+    yg = torch.ops.exl3rocm.linear_groups(X, Ts, SUs, SVs, Ks, False, True)
+    ys = torch.cat([torch.ops.exl3rocm.linear(X, T, SU, SV, K, False, True) for T, SU, SV, K in zip(Ts, SUs, SVs, Ks)],
+                   dim=1)
+    assert torch.equal(yg.view(torch.int16), ys.view(torch.int16))
+
+
 @pytest.mark.parametrize("m,k,n", [(96, 1024, 512), (512, 256, 65536)])
 def test_recon_route_matches_fused_route(m, k, n):
     """reconstruct + hgemm_recon + output transform == the fused prefill route, bitwise (same
