@@ -141,6 +141,7 @@ struct GemvGroup {
     int max_seg;               // partial slots per workgroup
     int64_t part_off;          // first partial (floats) of this group
     int cnt_off;               // first completion counter of this group
+    int h;                     // its workgroups dispatched first on their CU (weight wa; the rest wb)
 };
 
 struct GemvArgs {
@@ -151,6 +152,7 @@ struct GemvArgs {
     const int64_t* tab_suh;     // replace g[i].trellis / suh / svh
     const int64_t* tab_svh;
     int groups, M, k, UPB;
+    int wa, wb;                // unit-split weights of first-dispatched / second workgroups on a CU
     int chunk_units;           // units whose rotated input fits the LDS at once
     int64_t ldy;
     float* part;               // per group: [G][max_seg][M][128] fp32 partials
@@ -172,9 +174,41 @@ __device__ __forceinline__ void wait_stores_complete()
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-__device__ __forceinline__ int wg_lo(int w, int U, int G) { return (int) ((int64_t) w * U / G); }
-// workgroup owning unit u: the largest w with floor(w*U/G) <= u
-__device__ __forceinline__ int wg_of_unit(int u, int U, int G) { return (int) (((int64_t) (u + 1) * G - 1) / U); }
+// a wave-uniform 64-bit value as a scalar (readfirstlane of both halves)
+__device__ __forceinline__ int64_t uniform_i64(int64_t v)
+{
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) v);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) ((uint64_t) v >> 32));
+    return (int64_t) (((uint64_t) hi << 32) | lo);
+}
+
+// Unit split of a group's U units over its G workgroups: workgroup w owns [lo(w), lo(w + 1)),
+// lo(w) = floor(U * S(w) / S(G)) with S(w) = wa * min(w, h) + wb * max(w - h, 0).  The first h
+// workgroups of the group are dispatched first on their CU; the SIMD arbiter favours their (older)
+// waves, so they get the larger weight wa and both waves of a CU finish their units together.  A
+// function of the shape only (never of m): rows stay bitwise equal to the m == 1 call.
+struct Split {
+    int U, G, h, wa, wb;
+    __host__ __device__ int64_t S(int w) const
+    {
+        return (int64_t) wa * (w < h ? w : h) + (int64_t) wb * (w > h ? w - h : 0);
+    }
+    __host__ __device__ int lo(int w) const { return (int) ((int64_t) U * S(w) / S(G)); }
+    // the workgroup owning unit u: the largest w in [0, G) with lo(w) <= u, i.e. S(w) <= T
+    __host__ __device__ int owner(int u) const
+    {
+        const int64_t SG = S(G);
+        const int64_t T = ((int64_t) (u + 1) * SG + U - 1) / U - 1;
+        const int w = T < (int64_t) wa * h ? (int) (T / wa) : h + (int) ((T - (int64_t) wa * h) / wb);
+        return w < G - 1 ? w : G - 1;
+    }
+    // most units any workgroup owns
+    __host__ __device__ int max_units() const
+    {
+        const int wmax = wa > wb ? wa : wb;
+        return (int) (((int64_t) U * wmax + S(G) - 1) / S(G)) + 1;
+    }
+};
 
 
 // Two workgroups (8 waves) per CU are resident at once: up to 256 registers per lane, enough for
@@ -197,14 +231,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     const int w = blockIdx.x - gg.wg0;
     const int G = gg.G, UPB = a.UPB, M = a.M;
     const int NB = gg.n / 128, NT = gg.n / 16, U = NB * UPB;
+    const Split sp{U, G, gg.h, a.wa, a.wb};
     const uint32_t* trel = gg.trellis;
     const uint16_t* suh = gg.suh;
     const uint16_t* svh = gg.svh;
     uint16_t* y = gg.y;
     if (a.tab_trellis) {
-        trel = reinterpret_cast<const uint32_t*>(a.tab_trellis[grp]);
-        suh = reinterpret_cast<const uint16_t*>(a.tab_suh[grp]);
-        svh = reinterpret_cast<const uint16_t*>(a.tab_svh[grp]);
+        // table entries are uniform (grp is): keep them in scalar registers, or the trellis buffer
+        // resource would look divergent and every buffer load would be wrapped in a waterfall loop
+        trel = reinterpret_cast<const uint32_t*>(uniform_i64(a.tab_trellis[grp]));
+        suh = reinterpret_cast<const uint16_t*>(uniform_i64(a.tab_suh[grp]));
+        svh = reinterpret_cast<const uint16_t*>(uniform_i64(a.tab_svh[grp]));
     }
     uint32_t* const counters = a.counters + gg.cnt_off;
     // the trellis as one raw buffer (layers of 4 GiB and more are declined on the host)
@@ -222,7 +259,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     uint16_t* lds_c = smem + a.chunk_units * UROWS * A_ROW;   // [M][A_ROW]
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int g = lane >> 4, j = lane & 15, q = j & 7;
-    const int ulo = wg_lo(w, U, G), uhi = wg_lo(w + 1, U, G);
+    const int ulo = sp.lo(w), uhi = sp.lo(w + 1);
     if (ulo >= uhi) return;                                   // uniform per workgroup
     const int seg0_cb = ulo / UPB;
     float* part_grp = a.part + gg.part_off;
@@ -436,7 +473,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
         const int nb = min(256, nblk - b0);
         if ((int) threadIdx.x < nb) {                         // one counter per thread, all in flight
             const int cb = seg0_cb + b0 + threadIdx.x;
-            const int wf = wg_of_unit(cb * UPB, U, G), wl = wg_of_unit(cb * UPB + UPB - 1, U, G);
+            const int wf = sp.owner(cb * UPB), wl = sp.owner(cb * UPB + UPB - 1);
             const uint32_t prev = __hip_atomic_fetch_add(&counters[cb], 1u, __ATOMIC_RELAXED,
                                                          __HIP_MEMORY_SCOPE_AGENT);
             s_last[threadIdx.x] = prev == (uint32_t) (wl - wf) ? 1 : 0;
@@ -452,14 +489,22 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
         const int nred = __builtin_amdgcn_readfirstlane(s_nred);
         for (int r0 = 0; r0 < nred; r0 += RB) {
             const int rb = min(RB, nred - r0);
+            // svh of the first output-transform pass, requested before the partial loads so that its
+            // round trip overlaps theirs
+            const int l16 = threadIdx.x & 15;
+            u32x4 sv_first = {0u, 0u, 0u, 0u};
+            {
+                const int rr = threadIdx.x >> 4;
+                if (rr < rb * M) sv_first = *reinterpret_cast<gc_u32x4*>(gsvh + s_list[r0 + rr / M] * 128 + 8 * l16);
+            }
             // contributor wf holds block cb in its segment cb - first_cb(wf); every later
             // contributor starts inside cb, so its segment is 0.  Loads go out in batches of
             // RED_BATCH; the sum runs in contributor order.
             for (int e = threadIdx.x; e < rb * M * 128; e += 256) {
                 const int r = e / (M * 128), el = e - r * (M * 128);
                 const int cb = s_list[r0 + r];
-                const int wf = wg_of_unit(cb * UPB, U, G), wl = wg_of_unit(cb * UPB + UPB - 1, U, G);
-                const int seg_f = cb - wg_lo(wf, U, G) / UPB;
+                const int wf = sp.owner(cb * UPB), wl = sp.owner(cb * UPB + UPB - 1);
+                const int seg_f = cb - sp.lo(wf) / UPB;
                 const int nc = wl - wf + 1;
                 float sum = 0.f;
                 for (int cc0 = 0; cc0 < nc; cc0 += RED_BATCH) {
@@ -483,7 +528,6 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                                    __HIP_MEMORY_SCOPE_AGENT);
             __syncthreads();
             // output Hadamard + svh: 16 lanes per (block, row)
-            const int l16 = threadIdx.x & 15;
             for (int rr0 = 0; rr0 < rb * M; rr0 += 16) {
                 const int rr = rr0 + (threadIdx.x >> 4);
                 const bool live = rr < rb * M;
@@ -492,7 +536,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 u32x4 c = {0u, 0u, 0u, 0u}, sv = c;
                 if (live) {
                     c = *reinterpret_cast<const u32x4*>(lds_c + rr * A_ROW + 8 * l16);
-                    sv = *reinterpret_cast<gc_u32x4*>(gsvh + cb * 128 + 8 * l16);
+                    sv = rr0 == 0 ? sv_first : *reinterpret_cast<gc_u32x4*>(gsvh + cb * 128 + 8 * l16);
                 }
                 const u32x4 res = had128_x8(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, R_SCALE);
                 if (live) *reinterpret_cast<g_u32x4*>(gy + (int64_t) m * a.ldy + cb * 128 + 8 * l16) = res;
@@ -519,7 +563,8 @@ int codebook_of(int mcg, int mul1) { return mul1 ? 2 : (mcg ? 1 : 0); }
 // so every row of an m-row call is bitwise equal to the m == 1 call, and a module's grouped
 // launches agree across row counts.  The groups share the resident workgroup slots in proportion
 // to their units; each keeps its own workgroup range, partial slots and completion counters.
-constexpr int RESIDENT_WGS = 256 * WAVES_PER_SIMD;   // 256 CUs x workgroups per CU
+constexpr int NUM_CUS = 256;                          // MI355X
+constexpr int RESIDENT_WGS = NUM_CUS * WAVES_PER_SIMD;   // workgroups per CU x CUs
 
 struct GridPlan {
     int groups;
@@ -528,13 +573,21 @@ struct GridPlan {
     int total_wgs, counters;
     int64_t slots;
     int max_per;                         // most units any workgroup owns
+    int h[EXL3_MAX_GROUPS], wa, wb;      // unit-split weights (Split)
 };
 
-int max_segments(int UPB, int n, int G)
+// Unit-split weights of first-dispatched / second workgroups on a CU: the measured issue share of
+// an older wave on a SIMD shared by two (EXL3_GEMV_WEIGHTS="a,b" overrides, for measurement)
+void split_weights(int& wa, int& wb)
 {
-    const int64_t U = (int64_t) (n / 128) * UPB;
-    const int64_t per = (U + G - 1) / G;
-    return (int) ((per + UPB - 1) / UPB + 1);
+    wa = 3;
+    wb = 2;
+    const char* e = getenv("EXL3_GEMV_WEIGHTS");
+    int a = 0, b = 0;
+    if (e && sscanf(e, "%d,%d", &a, &b) == 2 && a >= 1 && b >= 1 && a <= 64 && b <= 64) {
+        wa = a;
+        wb = b;
+    }
 }
 
 GridPlan plan_grid(int k, const int* widths, int groups)
@@ -550,17 +603,33 @@ GridPlan plan_grid(int k, const int* widths, int groups)
     const int64_t min_units = std::max<int64_t>(1, (UPB + max_contrib - 1) / max_contrib);
     int64_t Gt = forced > 0 ? (int64_t) forced * groups : std::min<int64_t>(RESIDENT_WGS, Utot / min_units);
     Gt = std::max<int64_t>(Gt, groups);
+    split_weights(p.wa, p.wb);
+    int Gs[EXL3_MAX_GROUPS], gsum = 0;
+    for (int i = 0; i < groups; ++i) {
+        const int64_t Ui = (int64_t) (widths[i] / 128) * UPB;
+        Gs[i] = (int) std::max<int64_t>(1, std::min<int64_t>(Ui, (Gt * Ui + Utot / 2) / Utot));
+        gsum += Gs[i];
+    }
+    // workgroups [0, NUM_CUS) of the grid are the first on their CU; with at most one per CU all
+    // are, and the split is uniform
+    const int first = gsum > NUM_CUS ? NUM_CUS : gsum;
     int wg = 0, cnt = 0;
     int64_t slots = 0;
     for (int i = 0; i < groups; ++i) {
-        const int64_t Ui = (int64_t) (widths[i] / 128) * UPB;
-        const int64_t Gi = std::max<int64_t>(1, std::min<int64_t>(Ui, (Gt * Ui + Utot / 2) / Utot));
-        p.G[i] = (int) Gi;
+        const int Ui = (widths[i] / 128) * UPB;
+        p.G[i] = Gs[i];
         p.wg0[i] = wg;
-        p.max_seg[i] = max_segments(UPB, widths[i], p.G[i]);
+        // weighted only where every workgroup still gets a unit (U * min(wa, wb) >= max(wa, wb) * G;
+        // the completion count assumes each workgroup between a block's first and last owner
+        // contributes to it)
+        const bool weighted = (int64_t) Ui * std::min(p.wa, p.wb) >= (int64_t) std::max(p.wa, p.wb) * Gs[i];
+        p.h[i] = weighted ? std::min(std::max(first - wg, 0), Gs[i]) : Gs[i];
+        const Split sp{Ui, Gs[i], p.h[i], p.wa, p.wb};
+        const int per = sp.max_units();
+        p.max_seg[i] = (per + UPB - 1) / UPB + 1;
         p.cnt_off[i] = cnt;
         p.slot_off[i] = slots;
-        p.max_per = std::max<int>(p.max_per, (int) ((Ui + Gi - 1) / Gi));
+        p.max_per = std::max(p.max_per, per);
         wg += p.G[i];
         cnt += widths[i] / 128;
         slots += (int64_t) p.G[i] * p.max_seg[i];
@@ -672,7 +741,10 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
         a.g[i].max_seg = p.max_seg[i];
         a.g[i].part_off = p.slot_off[i] * m * 128;
         a.g[i].cnt_off = p.cnt_off[i];
+        a.g[i].h = p.h[i];
     }
+    a.wa = p.wa;
+    a.wb = p.wb;
     if (tabs) {
         a.tab_trellis = tabs[0];
         a.tab_suh = tabs[1];
