@@ -147,10 +147,18 @@ int exl3_gemm_trellis(const void* x, int64_t ldx, const void* trellis, void* y, 
  * elements (each group's rotated input).  No counterpart in the reference: its linear_groups runs
  * one prefill per group (reference vllm_plugin/exl3rocm/ops.py:171-175).  Callers: exl3rocm's
  * linear_groups for M > 32.  All groups' output tiles share one GEMM launch, so a module fills the
- * GPU as one layer would. */
+ * GPU as one layer would.  workspace / ws_bytes: see exl3_gemm_trellis_workspace_size. */
 int exl3_gemm_trellis_grouped(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
                               const void* const* suh, void* xh, const void* const* svh, const int* widths, int groups,
-                              int m, int k, int K, int mcg, int mul1, void* stream);
+                              int m, int k, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
+                              void* stream);
+
+/* Workspace bytes exl3_gemm_trellis_grouped uses to balance the launch's last, partial wave of
+ * output tiles (those tiles are split along K; fp32 partials and completion counters).  0 when the
+ * shape needs none.  Zero before the first call; every call leaves its counters zero.  With a
+ * smaller or NULL workspace the tail is not split: the same results to the tolerance, less
+ * balance.  No reference counterpart (the reference prefill has no split). */
+size_t exl3_gemm_trellis_workspace_size(int m, int k, const int* widths, int groups);
 
 /* Dispatcher by row count: m <= 32 -> fused GEMV, else the prefill GEMM.  Returns the route
  * tag (1 = GEMV, 2 = prefill GEMM) or a negative error.

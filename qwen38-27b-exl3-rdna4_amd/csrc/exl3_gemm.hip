@@ -14,6 +14,8 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
+
 using namespace exl3;
 
 namespace {
@@ -315,6 +317,14 @@ struct PcGroup {
 struct PcArgs {
     int64_t ldx, ldy;
     int M, K, groups, total, xcd_remap;
+    // Balanced tail: items [0, n_full) are whole tiles; every later tile (the last, partial wave of
+    // a plain tile grid) is split along K into `split` pieces (split == 1: no split).  A piece
+    // leaves its fp32 partial tile in `part`; the last of a tile's pieces (completion counter)
+    // adds them in piece order and applies the epilogue.
+    int n_full, split;
+    f32x4* part;                // [(tiles - n_full) * split][32][256] partial tiles
+    uint32_t part_bytes;        // their size (the raw buffer's range)
+    uint32_t* counters;         // [tiles - n_full], zero between calls (the last piece resets)
     PcGroup g[EXL3_MAX_GROUPS];
 };
 
@@ -348,9 +358,18 @@ template <int BITS, int CB>
 __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
 {
     extern __shared__ __align__(16) char lds[];
+    __shared__ int s_last;
     const int t = threadIdx.x;
-    int u = blockIdx.x;
-    if (a.xcd_remap) u = (u & 7) * (a.total / 8) + (u >> 3);    // consecutive tiles share an XCD
+    const int b = blockIdx.x;
+    const bool piece = b >= a.n_full;
+    int u, q = 0;
+    if (!piece) {
+        u = a.xcd_remap ? (b & 7) * (a.n_full / 8) + (b >> 3) : b;    // consecutive tiles share an XCD
+    } else {
+        const int bb = b - a.n_full;
+        u = a.n_full + bb / a.split;
+        q = bb - (bb / a.split) * a.split;
+    }
     // constant indices only into the kernel-argument struct (a runtime index copies it to scratch)
     int gi = 0;
     if (a.groups > 1 && u >= a.g[1].tile0) gi = 1;
@@ -360,9 +379,20 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
     const int tiles_n = gg.n / NT_COLS, v = u - gg.tile0;
     const int tm = v / tiles_n, tn = v - tm * tiles_n;
     const int row0 = tm * PC::MT, col0 = tn * NT_COLS;
-    const int steps = a.K / KSTEP, M = a.M;
+    const int M = a.M;
+    // K steps [sb, sb + steps) of the tile (all of them unless this item is a piece)
+    const int all_steps = a.K / KSTEP;
+    const int sb = piece ? q * all_steps / a.split : 0;
+    const int steps = piece ? (q + 1) * all_steps / a.split - sb : all_steps;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
     auto stage = [&](int s) __attribute__((always_inline)) { return lds + (s & 1) * PC::BUF; };
+    // partial tile of piece pq of this tile: consumer thread t's 32 accumulator quads, 16 B apart
+    // per thread (coalesced); system-coherent (sc1) accesses, read by another CU after the counter
+    const int tile_r = u - a.n_full;
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(a.part, 0, (int) a.part_bytes, RAW_BUFFER_FLAGS);
+    auto part_off = [&](int pq, int ij) __attribute__((always_inline)) {
+        return (uint32_t) ((((tile_r * a.split + pq) * 32 + ij) * 256 + t) * 16);
+    };
 
     if (wave < 4) {
         // ---- consumer ---------------------------------------------------------------------
@@ -424,6 +454,39 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
             mm(A1, 1, B1);
             __builtin_amdgcn_sched_barrier(0);
         }
+        if (piece) {
+            // this piece's partial out; then count the pieces in, and the last one sums them all
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), prs,
+                                                           part_off(q, i * 8 + j), 0, 0x10);
+            __builtin_amdgcn_s_waitcnt(0x0F70);            // vmcnt(0): the partial has landed
+            __syncthreads();
+            if (t == 0) {
+                const uint32_t prev = __hip_atomic_fetch_add(&a.counters[tile_r], 1u, __ATOMIC_RELAXED,
+                                                             __HIP_MEMORY_SCOPE_AGENT);
+                s_last = prev == (uint32_t) (a.split - 1);
+                if (s_last) __hip_atomic_store(&a.counters[tile_r], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            __syncthreads();
+            if (!s_last) return;                           // uniform: the whole workgroup leaves
+            // C = sum of the pieces' partials in piece order (this piece's own from registers)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
+                    for (int pq = 0; pq < a.split; ++pq) {
+                        const f32x4 v = pq == q ? acc[i][j]
+                                                : __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                                prs, part_off(pq, i * 8 + j), 0, 0x10));
+                        sum = pq == 0 ? v : sum + v;
+                    }
+                    acc[i][j] = sum;
+                }
+        }
         // C = fp16(acc) into LDS: every read and write of the stages finished before the last B_s
         uint16_t* ct = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
@@ -457,7 +520,7 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
         auto load_a = [&](int st, u32x4* A) __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                A[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, aoff[i], st * (KSTEP * 2), 0));
+                A[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, aoff[i], (sb + st) * (KSTEP * 2), 0));
         };
         auto store_a = [&](char* stg, const u32x4* A) __attribute__((always_inline)) {
 #pragma unroll
@@ -475,7 +538,7 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
         const uint32_t off_prev = (tile_w + (q == 0 ? 8 * BITS - 1 : q * BITS - 1)) * 4u;
         const uint32_t step_bytes = (uint32_t) nt_total * 4u * 32u * BITS;   // 4 k-tile rows
         auto fetch = [&](int st, uint32_t* W) __attribute__((always_inline)) {
-            load_qblock_buf<BITS>(trs, off_main, off_prev, (uint32_t) st * step_bytes, W);
+            load_qblock_buf<BITS>(trs, off_main, off_prev, (uint32_t) (sb + st) * step_bytes, W);
         };
         // B fragment tile ks * 8 + ntl, lanes XOR-swizzled by n-tile (conflict-free stores)
         auto decode_store = [&](const uint32_t* W, char* stg) __attribute__((always_inline)) {
@@ -525,6 +588,11 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
         if (s < steps) interval(s, R1, X1, R0, X0);
         if (s + 1 < steps) interval(s + 1, R2, X2, R1, X1);
         __builtin_amdgcn_s_setprio(0);
+        if (piece) {                                       // the consumers' two completion barriers
+            __syncthreads();
+            __syncthreads();
+            if (!s_last) return;
+        }
     }
     __syncthreads();                                       // C tile complete in LDS
 
@@ -542,7 +610,7 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
 }
 
 template <int BITS, int CB>
-int launch_gemm_pc(const PcArgs& a, hipStream_t s)
+int launch_gemm_pc(const PcArgs& a, int items, hipStream_t s)
 {
     auto kern = gemm_pc_kernel<BITS, CB>;
     static bool attr_set = false;            // dynamic LDS above 64 KB must be enabled per kernel
@@ -551,17 +619,44 @@ int launch_gemm_pc(const PcArgs& a, hipStream_t s)
             return EXL3_ELAUNCH;
         attr_set = true;
     }
-    hipLaunchKernelGGL(kern, dim3(a.total), dim3(PC::THREADS), PC::LDS, s, a);
+    hipLaunchKernelGGL(kern, dim3(items), dim3(PC::THREADS), PC::LDS, s, a);
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
+}
+
+// Tile plan of one producer/consumer launch: whole tiles for every full wave over the CUs (one
+// workgroup per CU), the last, partial wave's tiles split along K into up to CUs / tail pieces of
+// at least 8 K steps, so the launch ends in balance.  A function of the shape only.
+constexpr int PC_CUS = 256;                    // MI355X compute units
+constexpr size_t PC_COUNTER_BYTES = 4096;      // workspace head: completion counters of split tiles
+constexpr size_t PC_PIECE_BYTES = (size_t) PC::MT * NT_COLS * 4;   // one fp32 partial tile
+
+struct PcPlan {
+    int tiles, n_full, split;
+    size_t ws_bytes;                           // 0: no split
+};
+
+PcPlan pc_plan(int M, int K, const int* widths, int groups)
+{
+    PcPlan p{};
+    const int tiles_m = (M + PC::MT - 1) / PC::MT;
+    for (int i = 0; i < groups; ++i) p.tiles += tiles_m * (widths[i] / NT_COLS);
+    const int full = p.tiles / PC_CUS, tail = p.tiles - full * PC_CUS;
+    p.split = 1;
+    if (full >= 1 && tail > 0) p.split = std::min(PC_CUS / tail, (K / KSTEP) / 8);
+    if (p.split < 2) p.split = 1;
+    p.n_full = p.split > 1 ? full * PC_CUS : p.tiles;
+    p.ws_bytes = p.split > 1 ? PC_COUNTER_BYTES + (size_t) (p.tiles - p.n_full) * p.split * PC_PIECE_BYTES : 0;
+    return p;
 }
 
 // One GEMM launch over `groups` groups sharing M and K: group i reads xh[i] and writes widths[i]
 // columns at y[i] (rows ldy apart).  Operands too large for 32-bit raw-buffer offsets take the
-// 128 x 128 kernel, one launch per group.
+// 128 x 128 kernel, one launch per group.  Without a workspace of the plan's size the tail is not
+// split (same results, less balance).
 template <int BITS, int CB>
 int launch_trellis_gemm(const uint16_t* const* xh, int64_t ldx, const void* const* trellis, uint16_t* const* y,
                         int64_t ldy, const uint16_t* const* svh, const int* widths, int groups, int M, int K,
-                        hipStream_t s)
+                        void* ws, size_t ws_bytes, hipStream_t s)
 {
     bool fits = (uint64_t) M * (uint64_t) ldx * 2 < (1ull << 31);
     for (int i = 0; i < groups; ++i) fits = fits && (uint64_t) K * widths[i] * BITS / 8 < (1ull << 31);
@@ -574,6 +669,11 @@ int launch_trellis_gemm(const uint16_t* const* xh, int64_t ldx, const void* cons
             if (rc) return rc;
         }
         return EXL3_OK;
+    }
+    PcPlan pl = pc_plan(M, K, widths, groups);
+    if (pl.split > 1 && (!ws || ws_bytes < pl.ws_bytes || pl.ws_bytes - PC_COUNTER_BYTES >= (1ull << 31))) {
+        pl.split = 1;
+        pl.n_full = pl.tiles;
     }
     PcArgs a{};
     a.ldx = ldx;
@@ -588,24 +688,31 @@ int launch_trellis_gemm(const uint16_t* const* xh, int64_t ldx, const void* cons
         tiles += tiles_m * (widths[i] / NT_COLS);
     }
     a.total = tiles;
-    a.xcd_remap = a.total % 8 == 0;
-    return launch_gemm_pc<BITS, CB>(a, s);
+    a.n_full = pl.n_full;
+    a.split = pl.split;
+    a.xcd_remap = a.n_full % 8 == 0;
+    if (pl.split > 1) {
+        a.counters = (uint32_t*) ws;
+        a.part = (f32x4*) ((char*) ws + PC_COUNTER_BYTES);
+        a.part_bytes = (uint32_t) (pl.ws_bytes - PC_COUNTER_BYTES);
+    }
+    return launch_gemm_pc<BITS, CB>(a, a.n_full + (tiles - a.n_full) * a.split, s);
 }
 
 template <int BITS>
 int launch_trellis_gemm_cb(int cb, const uint16_t* const* xh, int64_t ldx, const void* const* tr, uint16_t* const* y,
                            int64_t ldy, const uint16_t* const* svh, const int* widths, int groups, int M, int K,
-                           hipStream_t s)
+                           void* ws, size_t wsb, hipStream_t s)
 {
-    if (cb == 0) return launch_trellis_gemm<BITS, 0>(xh, ldx, tr, y, ldy, svh, widths, groups, M, K, s);
-    if (cb == 1) return launch_trellis_gemm<BITS, 1>(xh, ldx, tr, y, ldy, svh, widths, groups, M, K, s);
-    return launch_trellis_gemm<BITS, 2>(xh, ldx, tr, y, ldy, svh, widths, groups, M, K, s);
+    if (cb == 0) return launch_trellis_gemm<BITS, 0>(xh, ldx, tr, y, ldy, svh, widths, groups, M, K, ws, wsb, s);
+    if (cb == 1) return launch_trellis_gemm<BITS, 1>(xh, ldx, tr, y, ldy, svh, widths, groups, M, K, ws, wsb, s);
+    return launch_trellis_gemm<BITS, 2>(xh, ldx, tr, y, ldy, svh, widths, groups, M, K, ws, wsb, s);
 }
 
 // x -> per-group xh (input Hadamards), then one GEMM launch over every group's tiles
 int gemm_trellis_common(const void* x, int64_t ldx, const void* const* trellis, uint16_t* const* y, int64_t ldy,
                         const void* const* suh, uint16_t* xh, const void* const* svh, const int* widths, int groups,
-                        int m, int k, int K, int mcg, int mul1, hipStream_t s)
+                        int m, int k, int K, int mcg, int mul1, void* ws, size_t wsb, hipStream_t s)
 {
     const uint16_t* xhs[EXL3_MAX_GROUPS];
     const uint16_t* svs[EXL3_MAX_GROUPS];
@@ -618,14 +725,14 @@ int gemm_trellis_common(const void* x, int64_t ldx, const void* const* trellis, 
     }
     const int cb = codebook_of(mcg, mul1);
     switch (K) {
-        case 1: return launch_trellis_gemm_cb<1>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
-        case 2: return launch_trellis_gemm_cb<2>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
-        case 3: return launch_trellis_gemm_cb<3>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
-        case 4: return launch_trellis_gemm_cb<4>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
-        case 5: return launch_trellis_gemm_cb<5>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
-        case 6: return launch_trellis_gemm_cb<6>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
-        case 7: return launch_trellis_gemm_cb<7>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
-        default: return launch_trellis_gemm_cb<8>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, s);
+        case 1: return launch_trellis_gemm_cb<1>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, ws, wsb, s);
+        case 2: return launch_trellis_gemm_cb<2>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, ws, wsb, s);
+        case 3: return launch_trellis_gemm_cb<3>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, ws, wsb, s);
+        case 4: return launch_trellis_gemm_cb<4>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, ws, wsb, s);
+        case 5: return launch_trellis_gemm_cb<5>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, ws, wsb, s);
+        case 6: return launch_trellis_gemm_cb<6>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, ws, wsb, s);
+        case 7: return launch_trellis_gemm_cb<7>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, ws, wsb, s);
+        default: return launch_trellis_gemm_cb<8>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, ws, wsb, s);
     }
 }
 
@@ -656,12 +763,20 @@ int exl3_gemm_trellis(const void* x, int64_t ldx, const void* trellis, void* y, 
     if (m == 0) return EXL3_OK;
     uint16_t* yp = (uint16_t*) y;
     return gemm_trellis_common(x, ldx, &trellis, &yp, ldy, &suh, (uint16_t*) xh, &svh, &n, 1, m, k, K, mcg, mul1,
-                               (hipStream_t) stream);
+                               nullptr, 0, (hipStream_t) stream);
+}
+
+size_t exl3_gemm_trellis_workspace_size(int m, int k, const int* widths, int groups)
+{
+    if (!widths || groups < 1 || groups > EXL3_MAX_GROUPS || m < 1 || k < 128 || k % 128) return 0;
+    for (int i = 0; i < groups; ++i)
+        if (widths[i] < 128 || widths[i] % 128) return 0;
+    return pc_plan(m, k, widths, groups).ws_bytes;
 }
 
 int exl3_gemm_trellis_grouped(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
                               const void* const* suh, void* xh, const void* const* svh, const int* widths, int groups,
-                              int m, int k, int K, int mcg, int mul1, void* stream)
+                              int m, int k, int K, int mcg, int mul1, void* workspace, size_t ws_bytes, void* stream)
 {
     if (!x || !trellis || !y || !suh || !xh || !svh || !widths || groups < 1 || groups > EXL3_MAX_GROUPS || m < 0 ||
         K < 1 || K > 8 || k % 128 || k < 128 || ldx < k || ldx % 8 || ldy % 8 || (((uintptr_t) xh) & 15) ||
@@ -679,7 +794,7 @@ int exl3_gemm_trellis_grouped(const void* x, int64_t ldx, const void* const* tre
     if (ldy < total) return EXL3_EINVAL;
     if (m == 0) return EXL3_OK;
     return gemm_trellis_common(x, ldx, trellis, ys, ldy, suh, (uint16_t*) xh, svh, widths, groups, m, k, K, mcg, mul1,
-                               (hipStream_t) stream);
+                               workspace, ws_bytes, (hipStream_t) stream);
 }
 
 int exl3_gemm(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh, void* A_had,

@@ -40,7 +40,9 @@ SIGNATURES = {
     "exl3_mgemm": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "exl3_hgemm_recon": (_i, [_p, _i64, _p, _i64, _p, _i64, _i, _i, _i, _p]),
     "exl3_gemm_trellis": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
-    "exl3_gemm_trellis_grouped": (_i, [_p, _i64, _pp, _p, _i64, _pp, _p, _pp, _ip, _i, _i, _i, _i, _i, _i, _p]),
+    "exl3_gemm_trellis_grouped": (_i, [_p, _i64, _pp, _p, _i64, _pp, _p, _pp, _ip, _i, _i, _i, _i, _i, _i, _p, _sz,
+                                       _p]),
+    "exl3_gemm_trellis_workspace_size": (_sz, [_i, _i, _ip, _i]),
     "exl3_gemm": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
 }
 

@@ -59,6 +59,27 @@ def workspace(device: torch.device, nbytes: int, stream: Optional[int] = None) -
     return buf
 
 
+_pf_workspaces: dict = {}
+
+
+def prefill_workspace(device: torch.device, nbytes: int, stream: Optional[int] = None) -> Optional[torch.Tensor]:
+    """Grow-only zeroed workspace of the prefill GEMM's split tail for the current (or given) stream.
+    During graph capture a missing or short one is not allocated: the launch then runs unsplit."""
+    if nbytes <= 0:
+        return None
+    device = torch.device(device)
+    if stream is None:
+        stream = torch.cuda.current_stream(device).cuda_stream
+    key = (device, stream)
+    buf = _pf_workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            return buf
+        buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _pf_workspaces[key] = buf
+    return buf
+
+
 def gemv_workspace_bytes(m: int, k: int, n: int, K: int, groups: int = 1) -> int:
     return int(L.lib().exl3_gemv_workspace_size(m, k, n, K, groups))
 
@@ -249,9 +270,12 @@ def exl3_gemm_trellis_grouped(A, B: Sequence[torch.Tensor], C, suh: Sequence[tor
     pt, _a = L.ptr_array([b.data_ptr() for b in B])
     ps, _b = L.ptr_array([s.data_ptr() for s in suh])
     pv, _c = L.ptr_array([s.data_ptr() for s in svh])
+    ws = prefill_workspace(A.device, int(L.lib().exl3_gemm_trellis_workspace_size(m, k, wa, g)))
     L.check(L.lib().exl3_gemm_trellis_grouped(x2.data_ptr(), x2.stride(0) if m > 1 else k, pt, C.data_ptr(),
                                               _ldy(C, sum(widths)), ps, xh.data_ptr(), pv, wa, g, m, k, K,
-                                              *_cb_flags(mcg, mul1), _stream(A)), "exl3_gemm_trellis_grouped")
+                                              *_cb_flags(mcg, mul1), ws.data_ptr() if ws is not None else None,
+                                              ws.numel() if ws is not None else 0, _stream(A)),
+            "exl3_gemm_trellis_grouped")
 
 
 def exl3_gemm(A, B, C, suh, A_had, svh, force_shape_idx: int = -1, mcg: bool = False, mul1: bool = True,

@@ -90,8 +90,9 @@ def _linear_into(x2, trellis, suh, svh, K, mcg, mul1, y):
             E.hgemm_recon(xh, w, y[:, n0:n1])
         E.had_r_128(y, y, None, svh, 1.0)
     else:
+        # the grouped entry point with one group: its launch balances the last wave of tiles
         xh = torch.empty_like(x2)
-        E.exl3_gemm_trellis(x2, trellis, y, suh, xh, svh, K, mcg, mul1)
+        E.exl3_gemm_trellis_grouped(x2, [trellis], y, [suh], xh, [svh], K, mcg, mul1)
 
 
 @torch.library.custom_op("exl3rocm::linear", mutates_args=())

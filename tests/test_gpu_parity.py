@@ -9,6 +9,8 @@ Bars:
     grouped == ungrouped, graph replay == eager.
 Expected values come from oracle/libexl3cpu.so (the C restatement pinned in test_oracle.py).
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -372,6 +374,31 @@ def test_prefill_grouped_widths_parity(widths, bits, cb):
         assert torch.equal(y[:, n0:n0 + n].view(torch.int16), single.view(torch.int16)), (widths, n0)
         assert_close(y[:, n0:n0 + n].cpu().numpy(), cpu.linear(x, tr, bits, su, sv, cb), (widths, n0))
         n0 += n
+
+
+def test_prefill_split_tail_parity_and_determinism():
+    """260 output tiles: one full wave of 256 whole tiles plus a tail of 4 tiles split along K into
+    pieces (fp32 partials summed in piece order).  Whole tiles equal the unsplit launch bitwise, the
+    split tiles match the oracle, and repeat calls are bitwise equal."""
+    m, k, bits = 256, 1024, 4
+    n = 128 * 260
+    tr, su, sv = synth.layer("pfsplit", 0, k, n, bits)
+    x = synth.activations(synth.key_of("pfsplit", "x"), m, k)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    wa = (ctypes.c_int * 1)(n)
+    assert _lib.lib().exl3_gemm_trellis_workspace_size(m, k, wa, 1) > 0
+    y1 = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, False, True)
+    y2 = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, False, True)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    y0 = torch.empty_like(y1)                                   # reference entry point: never split
+    E.exl3_gemm_trellis(X, T, y0, SU, torch.empty_like(X), SV, bits, False, True)
+    c_split = 256 * 128
+    assert torch.equal(y1[:, :c_split].view(torch.int16), y0[:, :c_split].view(torch.int16))
+    c0 = c_split - 128                                          # one whole tile, then the split ones
+    sub = np.ascontiguousarray(tr[:, c0 // 16:, :])
+    ref = cpu.linear(x[:8], sub, bits, su, np.ascontiguousarray(sv[c0:]), 2)
+    assert_close(y1[:8, c0:].cpu().numpy(), ref, "split tail")
+    assert_close(y1[:, c_split:].cpu().numpy(), y0[:, c_split:].cpu().numpy(), "split vs unsplit")
 
 
 def test_linear_groups_prefill_matches_per_group_linear():
