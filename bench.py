@@ -19,6 +19,7 @@ configuration 3 small-batch crossover, configuration 2 bitrate sweep.
 
   python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-sweep] [--no-cpu]
   python bench.py --traffic-probe      (what the PMC traffic passes profile)
+  python bench.py --prefill-only       (configuration 4 alone, for the prefill PMC passes)
 """
 from __future__ import annotations
 
@@ -325,6 +326,8 @@ def main() -> int:
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true", help="only the dispatches the PMC traffic passes read")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the configuration-4 prefill chunk (what the prefill PMC passes read); prints its dict")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this engine runs on one GPU; multi-GPU runs are not part of this build "
@@ -337,6 +340,9 @@ def main() -> int:
     bits = 4
     if args.traffic_probe:
         return traffic_probe(torch, bits, args.copies)
+    if args.prefill_only:
+        print(json.dumps(prefill_chunk(torch)), flush=True)
+        return 0
     log("building layer set (4 bpw, mul1) x %d copies" % args.copies)
     base, sets = build_layers(torch, bits, args.copies)
     from exl3rocm import synth
