@@ -27,8 +27,6 @@ MR_MAX = min(int(os.environ.get("EXL3_MR_MAX", str(_lib.GEMV_MAX_ROWS))), _lib.G
 # widest non-lm_head layer (17408): the shared reconstruction buffer of the `recon` prefill route
 RECON_SLICE_N = int(os.environ.get("EXL3_RECON_SLICE_N", "17408"))
 PREFILL_ROUTE = os.environ.get("EXL3_PREFILL", "fused")
-# timing-only debug switch: quantized linears return zeros without running kernels
-_DEBUG_SKIP = os.environ.get("EXL3_DEBUG_SKIP_LINEAR") == "1"
 
 _wbuf: dict = {}
 
@@ -102,8 +100,8 @@ def exl3_linear(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: 
     n = svh.shape[0]
     M = x2.shape[0]
     y = torch.empty((M, n), dtype=torch.float16, device=x.device)
-    if M == 0 or _DEBUG_SKIP:
-        return y.zero_().view(*x.shape[:-1], n) if _DEBUG_SKIP else y.view(*x.shape[:-1], n)
+    if M == 0:
+        return y.view(*x.shape[:-1], n)
     _linear_into(x2, trellis, suh, svh, K, mcg, mul1, y)
     return y.view(*x.shape[:-1], n)
 
@@ -124,8 +122,6 @@ def exl3_linear_groups(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[t
     ptrs_* = int64 device tensors of per-group data pointers, given when all groups share K and
     width: at M == 1 one grouped launch over the pointer tables computes every group."""
     widths = [s.shape[0] for s in svh]
-    if _DEBUG_SKIP:
-        return torch.zeros((*x.shape[:-1], sum(widths)), dtype=torch.float16, device=x.device)
     if len(trellis) == 1:
         return exl3_linear(x, trellis[0], suh[0], svh[0], K[0], mcg, mul1)
     x2, k = _prep(x)
