@@ -122,6 +122,27 @@ int exl3_gemv_mr_grouped_widths(const void* x, int64_t ldx, const void* const* t
  * counterpart, as exl3_gemv_workspace_size. */
 size_t exl3_gemv_workspace_size_widths(int m, int k, const int* widths, int groups);
 
+/* Gated MLP input, 1 <= m <= 32: the gate (group 0) and up (group 1) linears of one module, equal
+ * K and width n, share x and one stream-K launch; y[m, n] (rows ldy apart, ldy >= n) receives
+ * fp16(fp16(silu(gate)) * up), where gate and up are exactly what exl3_gemv_mr_grouped writes
+ * (fp16 C, output Hadamard, svh) and silu is g / (1 + exp(-g)) in fp32 (the SiluAndMul
+ * roundings).  trellis / suh / svh: host arrays of 2 device pointers.  Workspace as
+ * exl3_gemv_workspace_size(m, k, n, K, 2).  No counterpart in the reference: its gated MLP runs
+ * the gate/up linear_groups, then a separate SiLU-and-mul (reference
+ * docs/EFFICIENCY_INVESTIGATION.md:36-66 proposes this fusion).  Callers: model code that owns
+ * the gate/up module and its activation (exl3rocm's linear_silu_mul op).  Removes the [m, 2n]
+ * intermediate and the activation launch. */
+int exl3_gemv_silu_mul(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
+                       const void* const* suh, const void* const* svh, int m, int k, int n, int K, int mcg, int mul1,
+                       void* workspace, size_t ws_bytes, void* stream);
+
+/* Elementwise SiLU-and-mul: out[r][c] = fp16(fp16(silu(gate[r][c])) * up[r][c]) for r < rows,
+ * c < n (n % 8 == 0; gate and up rows ld_in apart, out rows ld_out apart; 16-byte aligned).
+ * No counterpart in the reference (vLLM's SiluAndMul does this there).  Callers: exl3rocm's
+ * linear_silu_mul op for m > 32, after the grouped prefill. */
+int exl3_silu_mul(const void* gate, const void* up, int64_t ld_in, void* out, int64_t ld_out, int rows, int n,
+                  void* stream);
+
 /* Grouped M == 1 linear over device int64 pointer tables (one entry per group), output
  * (groups, 1, n) == the concatenated row.
  * Replaces `exl3_mgemm(x, ptrs_trellis, y, ptrs_suh, xh, ptrs_svh, ...)` (reference ops.py:137-138). */

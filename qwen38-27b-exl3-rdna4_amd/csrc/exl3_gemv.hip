@@ -11,23 +11,14 @@
 //             rounds C to fp16 and applies y = fp16(fp16(Had128(C)) * svh).
 // Rows never interact, and the split count depends only on (k, n), so every row of an M-row
 // call is bitwise identical to the M == 1 call of that row, grouped or not.
-#include "exl3_device.h"
-#include "../../include/exl3_mi355x.h"
+#include "exl3_gemv_kernel.h"
 
 #include <stdio.h>
 #include <stdlib.h>
 #include <algorithm>
-#include <utility>
 
 using namespace exl3;
 
-// f(integral_constant<int, I>) for I in the sequence: ring slots are indexed by constants in the
-// source, so the ring always lives in registers (a loop index here could leave it in scratch memory)
-template <class F, int... I>
-__device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&& f)
-{
-    (f(std::integral_constant<int, I>{}), ...);
-}
 
 // ============================================================================================
 // Codebook decode of raw states (reference binding `decode`, tests/test_gpu_parity.py:101-109)
@@ -118,432 +109,18 @@ __global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ i
     if (live) *reinterpret_cast<u32x4*>(out + row * ld_out + col) = res;
 }
 
-// ============================================================================================
-// Fused GEMV with stream-K balancing
-//
-// Work unit: (128-column block cb, 128-row k slice ku) == two 64-row k steps == one Hadamard
-// block of the input; units are ordered cb-major, U in total, UPB = k / 128 per block.  The grid
-// has G workgroups (all resident); workgroup w owns units [w*U/G, (w+1)*U/G).  Wave i of a
-// workgroup covers n-tiles 2i, 2i+1 of the block; its lanes = (k-tile g of the step, n-tile,
-// q-block).  A workgroup keeps fp32 accumulators across consecutive units of one block and writes
-// one partial per block it touches; the block's completion counter counts the contributing
-// workgroups and the last one sums the partials in workgroup order (fixed for the shape, hence
-// deterministic), rounds C to fp16 and applies the output Hadamard and svh.
-// ============================================================================================
-struct GemvGroup {
-    const uint32_t* trellis;   // tile words
-    const uint16_t* suh;
-    const uint16_t* svh;
-    uint16_t* y;               // output columns of this group (row stride ldy)
-    int n;                     // width (columns)
-    int G;                     // workgroups of this group
-    int wg0;                   // its first workgroup in the flattened grid
-    int max_seg;               // partial slots per workgroup
-    int64_t part_off;          // first partial (floats) of this group
-    int cnt_off;               // first completion counter of this group
-    int h;                     // its workgroups dispatched first on their CU (weight wa; the rest wb)
-};
-
-struct GemvArgs {
-    const uint16_t* x;         // [M][ldx] fp16
-    int64_t ldx;
-    GemvGroup g[EXL3_MAX_GROUPS];
-    const int64_t* tab_trellis; // optional device pointer tables (grouped M=1 `mgemm` form): they
-    const int64_t* tab_suh;     // replace g[i].trellis / suh / svh
-    const int64_t* tab_svh;
-    int groups, M, k, UPB;
-    int wa, wb;                // unit-split weights of first-dispatched / second workgroups on a CU
-    int chunk_units;           // units whose rotated input fits the LDS at once
-    int64_t ldy;
-    float* part;               // per group: [G][max_seg][M][128] fp32 partials
-    uint32_t* counters;        // per group: [n / 128], zero between calls
-};
-
-constexpr int RED_BATCH = 16;                   // partial loads in flight per thread in the reduction
-constexpr int A_ROW = 136;                      // LDS row of one rotated 128-block (padded, halves)
-constexpr int LDS_BUDGET = 64 * 1024;           // per workgroup: 2 workgroups per CU
-constexpr int RING = 8;                         // 64-row k steps in flight per wave (even)
-constexpr int WAVES_PER_SIMD = 2;
-
-// s_waitcnt vmcnt(0) (gfx9 encoding: expcnt / lgkmcnt left at their maxima), fenced against
-// compiler reordering: every vector-memory store of this wave has completed.
-__device__ __forceinline__ void wait_stores_complete()
+// SiLU-and-mul of fp16 rows: out[r][c] = fp16(fp16(silu(gate[r][c])) * up[r][c]), 8 columns a thread
+__global__ void __launch_bounds__(256) silu_mul_kernel(const uint16_t* __restrict__ gate, const uint16_t* __restrict__ up,
+                                                       int64_t ld_in, uint16_t* __restrict__ out, int64_t ld_out,
+                                                       int rows, int n8)
 {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-// a wave-uniform 64-bit value as a scalar (readfirstlane of both halves)
-__device__ __forceinline__ int64_t uniform_i64(int64_t v)
-{
-    const uint32_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) v);
-    const uint32_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) ((uint64_t) v >> 32));
-    return (int64_t) (((uint64_t) hi << 32) | lo);
-}
-
-// Unit split of a group's U units over its G workgroups: workgroup w owns [lo(w), lo(w + 1)),
-// lo(w) = floor(U * S(w) / S(G)) with S(w) = wa * min(w, h) + wb * max(w - h, 0).  The first h
-// workgroups of the group are dispatched first on their CU; the SIMD arbiter favours their (older)
-// waves, so they get the larger weight wa and both waves of a CU finish their units together.  A
-// function of the shape only (never of m): rows stay bitwise equal to the m == 1 call.
-struct Split {
-    int U, G, h, wa, wb;
-    __host__ __device__ int64_t S(int w) const
-    {
-        return (int64_t) wa * (w < h ? w : h) + (int64_t) wb * (w > h ? w - h : 0);
-    }
-    __host__ __device__ int lo(int w) const { return (int) ((int64_t) U * S(w) / S(G)); }
-    // the workgroup owning unit u: the largest w in [0, G) with lo(w) <= u, i.e. S(w) <= T
-    __host__ __device__ int owner(int u) const
-    {
-        const int64_t SG = S(G);
-        const int64_t T = ((int64_t) (u + 1) * SG + U - 1) / U - 1;
-        const int w = T < (int64_t) wa * h ? (int) (T / wa) : h + (int) ((T - (int64_t) wa * h) / wb);
-        return w < G - 1 ? w : G - 1;
-    }
-    // most units any workgroup owns
-    __host__ __device__ int max_units() const
-    {
-        const int wmax = wa > wb ? wa : wb;
-        return (int) (((int64_t) U * wmax + S(G) - 1) / S(G)) + 1;
-    }
-};
-
-
-// Two workgroups (8 waves) per CU are resident at once: up to 256 registers per lane, enough for
-// a ring deep enough that one wave alone keeps its SIMD busy.
-template <int BITS, int CB, int MT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_SIMD, WAVES_PER_SIMD))) gemv_kernel(GemvArgs a)
-{
-    extern __shared__ __align__(16) uint16_t smem[];
-    __shared__ int s_last[256];
-    __shared__ int s_list[256];
-    __shared__ int s_nred;
-    // the group of this workgroup: a flattened grid, each group its own range of workgroups
-    int grp = 0;
-    if (a.groups > 1 && (int) blockIdx.x >= a.g[1].wg0) grp = 1;
-    if (a.groups > 2 && (int) blockIdx.x >= a.g[2].wg0) grp = 2;
-    if (a.groups > 3 && (int) blockIdx.x >= a.g[3].wg0) grp = 3;
-    // constant indices only: a runtime index into the kernel-argument struct would copy it to
-    // scratch memory, and every later read of it would be a vector-memory load
-    const GemvGroup gg = grp == 0 ? a.g[0] : grp == 1 ? a.g[1] : grp == 2 ? a.g[2] : a.g[3];
-    const int w = blockIdx.x - gg.wg0;
-    const int G = gg.G, UPB = a.UPB, M = a.M;
-    const int NB = gg.n / 128, NT = gg.n / 16, U = NB * UPB;
-    const Split sp{U, G, gg.h, a.wa, a.wb};
-    const uint32_t* trel = gg.trellis;
-    const uint16_t* suh = gg.suh;
-    const uint16_t* svh = gg.svh;
-    uint16_t* y = gg.y;
-    if (a.tab_trellis) {
-        // table entries are uniform (grp is): keep them in scalar registers, or the trellis buffer
-        // resource would look divergent and every buffer load would be wrapped in a waterfall loop
-        trel = reinterpret_cast<const uint32_t*>(uniform_i64(a.tab_trellis[grp]));
-        suh = reinterpret_cast<const uint16_t*>(uniform_i64(a.tab_suh[grp]));
-        svh = reinterpret_cast<const uint16_t*>(uniform_i64(a.tab_svh[grp]));
-    }
-    uint32_t* const counters = a.counters + gg.cnt_off;
-    // the trellis as one raw buffer (layers of 4 GiB and more are declined on the host)
-    const uint64_t trel_bytes = (uint64_t) a.k * gg.n * BITS / 8;
-    const __amdgpu_buffer_rsrc_t trsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint32_t*>(trel), 0, (int) (uint32_t) trel_bytes, RAW_BUFFER_FLAGS);
-    gc_u16* const gsuh = as_global(suh);
-    gc_u16* const gsvh = as_global(svh);
-    gc_u16* const gx = as_global(a.x);
-    g_u16* const gy = as_global(y);
-    // LDS: the rotated input of a chunk of units, M rows per unit followed by one zero row (the A
-    // operand of MFMA rows >= M), then the fp16 C of one block for the output transform
-    const int UROWS = M + 1;
-    uint16_t* lds_a = smem;                                   // [chunk_units][M + 1][A_ROW]
-    uint16_t* lds_c = smem + a.chunk_units * UROWS * A_ROW;   // [M][A_ROW]
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    const int g = lane >> 4, j = lane & 15, q = j & 7;
-    const int ulo = sp.lo(w), uhi = sp.lo(w + 1);
-    if (ulo >= uhi) return;                                   // uniform per workgroup
-    const int seg0_cb = ulo / UPB;
-    float* part_grp = a.part + gg.part_off;
-
-    // Trellis addressing.  Step d (0, 1) of unit (cb, ku) covers k-tiles 8ku + 4d .. +3 and n-tiles
-    // 8cb .. 8cb + 7; this lane reads q-block q of tile (k-tile + g, n-tile 8cb + 2 wave + (j >> 3)).
-    // A uniform byte offset walks the units; the lane adds fixed byte offsets.
-    const int tile_lane = (g * NT + wave * 2 + (j >> 3)) * (8 * BITS);            // words
-    const uint32_t off_main = (uint32_t) (tile_lane + q * BITS) * 4u;
-    const uint32_t off_prev = (uint32_t) (tile_lane + (q == 0 ? 8 * BITS - 1 : q * BITS - 1)) * 4u;
-    const uint32_t STEP_D = (uint32_t) (4 * NT * 8 * BITS * 4);   // bytes from step 0 to step 1 of a unit
-    const uint32_t STEP_KU = 2 * STEP_D;                          // to the next unit of the same block
-    const uint32_t STEP_CB = 8 * 8 * BITS * 4;                    // to the next block, same ku
-    const uint32_t STEP_WRAP = STEP_CB - (uint32_t) (UPB - 1) * STEP_KU;   // to ku 0 of the next block (mod 2^32)
-
-    // rotated-input job i of a chunk starting at unit u0: (unit u0 + i / M, row i % M), 16 lanes each
-    auto job_src = [&](int u0, int i, int& m, int& col) __attribute__((always_inline)) {
-        const int u = u0 + i / M;
-        m = i - (i / M) * M;
-        col = (u - (u / UPB) * UPB) * 128 + 8 * (threadIdx.x & 15);
-    };
-
-    // The prologue and the completion phase sit on every workgroup's critical path while other
-    // workgroups on the same SIMDs run VALU-heavy decode loops: give them issue priority.
-    __builtin_amdgcn_s_setprio(2);
-
-    // ---- first input chunk: its x / suh loads go out before the trellis ring ----------------
-    const int nfirst = min(a.chunk_units, uhi - ulo) * M;
-    u32x4 px = {0u, 0u, 0u, 0u}, ps = px;
-    {
-        const int i = threadIdx.x >> 4;
-        if (i < nfirst) {
-            int m, col;
-            job_src(ulo, i, m, col);
-            px = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
-            ps = *reinterpret_cast<gc_u32x4*>(gsuh + col);
-        }
-    }
-    // ---- the trellis ring: RING steps in flight per wave ----------------------------------------
-    // Slot i always holds a step with d == i & 1.  The load cursor (ul, ku_l, lp) is the unit of the
-    // next refill; it stops at the last unit, whose steps are reloaded (in bounds, never used).
-    uint32_t Wr[RING][BITS + 1];
-    int ul = ulo, ku_l = ulo - seg0_cb * UPB;
-    uint32_t lp = (uint32_t) seg0_cb * STEP_CB + (uint32_t) ku_l * STEP_KU;
-    auto advance_load = [&]() __attribute__((always_inline)) {
-        if (ul + 1 < uhi) {
-            ++ul;
-            if (++ku_l == UPB) {
-                ku_l = 0;
-                lp += STEP_WRAP;
-            } else {
-                lp += STEP_KU;
-            }
-        }
-    };
-    static_for(std::make_integer_sequence<int, RING>{}, [&](auto I) __attribute__((always_inline)) {
-        constexpr int i = decltype(I)::value;
-        load_qblock_buf<BITS>(trsrc, off_main, off_prev, lp + (i & 1) * STEP_D, Wr[i]);
-        if (i & 1) advance_load();
-    });
-    // rotated input of units [c0, c1) -> LDS; the first 16-lane job of each lane uses (x0, s0)
-    auto rotate_chunk = [&](int c0, int c1, u32x4 x0, u32x4 s0, bool have_first) __attribute__((always_inline)) {
-        const int njobs = (c1 - c0) * M;
-        const int i = threadIdx.x >> 4;
-        if (i - (threadIdx.x & 63) / 16 < njobs) {            // waves with a job (whole 16-lane groups)
-            if (!have_first && i < njobs) {
-                int m, col;
-                job_src(c0, i, m, col);
-                x0 = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
-                s0 = *reinterpret_cast<gc_u32x4*>(gsuh + col);
-            }
-            const u32x4 r = had128_x8(x0, s0, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
-            if (i < njobs) {
-                int m, col;
-                job_src(c0, i, m, col);
-                *reinterpret_cast<u32x4*>(lds_a + ((i / M) * UROWS + m) * A_ROW + 8 * (threadIdx.x & 15)) = r;
-            }
-            for (int i2 = i + 16; i2 - (threadIdx.x & 63) / 16 < njobs; i2 += 16) {
-                u32x4 xv = {0u, 0u, 0u, 0u}, sv = xv;
-                int m = 0, col = 0;
-                if (i2 < njobs) {
-                    job_src(c0, i2, m, col);
-                    xv = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
-                    sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
-                }
-                const u32x4 r2 = had128_x8(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
-                if (i2 < njobs)
-                    *reinterpret_cast<u32x4*>(lds_a + ((i2 / M) * UROWS + m) * A_ROW + 8 * (threadIdx.x & 15)) = r2;
-            }
-        }
-    };
-    int c0 = ulo, c1 = min(ulo + a.chunk_units, uhi);
-    rotate_chunk(c0, c1, px, ps, true);
-    // zero rows: never overwritten by later chunks
-    for (int t = threadIdx.x; t < a.chunk_units * (A_ROW / 8); t += 256)
-        *reinterpret_cast<u32x4*>(lds_a + ((t / (A_ROW / 8)) * UROWS + M) * A_ROW + 8 * (t % (A_ROW / 8))) =
-            u32x4{0u, 0u, 0u, 0u};
-    __syncthreads();
-
-    // A operand row of this lane (per MFMA row tile) within a unit: rows >= M read the zero row
-    int a_lane[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) a_lane[mt] = (mt * 16 + j < M ? mt * 16 + j : M) * A_ROW + 16 * g;
-
-    f32x4 acc[2][MT];
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const int colb = wave * 32 + (j >> 3) * 16 + (j & 7);    // + 8h: column of this lane in the block
-    auto write_partial = [&](int cb) __attribute__((always_inline)) {
-        float* slab = part_grp + ((int64_t) w * gg.max_seg + (cb - seg0_cb)) * M * 128;
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int m = mt * 16 + 4 * g + v;
-                    if (m < M)
-                        __hip_atomic_store(&slab[m * 128 + colb + 8 * h], acc[h][mt][v], __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                }
-    };
-
-    // one k step: decode the slot's q-block, refill the slot from the load cursor (when the ring
-    // still has steps to fetch), two MFMAs per tile column half
-    auto step = [&](uint32_t (&Wq)[BITS + 1], const uint16_t* unit_a, int d, bool refill) __attribute__((always_inline)) {
-        uint32_t P[16];
-        decode_qblock<BITS, CB>(Wq, P);
-        if (refill) load_qblock_buf<BITS>(trsrc, off_main, off_prev, lp + d * STEP_D, Wq);
-        f16x8 A0[MT], A1[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const uint16_t* ap = unit_a + a_lane[mt] + 64 * d;
-            A0[mt] = *reinterpret_cast<const f16x8*>(ap);
-            A1[mt] = *reinterpret_cast<const f16x8*>(ap + 8);
-        }
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const u32x4 B0 = {P[2 * h], P[4 + 2 * h], P[8 + 2 * h], P[12 + 2 * h]};
-            const u32x4 B1 = {P[2 * h + 1], P[5 + 2 * h], P[9 + 2 * h], P[13 + 2 * h]};
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) {
-                acc[h][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0[mt], __builtin_bit_cast(f16x8, B0), acc[h][mt], 0, 0, 0);
-                acc[h][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[mt], __builtin_bit_cast(f16x8, B1), acc[h][mt], 0, 0, 0);
-            }
-        }
-    };
-
-    int cb_cur = seg0_cb;
-    int left = UPB - (ulo - seg0_cb * UPB);                   // units of block cb_cur still to come
-    // sub-step i of the ring turn starting at unit u0 (slot i, d = i & 1)
-    auto sub_step = [&](auto I, int u0, bool refill) __attribute__((always_inline)) {
-        constexpr int i = decltype(I)::value;
-        if (!(i & 1)) {
-            if (left == 0) {                                  // a new 128-column block starts
-                write_partial(cb_cur);
-#pragma unroll
-                for (int h = 0; h < 2; ++h)
-#pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) acc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                ++cb_cur;
-                left = UPB;
-            }
-            --left;
-        }
-        step(Wr[i], lds_a + (u0 + i / 2 - c0) * UROWS * A_ROW, i & 1, refill);
-        if ((i & 1) && refill) advance_load();
-    };
-    auto next_chunk = [&](int u0) __attribute__((always_inline)) {      // chunks hold whole ring turns
-        if (u0 == c1) {
-            c0 = c1;
-            c1 = min(c0 + a.chunk_units, uhi);
-            __syncthreads();
-            rotate_chunk(c0, c1, px, ps, false);
-            __syncthreads();
-        }
-    };
-
-    __builtin_amdgcn_s_setprio(0);
-    // Full ring turns run without per-step conditions (a conditional step would make the compiler
-    // wait for every load in flight); the last, partial turn only drains the ring.
-    const int S = 2 * (uhi - ulo);                            // 64-row k steps of this workgroup
-    const int S_full = S - S % RING;
-    int s0 = 0;
-    for (; s0 < S_full; s0 += RING) {
-        const int u0 = ulo + s0 / 2;
-        next_chunk(u0);
-        static_for(std::make_integer_sequence<int, RING>{}, [&](auto I) __attribute__((always_inline)) { sub_step(I, u0, true); });
-    }
-    if (s0 < S) {
-        const int u0 = ulo + s0 / 2;
-        next_chunk(u0);
-        static_for(std::make_integer_sequence<int, RING>{}, [&](auto I) __attribute__((always_inline)) {
-            if (s0 + decltype(I)::value < S) sub_step(I, u0, false);
-        });
-    }
-    __builtin_amdgcn_s_setprio(2);
-    write_partial(cb_cur);
-
-    // ---- completion: count this workgroup into every block it touched, reduce those it completed
-    // The partials are device-scope (write-through) stores: once complete (vmcnt(0)) they are
-    // visible to device-scope loads from any XCD, so no cache-wide release is needed.
-    wait_stores_complete();
-    __syncthreads();
-    const int nblk = cb_cur - seg0_cb + 1;
-    const int RB = M == 1 ? 2 : 1;                            // completed blocks reduced side by side
-    for (int b0 = 0; b0 < nblk; b0 += 256) {
-        const int nb = min(256, nblk - b0);
-        if ((int) threadIdx.x < nb) {                         // one counter per thread, all in flight
-            const int cb = seg0_cb + b0 + threadIdx.x;
-            const int wf = sp.owner(cb * UPB), wl = sp.owner(cb * UPB + UPB - 1);
-            const uint32_t prev = __hip_atomic_fetch_add(&counters[cb], 1u, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-            s_last[threadIdx.x] = prev == (uint32_t) (wl - wf) ? 1 : 0;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            int c = 0;
-            for (int bi = 0; bi < nb; ++bi)
-                if (s_last[bi]) s_list[c++] = seg0_cb + b0 + bi;
-            s_nred = c;
-        }
-        __syncthreads();
-        const int nred = __builtin_amdgcn_readfirstlane(s_nred);
-        for (int r0 = 0; r0 < nred; r0 += RB) {
-            const int rb = min(RB, nred - r0);
-            // svh of the first output-transform pass, requested before the partial loads so that its
-            // round trip overlaps theirs
-            const int l16 = threadIdx.x & 15;
-            u32x4 sv_first = {0u, 0u, 0u, 0u};
-            {
-                const int rr = threadIdx.x >> 4;
-                if (rr < rb * M) sv_first = *reinterpret_cast<gc_u32x4*>(gsvh + s_list[r0 + rr / M] * 128 + 8 * l16);
-            }
-            // contributor wf holds block cb in its segment cb - first_cb(wf); every later
-            // contributor starts inside cb, so its segment is 0.  Loads go out in batches of
-            // RED_BATCH; the sum runs in contributor order.
-            for (int e = threadIdx.x; e < rb * M * 128; e += 256) {
-                const int r = e / (M * 128), el = e - r * (M * 128);
-                const int cb = s_list[r0 + r];
-                const int wf = sp.owner(cb * UPB), wl = sp.owner(cb * UPB + UPB - 1);
-                const int seg_f = cb - sp.lo(wf) / UPB;
-                const int nc = wl - wf + 1;
-                float sum = 0.f;
-                for (int cc0 = 0; cc0 < nc; cc0 += RED_BATCH) {
-                    float v[RED_BATCH];
-#pragma unroll
-                    for (int ii = 0; ii < RED_BATCH; ++ii) {
-                        const int c = cc0 + ii;
-                        const int64_t slot = c == 0 ? (int64_t) wf * gg.max_seg + seg_f : (int64_t) (wf + c) * gg.max_seg;
-                        v[ii] = c < nc ? __hip_atomic_load(part_grp + slot * M * 128 + el, __ATOMIC_RELAXED,
-                                                           __HIP_MEMORY_SCOPE_AGENT)
-                                       : 0.f;
-                    }
-#pragma unroll
-                    for (int ii = 0; ii < RED_BATCH; ++ii)
-                        if (cc0 + ii < nc) sum += v[ii];
-                }
-                lds_c[(r * M + (el >> 7)) * A_ROW + (el & 127)] = f16_bits((f16) sum);
-            }
-            if ((int) threadIdx.x < rb)                        // ready for the next call (stream order)
-                __hip_atomic_store(&counters[s_list[r0 + threadIdx.x]], 0u, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-            __syncthreads();
-            // output Hadamard + svh: 16 lanes per (block, row)
-            for (int rr0 = 0; rr0 < rb * M; rr0 += 16) {
-                const int rr = rr0 + (threadIdx.x >> 4);
-                const bool live = rr < rb * M;
-                const int r = live ? rr / M : 0, m = live ? rr - r * M : 0;
-                const int cb = s_list[r0 + r];
-                u32x4 c = {0u, 0u, 0u, 0u}, sv = c;
-                if (live) {
-                    c = *reinterpret_cast<const u32x4*>(lds_c + rr * A_ROW + 8 * l16);
-                    sv = rr0 == 0 ? sv_first : *reinterpret_cast<gc_u32x4*>(gsvh + cb * 128 + 8 * l16);
-                }
-                const u32x4 res = had128_x8(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, R_SCALE);
-                if (live) *reinterpret_cast<g_u32x4*>(gy + (int64_t) m * a.ldy + cb * 128 + 8 * l16) = res;
-            }
-            __syncthreads();                                   // lds_c free for the next blocks
-        }
-    }
+    const int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t) rows * n8) return;
+    const int64_t r = i / n8;
+    const int64_t c = (i - r * n8) * 8;
+    const u32x4 g = *reinterpret_cast<gc_u32x4*>(as_global(gate) + r * ld_in + c);
+    const u32x4 u = *reinterpret_cast<gc_u32x4*>(as_global(up) + r * ld_in + c);
+    *reinterpret_cast<g_u32x4*>(as_global(out) + r * ld_out + c) = silu_mul_x8(g, u);
 }
 
 // ============================================================================================
@@ -648,45 +225,6 @@ int chunk_units(int m, int max_per)
     return (int) std::max<int64_t>(1, std::min<int64_t>(max_per, fit));
 }
 
-// LDS: chunk_units x (m + 1) input rows, then the C rows of the blocks reduced side by side
-size_t lds_bytes(int M, int cu) { return ((size_t) cu * (M + 1) + (M == 1 ? 2 : M)) * A_ROW * 2; }
-
-template <int BITS, int CB, int MT>
-int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t stream)
-{
-    hipLaunchKernelGGL((gemv_kernel<BITS, CB, MT>), dim3(wgs), dim3(256), lds_bytes(a.M, a.chunk_units), stream, a);
-    return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
-}
-
-template <int BITS, int CB>
-int launch_gemv_m(const GemvArgs& a, int wgs, hipStream_t s)
-{
-    return a.M <= 16 ? launch_gemv_t<BITS, CB, 1>(a, wgs, s) : launch_gemv_t<BITS, CB, 2>(a, wgs, s);
-}
-
-template <int BITS>
-int launch_gemv_cb(const GemvArgs& a, int cb, int wgs, hipStream_t s)
-{
-    switch (cb) {
-        case 0: return launch_gemv_m<BITS, 0>(a, wgs, s);
-        case 1: return launch_gemv_m<BITS, 1>(a, wgs, s);
-        default: return launch_gemv_m<BITS, 2>(a, wgs, s);
-    }
-}
-
-int launch_gemv(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s)
-{
-    switch (bits) {
-        case 1: return launch_gemv_cb<1>(a, cb, wgs, s);
-        case 2: return launch_gemv_cb<2>(a, cb, wgs, s);
-        case 3: return launch_gemv_cb<3>(a, cb, wgs, s);
-        case 4: return launch_gemv_cb<4>(a, cb, wgs, s);
-        case 5: return launch_gemv_cb<5>(a, cb, wgs, s);
-        case 6: return launch_gemv_cb<6>(a, cb, wgs, s);
-        case 7: return launch_gemv_cb<7>(a, cb, wgs, s);
-        default: return launch_gemv_cb<8>(a, cb, wgs, s);
-    }
-}
 
 // workspace layout: [counters: fixed EXL3_GEMV_COUNTER_BYTES region][partials: slots * m * 128 f32].
 // The counter region has a fixed size so calls of different shapes sharing one workspace never
@@ -708,8 +246,9 @@ bool shape_ok(int m, int k, int n, int K)
 // read from gs, the table entries are the caller's contract
 int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widths, int groups,
                 const int64_t* const* tabs, int64_t ldy, int m, int k, int K, int mcg, int mul1, void* ws,
-                size_t ws_bytes, void* stream)
+                size_t ws_bytes, void* stream, bool gated = false)
 {
+    if (gated && (groups != 2 || tabs || widths[0] != widths[1] || ldy < widths[0])) return EXL3_EINVAL;
     if (!x || groups < 1 || groups > EXL3_MAX_GROUPS || ldx < k) return EXL3_EINVAL;
     // the kernel moves fp16 in 16-byte groups of 8: x rows, y rows, suh and svh 16-byte aligned
     if ((ldx & 7) || (ldy & 7) || (((uintptr_t) x) & 15)) return EXL3_EINVAL;
@@ -722,7 +261,7 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
         if (widths[i] < 1) return EXL3_EINVAL;
         total += widths[i];
     }
-    if (ldy < widths[0] || (m > 1 && ldy < total)) return EXL3_EINVAL;
+    if (ldy < widths[0] || (m > 1 && !gated && ldy < total)) return EXL3_EINVAL;
     for (int i = 0; i < groups; ++i) {
         if (!shape_ok(m, k, widths[i], K)) return EXL3_DECLINED;
         if ((uint64_t) k * widths[i] * K / 8 > 0xFFFFFFFFull) return EXL3_DECLINED;   // one raw buffer per trellis
@@ -758,7 +297,8 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
     a.ldy = ldy;
     a.counters = (uint32_t*) ws;
     a.part = (float*) ((char*) ws + COUNTER_BYTES);
-    return launch_gemv(a, K, codebook_of(mcg, mul1), p.total_wgs, (hipStream_t) stream);
+    return gated ? launch_gemv_gated(a, K, codebook_of(mcg, mul1), p.total_wgs, (hipStream_t) stream)
+                 : launch_gemv_impl<false>(a, K, codebook_of(mcg, mul1), p.total_wgs, (hipStream_t) stream);
 }
 
 }  // namespace
@@ -853,6 +393,18 @@ int exl3_gemv_mr_grouped_widths(const void* x, int64_t ldx, const void* const* t
     return gemv_common(x, ldx, gs, widths, groups, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream);
 }
 
+int exl3_gemv_silu_mul(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
+                       const void* const* suh, const void* const* svh, int m, int k, int n, int K, int mcg, int mul1,
+                       void* workspace, size_t ws_bytes, void* stream)
+{
+    if (!trellis || !suh || !svh || !y) return EXL3_EINVAL;
+    GemvGroup gs[2];
+    const int widths[2] = {n, n};
+    for (int i = 0; i < 2; ++i)
+        gs[i] = {(const uint32_t*) trellis[i], (const uint16_t*) suh[i], (const uint16_t*) svh[i], (uint16_t*) y};
+    return gemv_common(x, ldx, gs, widths, 2, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream, true);
+}
+
 int exl3_mgemm(const void* x, const int64_t* ptrs_trellis, void* y, const int64_t* ptrs_suh, void* xh,
                const int64_t* ptrs_svh, int groups, int k, int n, int K, int mcg, int mul1, void* workspace,
                size_t ws_bytes, void* stream)
@@ -913,6 +465,19 @@ int exl3_decode(const void* states, void* out_f32, int64_t count, int mcg, int m
     if (cb == 0) hipLaunchKernelGGL(decode_kernel<0>, grid, dim3(256), 0, s, (const uint16_t*) states, (float*) out_f32, count);
     else if (cb == 1) hipLaunchKernelGGL(decode_kernel<1>, grid, dim3(256), 0, s, (const uint16_t*) states, (float*) out_f32, count);
     else hipLaunchKernelGGL(decode_kernel<2>, grid, dim3(256), 0, s, (const uint16_t*) states, (float*) out_f32, count);
+    return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
+}
+
+int exl3_silu_mul(const void* gate, const void* up, int64_t ld_in, void* out, int64_t ld_out, int rows, int n,
+                  void* stream)
+{
+    if (!gate || !up || !out || rows < 0 || n < 8 || n % 8 || ld_in < n || ld_out < n || ld_in % 8 || ld_out % 8 ||
+        (((uintptr_t) gate) & 15) || (((uintptr_t) up) & 15) || (((uintptr_t) out) & 15))
+        return EXL3_EINVAL;
+    if (rows == 0) return EXL3_OK;
+    const int64_t jobs = (int64_t) rows * (n / 8);
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned) ((jobs + 255) / 256)), dim3(256), 0, (hipStream_t) stream,
+                       (const uint16_t*) gate, (const uint16_t*) up, ld_in, (uint16_t*) out, ld_out, rows, n / 8);
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 

@@ -1,0 +1,552 @@
+// exl3_gemv_kernel.h -- the fused stream-K GEMV kernel template, shared by exl3_gemv.hip (plain
+// launches) and exl3_gemv_gated.hip (gate / up launches with the SiLU-and-mul epilogue), so the two
+// sets of instantiations compile in parallel and the plain kernels are unaffected by the gated one.
+#pragma once
+#include "exl3_device.h"
+#include "../../include/exl3_mi355x.h"
+
+#include <utility>
+
+using namespace exl3;
+
+// f(integral_constant<int, I>) for I in the sequence: ring slots are indexed by constants in the
+// source, so the ring always lives in registers (a loop index here could leave it in scratch memory)
+template <class F, int... I>
+__device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&& f)
+{
+    (f(std::integral_constant<int, I>{}), ...);
+}
+
+// ============================================================================================
+// Fused GEMV with stream-K balancing
+//
+// Work unit: (128-column block cb, 128-row k slice ku) == two 64-row k steps == one Hadamard
+// block of the input; units are ordered cb-major, U in total, UPB = k / 128 per block.  The grid
+// has G workgroups (all resident); workgroup w owns units [w*U/G, (w+1)*U/G).  Wave i of a
+// workgroup covers n-tiles 2i, 2i+1 of the block; its lanes = (k-tile g of the step, n-tile,
+// q-block).  A workgroup keeps fp32 accumulators across consecutive units of one block and writes
+// one partial per block it touches; the block's completion counter counts the contributing
+// workgroups and the last one sums the partials in workgroup order (fixed for the shape, hence
+// deterministic), rounds C to fp16 and applies the output Hadamard and svh.
+// ============================================================================================
+struct GemvGroup {
+    const uint32_t* trellis;   // tile words
+    const uint16_t* suh;
+    const uint16_t* svh;
+    uint16_t* y;               // output columns of this group (row stride ldy)
+    int n;                     // width (columns)
+    int G;                     // workgroups of this group
+    int wg0;                   // its first workgroup in the flattened grid
+    int max_seg;               // partial slots per workgroup
+    int64_t part_off;          // first partial (floats) of this group
+    int cnt_off;               // first completion counter of this group
+    int h;                     // its workgroups dispatched first on their CU (weight wa; the rest wb)
+};
+
+struct GemvArgs {
+    const uint16_t* x;         // [M][ldx] fp16
+    int64_t ldx;
+    GemvGroup g[EXL3_MAX_GROUPS];
+    const int64_t* tab_trellis; // optional device pointer tables (grouped M=1 `mgemm` form): they
+    const int64_t* tab_suh;     // replace g[i].trellis / suh / svh
+    const int64_t* tab_svh;
+    int groups, M, k, UPB;
+    int wa, wb;                // unit-split weights of first-dispatched / second workgroups on a CU
+    int chunk_units;           // units whose rotated input fits the LDS at once
+    int64_t ldy;
+    float* part;               // per group: [G][max_seg][M][128] fp32 partials
+    uint32_t* counters;        // per group: [n / 128], zero between calls
+};
+
+constexpr int RED_BATCH = 16;                   // partial loads in flight per thread in the reduction
+constexpr int A_ROW = 136;                      // LDS row of one rotated 128-block (padded, halves)
+constexpr int LDS_BUDGET = 64 * 1024;           // per workgroup: 2 workgroups per CU
+constexpr int RING = 8;                         // 64-row k steps in flight per wave (even)
+constexpr int WAVES_PER_SIMD = 2;
+
+// s_waitcnt vmcnt(0) (gfx9 encoding: expcnt / lgkmcnt left at their maxima), fenced against
+// compiler reordering: every vector-memory store of this wave has completed.
+__device__ __forceinline__ void wait_stores_complete()
+{
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// SiLU-and-mul of 8 fp16 pairs with the activation kernels' roundings: silu in fp32
+// (g / (1 + exp(-g))) rounded to fp16, then the fp16 product (exact in fp32) rounded once.
+__device__ __forceinline__ u32x4 silu_mul_x8(u32x4 g, u32x4 u)
+{
+    const f16x8 gh = __builtin_bit_cast(f16x8, g), uh = __builtin_bit_cast(f16x8, u);
+    f16x8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float gf = (float) gh[i];
+        const f16 act = (f16) (gf / (1.0f + expf(-gf)));
+        r[i] = (f16) ((float) act * (float) uh[i]);
+    }
+    return __builtin_bit_cast(u32x4, r);
+}
+
+// a wave-uniform 64-bit value as a scalar (readfirstlane of both halves)
+__device__ __forceinline__ int64_t uniform_i64(int64_t v)
+{
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) v);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) ((uint64_t) v >> 32));
+    return (int64_t) (((uint64_t) hi << 32) | lo);
+}
+
+// Unit split of a group's U units over its G workgroups: workgroup w owns [lo(w), lo(w + 1)),
+// lo(w) = floor(U * S(w) / S(G)) with S(w) = wa * min(w, h) + wb * max(w - h, 0).  The first h
+// workgroups of the group are dispatched first on their CU; the SIMD arbiter favours their (older)
+// waves, so they get the larger weight wa and both waves of a CU finish their units together.  A
+// function of the shape only (never of m): rows stay bitwise equal to the m == 1 call.
+struct Split {
+    int U, G, h, wa, wb;
+    __host__ __device__ int64_t S(int w) const
+    {
+        return (int64_t) wa * (w < h ? w : h) + (int64_t) wb * (w > h ? w - h : 0);
+    }
+    __host__ __device__ int lo(int w) const { return (int) ((int64_t) U * S(w) / S(G)); }
+    // the workgroup owning unit u: the largest w in [0, G) with lo(w) <= u, i.e. S(w) <= T
+    __host__ __device__ int owner(int u) const
+    {
+        const int64_t SG = S(G);
+        const int64_t T = ((int64_t) (u + 1) * SG + U - 1) / U - 1;
+        const int w = T < (int64_t) wa * h ? (int) (T / wa) : h + (int) ((T - (int64_t) wa * h) / wb);
+        return w < G - 1 ? w : G - 1;
+    }
+    // most units any workgroup owns
+    __host__ __device__ int max_units() const
+    {
+        const int wmax = wa > wb ? wa : wb;
+        return (int) (((int64_t) U * wmax + S(G) - 1) / S(G)) + 1;
+    }
+};
+
+
+// Two workgroups (8 waves) per CU are resident at once: up to 256 registers per lane, enough for
+// a ring deep enough that one wave alone keeps its SIMD busy.
+// GATED: groups 0 (gate) and 1 (up) of equal width; the workgroup completing a block of both
+// writes fp16(fp16(silu(gate)) * up) to g[0].y instead of the two outputs.
+template <int BITS, int CB, int MT, bool GATED>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_SIMD, WAVES_PER_SIMD))) gemv_kernel(GemvArgs a)
+{
+    extern __shared__ __align__(16) uint16_t smem[];
+    __shared__ int s_last[256];
+    __shared__ int s_list[256];
+    __shared__ int s_nred;
+    // the group of this workgroup: a flattened grid, each group its own range of workgroups
+    int grp = 0;
+    if (a.groups > 1 && (int) blockIdx.x >= a.g[1].wg0) grp = 1;
+    if (a.groups > 2 && (int) blockIdx.x >= a.g[2].wg0) grp = 2;
+    if (a.groups > 3 && (int) blockIdx.x >= a.g[3].wg0) grp = 3;
+    // constant indices only: a runtime index into the kernel-argument struct would copy it to
+    // scratch memory, and every later read of it would be a vector-memory load
+    const GemvGroup gg = grp == 0 ? a.g[0] : grp == 1 ? a.g[1] : grp == 2 ? a.g[2] : a.g[3];
+    const int w = blockIdx.x - gg.wg0;
+    const int G = gg.G, UPB = a.UPB, M = a.M;
+    const int NB = gg.n / 128, NT = gg.n / 16, U = NB * UPB;
+    const Split sp{U, G, gg.h, a.wa, a.wb};
+    const uint32_t* trel = gg.trellis;
+    const uint16_t* suh = gg.suh;
+    const uint16_t* svh = gg.svh;
+    uint16_t* y = gg.y;
+    if (a.tab_trellis) {
+        // table entries are uniform (grp is): keep them in scalar registers, or the trellis buffer
+        // resource would look divergent and every buffer load would be wrapped in a waterfall loop
+        trel = reinterpret_cast<const uint32_t*>(uniform_i64(a.tab_trellis[grp]));
+        suh = reinterpret_cast<const uint16_t*>(uniform_i64(a.tab_suh[grp]));
+        svh = reinterpret_cast<const uint16_t*>(uniform_i64(a.tab_svh[grp]));
+    }
+    // a gated launch counts both groups' contributions to block cb in group 0's counter cb
+    constexpr bool gated = GATED;
+    uint32_t* const counters = a.counters + (gated ? a.g[0].cnt_off : gg.cnt_off);
+    // the trellis as one raw buffer (layers of 4 GiB and more are declined on the host)
+    const uint64_t trel_bytes = (uint64_t) a.k * gg.n * BITS / 8;
+    const __amdgpu_buffer_rsrc_t trsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(trel), 0, (int) (uint32_t) trel_bytes, RAW_BUFFER_FLAGS);
+    gc_u16* const gsuh = as_global(suh);
+    gc_u16* const gsvh = as_global(svh);
+    gc_u16* const gx = as_global(a.x);
+    g_u16* const gy = as_global(y);
+    // LDS: the rotated input of a chunk of units, M rows per unit followed by one zero row (the A
+    // operand of MFMA rows >= M), then the fp16 C of one block for the output transform
+    const int UROWS = M + 1;
+    uint16_t* lds_a = smem;                                   // [chunk_units][M + 1][A_ROW]
+    uint16_t* lds_c = smem + a.chunk_units * UROWS * A_ROW;   // [M][A_ROW]
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int g = lane >> 4, j = lane & 15, q = j & 7;
+    const int ulo = sp.lo(w), uhi = sp.lo(w + 1);
+    if (ulo >= uhi) return;                                   // uniform per workgroup
+    const int seg0_cb = ulo / UPB;
+    float* part_grp = a.part + gg.part_off;
+
+    // Trellis addressing.  Step d (0, 1) of unit (cb, ku) covers k-tiles 8ku + 4d .. +3 and n-tiles
+    // 8cb .. 8cb + 7; this lane reads q-block q of tile (k-tile + g, n-tile 8cb + 2 wave + (j >> 3)).
+    // A uniform byte offset walks the units; the lane adds fixed byte offsets.
+    const int tile_lane = (g * NT + wave * 2 + (j >> 3)) * (8 * BITS);            // words
+    const uint32_t off_main = (uint32_t) (tile_lane + q * BITS) * 4u;
+    const uint32_t off_prev = (uint32_t) (tile_lane + (q == 0 ? 8 * BITS - 1 : q * BITS - 1)) * 4u;
+    const uint32_t STEP_D = (uint32_t) (4 * NT * 8 * BITS * 4);   // bytes from step 0 to step 1 of a unit
+    const uint32_t STEP_KU = 2 * STEP_D;                          // to the next unit of the same block
+    const uint32_t STEP_CB = 8 * 8 * BITS * 4;                    // to the next block, same ku
+    const uint32_t STEP_WRAP = STEP_CB - (uint32_t) (UPB - 1) * STEP_KU;   // to ku 0 of the next block (mod 2^32)
+
+    // rotated-input job i of a chunk starting at unit u0: (unit u0 + i / M, row i % M), 16 lanes each
+    auto job_src = [&](int u0, int i, int& m, int& col) __attribute__((always_inline)) {
+        const int u = u0 + i / M;
+        m = i - (i / M) * M;
+        col = (u - (u / UPB) * UPB) * 128 + 8 * (threadIdx.x & 15);
+    };
+
+    // The prologue and the completion phase sit on every workgroup's critical path while other
+    // workgroups on the same SIMDs run VALU-heavy decode loops: give them issue priority.
+    __builtin_amdgcn_s_setprio(2);
+
+    // ---- first input chunk: its x / suh loads go out before the trellis ring ----------------
+    const int nfirst = min(a.chunk_units, uhi - ulo) * M;
+    u32x4 px = {0u, 0u, 0u, 0u}, ps = px;
+    {
+        const int i = threadIdx.x >> 4;
+        if (i < nfirst) {
+            int m, col;
+            job_src(ulo, i, m, col);
+            px = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
+            ps = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+        }
+    }
+    // ---- the trellis ring: RING steps in flight per wave ----------------------------------------
+    // Slot i always holds a step with d == i & 1.  The load cursor (ul, ku_l, lp) is the unit of the
+    // next refill; it stops at the last unit, whose steps are reloaded (in bounds, never used).
+    uint32_t Wr[RING][BITS + 1];
+    int ul = ulo, ku_l = ulo - seg0_cb * UPB;
+    uint32_t lp = (uint32_t) seg0_cb * STEP_CB + (uint32_t) ku_l * STEP_KU;
+    auto advance_load = [&]() __attribute__((always_inline)) {
+        if (ul + 1 < uhi) {
+            ++ul;
+            if (++ku_l == UPB) {
+                ku_l = 0;
+                lp += STEP_WRAP;
+            } else {
+                lp += STEP_KU;
+            }
+        }
+    };
+    static_for(std::make_integer_sequence<int, RING>{}, [&](auto I) __attribute__((always_inline)) {
+        constexpr int i = decltype(I)::value;
+        load_qblock_buf<BITS>(trsrc, off_main, off_prev, lp + (i & 1) * STEP_D, Wr[i]);
+        if (i & 1) advance_load();
+    });
+    // rotated input of units [c0, c1) -> LDS; the first 16-lane job of each lane uses (x0, s0)
+    auto rotate_chunk = [&](int c0, int c1, u32x4 x0, u32x4 s0, bool have_first) __attribute__((always_inline)) {
+        const int njobs = (c1 - c0) * M;
+        const int i = threadIdx.x >> 4;
+        if (i - (threadIdx.x & 63) / 16 < njobs) {            // waves with a job (whole 16-lane groups)
+            if (!have_first && i < njobs) {
+                int m, col;
+                job_src(c0, i, m, col);
+                x0 = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
+                s0 = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+            }
+            const u32x4 r = had128_x8(x0, s0, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
+            if (i < njobs) {
+                int m, col;
+                job_src(c0, i, m, col);
+                *reinterpret_cast<u32x4*>(lds_a + ((i / M) * UROWS + m) * A_ROW + 8 * (threadIdx.x & 15)) = r;
+            }
+            for (int i2 = i + 16; i2 - (threadIdx.x & 63) / 16 < njobs; i2 += 16) {
+                u32x4 xv = {0u, 0u, 0u, 0u}, sv = xv;
+                int m = 0, col = 0;
+                if (i2 < njobs) {
+                    job_src(c0, i2, m, col);
+                    xv = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
+                    sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+                }
+                const u32x4 r2 = had128_x8(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
+                if (i2 < njobs)
+                    *reinterpret_cast<u32x4*>(lds_a + ((i2 / M) * UROWS + m) * A_ROW + 8 * (threadIdx.x & 15)) = r2;
+            }
+        }
+    };
+    int c0 = ulo, c1 = min(ulo + a.chunk_units, uhi);
+    rotate_chunk(c0, c1, px, ps, true);
+    // zero rows: never overwritten by later chunks
+    for (int t = threadIdx.x; t < a.chunk_units * (A_ROW / 8); t += 256)
+        *reinterpret_cast<u32x4*>(lds_a + ((t / (A_ROW / 8)) * UROWS + M) * A_ROW + 8 * (t % (A_ROW / 8))) =
+            u32x4{0u, 0u, 0u, 0u};
+    __syncthreads();
+
+    // A operand row of this lane (per MFMA row tile) within a unit: rows >= M read the zero row
+    int a_lane[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) a_lane[mt] = (mt * 16 + j < M ? mt * 16 + j : M) * A_ROW + 16 * g;
+
+    f32x4 acc[2][MT];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int colb = wave * 32 + (j >> 3) * 16 + (j & 7);    // + 8h: column of this lane in the block
+    auto write_partial = [&](int cb) __attribute__((always_inline)) {
+        float* slab = part_grp + ((int64_t) w * gg.max_seg + (cb - seg0_cb)) * M * 128;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int m = mt * 16 + 4 * g + v;
+                    if (m < M)
+                        __hip_atomic_store(&slab[m * 128 + colb + 8 * h], acc[h][mt][v], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                }
+    };
+
+    // one k step: decode the slot's q-block, refill the slot from the load cursor (when the ring
+    // still has steps to fetch), two MFMAs per tile column half
+    auto step = [&](uint32_t (&Wq)[BITS + 1], const uint16_t* unit_a, int d, bool refill) __attribute__((always_inline)) {
+        uint32_t P[16];
+        decode_qblock<BITS, CB>(Wq, P);
+        if (refill) load_qblock_buf<BITS>(trsrc, off_main, off_prev, lp + d * STEP_D, Wq);
+        f16x8 A0[MT], A1[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const uint16_t* ap = unit_a + a_lane[mt] + 64 * d;
+            A0[mt] = *reinterpret_cast<const f16x8*>(ap);
+            A1[mt] = *reinterpret_cast<const f16x8*>(ap + 8);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const u32x4 B0 = {P[2 * h], P[4 + 2 * h], P[8 + 2 * h], P[12 + 2 * h]};
+            const u32x4 B1 = {P[2 * h + 1], P[5 + 2 * h], P[9 + 2 * h], P[13 + 2 * h]};
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                acc[h][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0[mt], __builtin_bit_cast(f16x8, B0), acc[h][mt], 0, 0, 0);
+                acc[h][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[mt], __builtin_bit_cast(f16x8, B1), acc[h][mt], 0, 0, 0);
+            }
+        }
+    };
+
+    int cb_cur = seg0_cb;
+    int left = UPB - (ulo - seg0_cb * UPB);                   // units of block cb_cur still to come
+    // sub-step i of the ring turn starting at unit u0 (slot i, d = i & 1)
+    auto sub_step = [&](auto I, int u0, bool refill) __attribute__((always_inline)) {
+        constexpr int i = decltype(I)::value;
+        if (!(i & 1)) {
+            if (left == 0) {                                  // a new 128-column block starts
+                write_partial(cb_cur);
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                ++cb_cur;
+                left = UPB;
+            }
+            --left;
+        }
+        step(Wr[i], lds_a + (u0 + i / 2 - c0) * UROWS * A_ROW, i & 1, refill);
+        if ((i & 1) && refill) advance_load();
+    };
+    auto next_chunk = [&](int u0) __attribute__((always_inline)) {      // chunks hold whole ring turns
+        if (u0 == c1) {
+            c0 = c1;
+            c1 = min(c0 + a.chunk_units, uhi);
+            __syncthreads();
+            rotate_chunk(c0, c1, px, ps, false);
+            __syncthreads();
+        }
+    };
+
+    __builtin_amdgcn_s_setprio(0);
+    // Full ring turns run without per-step conditions (a conditional step would make the compiler
+    // wait for every load in flight); the last, partial turn only drains the ring.
+    const int S = 2 * (uhi - ulo);                            // 64-row k steps of this workgroup
+    const int S_full = S - S % RING;
+    int s0 = 0;
+    for (; s0 < S_full; s0 += RING) {
+        const int u0 = ulo + s0 / 2;
+        next_chunk(u0);
+        static_for(std::make_integer_sequence<int, RING>{}, [&](auto I) __attribute__((always_inline)) { sub_step(I, u0, true); });
+    }
+    if (s0 < S) {
+        const int u0 = ulo + s0 / 2;
+        next_chunk(u0);
+        static_for(std::make_integer_sequence<int, RING>{}, [&](auto I) __attribute__((always_inline)) {
+            if (s0 + decltype(I)::value < S) sub_step(I, u0, false);
+        });
+    }
+    __builtin_amdgcn_s_setprio(2);
+    write_partial(cb_cur);
+
+    // ---- completion: count this workgroup into every block it touched, reduce those it completed
+    // The partials are device-scope (write-through) stores: once complete (vmcnt(0)) they are
+    // visible to device-scope loads from any XCD, so no cache-wide release is needed.
+    wait_stores_complete();
+    __syncthreads();
+    const int nblk = cb_cur - seg0_cb + 1;
+    // completed blocks reduced side by side; a gated pair is reduced alone, as 2M rows (gate, up)
+    const int RB = gated ? 1 : (M == 1 ? 2 : 1);
+    const int RM = gated ? 2 * M : M;
+    const Split sp0{U, a.g[0].G, a.g[0].h, a.wa, a.wb}, sp1{U, a.g[1].G, a.g[1].h, a.wa, a.wb};
+    for (int b0 = 0; b0 < nblk; b0 += 256) {
+        const int nb = min(256, nblk - b0);
+        if ((int) threadIdx.x < nb) {                         // one counter per thread, all in flight
+            const int cb = seg0_cb + b0 + threadIdx.x;
+            const int uf = cb * UPB, ul = cb * UPB + UPB - 1;
+            // contributors before the last one
+            const int before = gated ? sp0.owner(ul) - sp0.owner(uf) + sp1.owner(ul) - sp1.owner(uf) + 1
+                                     : sp.owner(ul) - sp.owner(uf);
+            const uint32_t prev = __hip_atomic_fetch_add(&counters[cb], 1u, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+            s_last[threadIdx.x] = prev == (uint32_t) before ? 1 : 0;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int c = 0;
+            for (int bi = 0; bi < nb; ++bi)
+                if (s_last[bi]) s_list[c++] = seg0_cb + b0 + bi;
+            s_nred = c;
+        }
+        __syncthreads();
+        const int nred = __builtin_amdgcn_readfirstlane(s_nred);
+        for (int r0 = 0; r0 < nred; r0 += RB) {
+            const int rb = min(RB, nred - r0);
+            // svh of the first output-transform pass, requested before the partial loads so that its
+            // round trip overlaps theirs
+            const int l16 = threadIdx.x & 15;
+            u32x4 sv_first = {0u, 0u, 0u, 0u}, sv_first_u = sv_first;
+            {
+                const int rr = threadIdx.x >> 4;
+                if (gated) {
+                    if (rr < M) {
+                        sv_first = *reinterpret_cast<gc_u32x4*>(as_global(a.g[0].svh) + s_list[r0] * 128 + 8 * l16);
+                        sv_first_u = *reinterpret_cast<gc_u32x4*>(as_global(a.g[1].svh) + s_list[r0] * 128 + 8 * l16);
+                    }
+                } else if (rr < rb * M) {
+                    sv_first = *reinterpret_cast<gc_u32x4*>(gsvh + s_list[r0 + rr / M] * 128 + 8 * l16);
+                }
+            }
+            // contributor wf holds block cb in its segment cb - first_cb(wf); every later
+            // contributor starts inside cb, so its segment is 0.  Loads go out in batches of
+            // RED_BATCH; the sum runs in contributor order.
+            for (int e = threadIdx.x; e < rb * RM * 128; e += 256) {
+                const int r = e / (RM * 128);
+                int el = e - r * (RM * 128);
+                const int cb = s_list[r0 + r];
+                // the group whose partials hold element el: this workgroup's, or gate / up rows
+                const bool up = gated && el >= M * 128;
+                if (up) el -= M * 128;
+                const Split spr = !gated ? sp : up ? sp1 : sp0;
+                const int max_seg = !gated ? gg.max_seg : up ? a.g[1].max_seg : a.g[0].max_seg;
+                const float* pr = !gated ? part_grp : a.part + (up ? a.g[1].part_off : a.g[0].part_off);
+                const int wf = spr.owner(cb * UPB), wl = spr.owner(cb * UPB + UPB - 1);
+                const int seg_f = cb - spr.lo(wf) / UPB;
+                const int nc = wl - wf + 1;
+                float sum = 0.f;
+                for (int cc0 = 0; cc0 < nc; cc0 += RED_BATCH) {
+                    float v[RED_BATCH];
+#pragma unroll
+                    for (int ii = 0; ii < RED_BATCH; ++ii) {
+                        const int c = cc0 + ii;
+                        const int64_t slot = c == 0 ? (int64_t) wf * max_seg + seg_f : (int64_t) (wf + c) * max_seg;
+                        v[ii] = c < nc ? __hip_atomic_load(pr + slot * M * 128 + el, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT)
+                                       : 0.f;
+                    }
+#pragma unroll
+                    for (int ii = 0; ii < RED_BATCH; ++ii)
+                        if (cc0 + ii < nc) sum += v[ii];
+                }
+                lds_c[(r * RM + (up ? M : 0) + (el >> 7)) * A_ROW + (el & 127)] = f16_bits((f16) sum);
+            }
+            if ((int) threadIdx.x < rb)                        // ready for the next call (stream order)
+                __hip_atomic_store(&counters[s_list[r0 + threadIdx.x]], 0u, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            if (gated) {
+                // gate and up rows m: output Hadamard + svh each, then SiLU-and-mul into g[0].y
+                const int cb = s_list[r0];
+                for (int rr0 = 0; rr0 < M; rr0 += 16) {
+                    const int m = rr0 + (threadIdx.x >> 4);
+                    const bool live = m < M;
+                    u32x4 cg = {0u, 0u, 0u, 0u}, cu = cg, svg = cg, svu = cg;
+                    if (live) {
+                        cg = *reinterpret_cast<const u32x4*>(lds_c + m * A_ROW + 8 * l16);
+                        cu = *reinterpret_cast<const u32x4*>(lds_c + (M + m) * A_ROW + 8 * l16);
+                        svg = rr0 == 0 ? sv_first : *reinterpret_cast<gc_u32x4*>(as_global(a.g[0].svh) + cb * 128 + 8 * l16);
+                        svu = rr0 == 0 ? sv_first_u : *reinterpret_cast<gc_u32x4*>(as_global(a.g[1].svh) + cb * 128 + 8 * l16);
+                    }
+                    const u32x4 rg = had128_x8(cg, u32x4{0u, 0u, 0u, 0u}, false, svg, true, R_SCALE);
+                    const u32x4 ru = had128_x8(cu, u32x4{0u, 0u, 0u, 0u}, false, svu, true, R_SCALE);
+                    if (live)
+                        *reinterpret_cast<g_u32x4*>(as_global(a.g[0].y) + (int64_t) m * a.ldy + cb * 128 + 8 * l16) =
+                            silu_mul_x8(rg, ru);
+                }
+                __syncthreads();
+                continue;
+            }
+            // output Hadamard + svh: 16 lanes per (block, row)
+            for (int rr0 = 0; rr0 < rb * M; rr0 += 16) {
+                const int rr = rr0 + (threadIdx.x >> 4);
+                const bool live = rr < rb * M;
+                const int r = live ? rr / M : 0, m = live ? rr - r * M : 0;
+                const int cb = s_list[r0 + r];
+                u32x4 c = {0u, 0u, 0u, 0u}, sv = c;
+                if (live) {
+                    c = *reinterpret_cast<const u32x4*>(lds_c + rr * A_ROW + 8 * l16);
+                    sv = rr0 == 0 ? sv_first : *reinterpret_cast<gc_u32x4*>(gsvh + cb * 128 + 8 * l16);
+                }
+                const u32x4 res = had128_x8(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, R_SCALE);
+                if (live) *reinterpret_cast<g_u32x4*>(gy + (int64_t) m * a.ldy + cb * 128 + 8 * l16) = res;
+            }
+            __syncthreads();                                   // lds_c free for the next blocks
+        }
+    }
+}
+
+// LDS: chunk_units x (m + 1) input rows, then the C rows of the blocks reduced side by side
+inline size_t lds_bytes(int M, int cu, bool gated) { return ((size_t) cu * (M + 1) + (gated || M == 1 ? 2 * M : M)) * A_ROW * 2; }
+
+template <int BITS, int CB, int MT, bool GATED>
+int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t stream)
+{
+    hipLaunchKernelGGL((gemv_kernel<BITS, CB, MT, GATED>), dim3(wgs), dim3(256), lds_bytes(a.M, a.chunk_units, GATED), stream, a);
+    return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
+}
+
+template <int BITS, int CB, bool GATED>
+int launch_gemv_m(const GemvArgs& a, int wgs, hipStream_t s)
+{
+    return a.M <= 16 ? launch_gemv_t<BITS, CB, 1, GATED>(a, wgs, s) : launch_gemv_t<BITS, CB, 2, GATED>(a, wgs, s);
+}
+
+template <int BITS, bool GATED>
+int launch_gemv_cb(const GemvArgs& a, int cb, int wgs, hipStream_t s)
+{
+    switch (cb) {
+        case 0: return launch_gemv_m<BITS, 0, GATED>(a, wgs, s);
+        case 1: return launch_gemv_m<BITS, 1, GATED>(a, wgs, s);
+        default: return launch_gemv_m<BITS, 2, GATED>(a, wgs, s);
+    }
+}
+
+// the kernel instantiation for (bits, codebook, rows); GATED: the gate / up form
+template <bool GATED>
+int launch_gemv_impl(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s)
+{
+    switch (bits) {
+        case 1: return launch_gemv_cb<1, GATED>(a, cb, wgs, s);
+        case 2: return launch_gemv_cb<2, GATED>(a, cb, wgs, s);
+        case 3: return launch_gemv_cb<3, GATED>(a, cb, wgs, s);
+        case 4: return launch_gemv_cb<4, GATED>(a, cb, wgs, s);
+        case 5: return launch_gemv_cb<5, GATED>(a, cb, wgs, s);
+        case 6: return launch_gemv_cb<6, GATED>(a, cb, wgs, s);
+        case 7: return launch_gemv_cb<7, GATED>(a, cb, wgs, s);
+        default: return launch_gemv_cb<8, GATED>(a, cb, wgs, s);
+    }
+}
+
+// gated instantiations live in exl3_gemv_gated.hip
+int launch_gemv_gated(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s);

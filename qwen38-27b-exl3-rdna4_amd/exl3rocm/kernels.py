@@ -218,6 +218,41 @@ def exl3_gemv_mr_grouped_widths(A, B: Sequence[torch.Tensor], C, suh: Sequence[t
                    "exl3_gemv_mr_grouped_widths")
 
 
+def exl3_gemv_silu_mul(A, B: Sequence[torch.Tensor], C, suh: Sequence[torch.Tensor], svh: Sequence[torch.Tensor],
+                       K: int, mcg: bool, mul1: bool) -> int:
+    """Gate (group 0) and up (group 1) of equal width n in one GEMV launch (m <= 32); C[m, n] gets
+    fp16(fp16(silu(gate)) * up).  No counterpart in the reference extension."""
+    _cuda(A, C, *B, *suh, *svh)
+    x2, m, k = _rows(A)
+    n = svh[0].shape[0]
+    _need(len(B) == 2 and len(suh) == 2 and len(svh) == 2 and svh[1].shape[0] == n,
+          "silu_mul: gate and up of equal width")
+    _need(C.shape[-1] >= n, "silu_mul: output narrower than n")
+    ws = workspace(A.device, gemv_workspace_bytes(m, k, n, K, 2))
+    pt, _a = L.ptr_array([b.data_ptr() for b in B])
+    ps, _b = L.ptr_array([s.data_ptr() for s in suh])
+    pv, _c = L.ptr_array([s.data_ptr() for s in svh])
+    return L.check(L.lib().exl3_gemv_silu_mul(x2.data_ptr(), x2.stride(0) if m > 1 else k, pt, C.data_ptr(),
+                                              _ldy(C, n), ps, pv, m, k, n, K, *_cb_flags(mcg, mul1), ws.data_ptr(),
+                                              ws.numel(), _stream(A)), "exl3_gemv_silu_mul")
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor) -> None:
+    """out = fp16(fp16(silu(gate)) * up) over rows of n columns (gate / up may be column slices of
+    one [rows, 2n] tensor)."""
+    _cuda(gate, up, out)
+    n = gate.shape[-1]
+    g2, u2, o2 = gate.reshape(-1, n), up.reshape(-1, n), out.reshape(-1, n)
+    rows = g2.shape[0]
+    _need(u2.shape == g2.shape and o2.shape == g2.shape, "silu_mul: gate, up and out of one shape")
+    _need(all(t.dtype == torch.float16 and t.stride(-1) == 1 for t in (g2, u2, o2)), "silu_mul: fp16, unit stride")
+    _need(rows <= 1 or g2.stride(0) == u2.stride(0), "silu_mul: gate and up rows equally spaced")
+    ld_in = g2.stride(0) if rows > 1 else n
+    ld_out = o2.stride(0) if rows > 1 else n
+    L.check(L.lib().exl3_silu_mul(g2.data_ptr(), u2.data_ptr(), ld_in, o2.data_ptr(), ld_out, rows, n,
+                                  _stream(gate)), "exl3_silu_mul")
+
+
 def exl3_mgemm(x, ptrs_trellis, y, ptrs_suh, xh, ptrs_svh, K: int, mcg: bool, mul1: bool) -> int:
     """Grouped M == 1 over int64 device pointer tables; y is (groups, 1, n)."""
     _cuda(x, ptrs_trellis, y, ptrs_suh, ptrs_svh)

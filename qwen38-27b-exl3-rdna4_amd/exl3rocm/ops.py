@@ -177,3 +177,37 @@ def exl3_linear_groups(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[t
 @exl3_linear_groups.register_fake
 def _(x, trellis, suh, svh, K, mcg, mul1, ptrs_trellis=None, ptrs_suh=None, ptrs_svh=None):
     return x.new_empty((*x.shape[:-1], sum(s.shape[0] for s in svh)), dtype=torch.float16)
+
+
+@torch.library.custom_op("exl3rocm::linear_silu_mul", mutates_args=())
+def exl3_linear_silu_mul(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[torch.Tensor],
+                         svh: list[torch.Tensor], K: list[int], mcg: bool, mul1: bool) -> torch.Tensor:
+    """A gated MLP's input: the gate (group 0) and up (group 1) linears of one module followed by
+    SiLU-and-mul, act = fp16(fp16(silu(gate)) * up) with gate / up exactly as linear_groups
+    computes them.  No counterpart in the reference plugin, whose MLP runs linear_groups and then
+    a separate SiluAndMul (the fusion is proposed in reference docs/EFFICIENCY_INVESTIGATION.md:36-66).
+
+    M <= EXL3_MR_MAX with equal K and width: one GEMV launch, the activation applied by the
+    workgroup that completes a 128-column block of both groups; otherwise linear_groups and an
+    elementwise SiLU-and-mul kernel."""
+    if not (len(trellis) == 2 and len(suh) == 2 and len(svh) == 2 and len(K) == 2):
+        raise RuntimeError("exl3rocm: linear_silu_mul takes exactly two groups (gate, up)")
+    n = svh[0].shape[0]
+    if svh[1].shape[0] != n:
+        raise RuntimeError("exl3rocm: linear_silu_mul needs gate and up of equal width")
+    x2, k = _prep(x)
+    M = x2.shape[0]
+    act = torch.empty((M, n), dtype=torch.float16, device=x.device)
+    if M == 0:
+        return act.view(*x.shape[:-1], n)
+    if M <= MR_MAX and K[0] == K[1]:
+        E.exl3_gemv_silu_mul(x2, list(trellis), act, list(suh), list(svh), K[0], mcg, mul1)
+    else:
+        gu = exl3_linear_groups(x2, trellis, suh, svh, K, mcg, mul1)
+        E.silu_mul(gu[:, :n], gu[:, n:], act)
+    return act.view(*x.shape[:-1], n)
+
+
+@exl3_linear_silu_mul.register_fake
+def _(x, trellis, suh, svh, K, mcg, mul1):
+    return x.new_empty((*x.shape[:-1], svh[0].shape[0]), dtype=torch.float16)

@@ -435,6 +435,113 @@ def test_recon_route_matches_fused_route(m, k, n):
     assert torch.equal(y.view(torch.int16), fused.view(torch.int16))
 
 
+# ---------------------------------------------------------------------------------- gated MLP input
+def gate_up(k, n, bits, m, tag="gated"):
+    mats = [synth.layer(tag, f"{part}{k}x{n}x{bits}", k, n, bits) for part in ("gate", "up")]
+    x = synth.activations(synth.key_of(tag, f"{k}x{n}x{bits}", "x", m), m, k)
+    dev = [to_dev(tr.view(np.int16), su, sv) for tr, su, sv in mats]
+    return x, mats, [d[0] for d in dev], [d[1] for d in dev], [d[2] for d in dev]
+
+
+def torch_silu_mul(gu, n):
+    """SiluAndMul as torch computes it in fp16: silu in fp32 rounded to fp16, fp16 product."""
+    return torch.nn.functional.silu(gu[:, :n]) * gu[:, n:]
+
+
+@pytest.mark.parametrize("m,k,n,bits", [(1, 512, 1024, 4), (4, 1024, 2048, 3), (16, 256, 512, 5), (32, 512, 256, 2),
+                                        (1, 5120, 17408, 4), (8, 5120, 17408, 4)])
+def test_gemv_silu_mul_matches_unfused(m, k, n, bits):
+    """The gated GEMV == linear_groups followed by SiLU-and-mul (both elementwise routes, ours and
+    torch's fp16 silu * up), bitwise, and every row == its m == 1 call."""
+    x, mats, T, SU, SV = gate_up(k, n, bits, m)
+    X = to_dev(x)[0]
+    act = torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True)
+    gu = torch.ops.exl3rocm.linear_groups(X, T, SU, SV, [bits, bits], False, True)
+    ours = torch.empty_like(act)
+    E.silu_mul(gu[:, :n], gu[:, n:], ours)
+    assert torch.equal(act.view(torch.int16), ours.view(torch.int16))
+    ref = torch_silu_mul(gu, n).float()
+    a = act.float()
+    same = a == ref                                   # includes the +-inf of fp16 overflow
+    ulp = (ref.abs() * 2.0 ** -10).clamp_min(2.0 ** -24)
+    assert (same | ((a - ref).abs() <= ulp)).all(), "vs torch silu * up: within one fp16 ulp"
+    assert (~same).float().mean().item() <= 1e-3, "vs torch silu * up: last-place flips are rare"
+    a1 = torch.ops.exl3rocm.linear_silu_mul(X[:1], T, SU, SV, [bits, bits], False, True)
+    assert torch.equal(act[:1].view(torch.int16), a1.view(torch.int16))
+    again = torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True)
+    assert torch.equal(act.view(torch.int16), again.view(torch.int16))       # counters reset
+
+
+def test_gemv_silu_mul_vs_oracle():
+    """Against the oracle: gate and up from the faithful linear, then fp16(fp16(silu(g)) * u) in
+    float64 (one rounding each)."""
+    m, k, n, bits = 3, 1024, 1536, 4
+    x, mats, T, SU, SV = gate_up(k, n, bits, m, tag="gated-oracle")
+    act = torch.ops.exl3rocm.linear_silu_mul(to_dev(x)[0], T, SU, SV, [bits, bits], False, True)
+    g, u = (cpu.linear(x, tr, bits, su, sv, 2) for tr, su, sv in mats)
+    with np.errstate(over="ignore"):                  # exp(-g) = inf for very negative g: silu -> -0
+        ref = O.to_f16(O.to_f16(g / (1.0 + np.exp(-g))) * u)
+    assert_close(act.cpu().numpy(), ref, "gated vs oracle")
+
+
+def test_silu_mul_kernel_special_values():
+    vals = torch.tensor([0.0, -0.0, 1.0, -1.0, 6.0, -6.0, 11.0, -11.0, 17.5, -17.5, 65504.0, -65504.0,
+                         2.0 ** -24, -(2.0 ** -24), 2.0 ** -14, 0.5, -0.5, 3.140625], dtype=torch.float16)
+    g = vals.repeat_interleave(vals.numel()).to(DEV)
+    u = vals.repeat(vals.numel()).to(DEV)
+    n = 8 * ((g.numel() + 7) // 8)
+    G = torch.zeros(2, n, dtype=torch.float16, device=DEV)
+    U = torch.zeros(2, n, dtype=torch.float16, device=DEV)
+    G[:, :g.numel()] = g
+    U[:, :u.numel()] = u
+    out = torch.full((2, n), float("nan"), dtype=torch.float16, device=DEV)
+    E.silu_mul(G, U, out)
+    ref = torch.nn.functional.silu(G) * U
+    assert torch.equal(torch.isnan(out), torch.isnan(ref))
+    fin = ~torch.isnan(ref)
+    o, r = out[fin].float(), ref[fin].float()
+    ulp = (r.abs() * 2.0 ** -10).clamp_min(2.0 ** -24)
+    assert ((o == r) | ((o - r).abs() <= ulp)).all()
+
+
+def test_linear_silu_mul_prefill_route():
+    """M > 32: the grouped prefill, then the elementwise kernel: == linear_groups + silu_mul."""
+    m, k, n, bits = 300, 512, 1024, 4
+    x, mats, T, SU, SV = gate_up(k, n, bits, m, tag="gated-prefill")
+    X = to_dev(x)[0]
+    act = torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True)
+    gu = torch.ops.exl3rocm.linear_groups(X, T, SU, SV, [bits, bits], False, True)
+    ours = torch.empty_like(act)
+    E.silu_mul(gu[:, :n], gu[:, n:], ours)
+    assert torch.equal(act.view(torch.int16), ours.view(torch.int16))
+    g, u = (cpu.linear(x[:4], tr, bits, su, sv, 2) for tr, su, sv in mats)
+    with np.errstate(over="ignore"):
+        ref = O.to_f16(O.to_f16(g / (1.0 + np.exp(-g))) * u)
+    assert_close(act[:4].cpu().numpy(), ref, "prefill gated vs oracle")
+
+
+def test_gemv_silu_mul_graph_replays():
+    m, k, n, bits = 1, 1024, 2048, 4
+    x, mats, T, SU, SV = gate_up(k, n, bits, m, tag="gated-graph")
+    X = to_dev(x)[0]
+    eager = torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.reserve_workspace(DEV, k, n, bits, groups=2)
+        torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        y = torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), eager.view(torch.int16))
+        torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True)
+        torch.cuda.synchronize()
+
+
 # ---------------------------------------------------------------------------------- plugin surface
 def test_linear_method_end_to_end():
     from exl3rocm import plugin
