@@ -174,6 +174,55 @@ def per_shape_gemv(torch, sets, x5120, x17408, reps=64):
     return out
 
 
+def gated_mlp(torch, sets, x5120, ms=(1, 8), reps=32):
+    """The MLP input of config 1: gate/up + SiLU-and-mul fused into one GEMV launch
+    (linear_silu_mul) against the unfused pair (linear_groups, then the elementwise kernel);
+    mean duration per call from a graph of `reps` calls over the weight copies."""
+    from exl3rocm import kernels as E
+    ops = torch.ops.exl3rocm
+    n = INTER
+    out = {}
+    s = torch.cuda.Stream()
+    for m in ms:
+        x = x5120.expand(m, HIDDEN).contiguous()
+        act = torch.empty(m, n, dtype=torch.float16, device="cuda")
+
+        def fused(ls):
+            w = ls.w
+            ops.linear_silu_mul(x, [w["gate"][0], w["up"][0]], [w["gate"][1], w["up"][1]],
+                                [w["gate"][2], w["up"][2]], [ls.bits, ls.bits], ls.mcg, ls.mul1)
+
+        def unfused(ls):
+            w = ls.w
+            ptrs = ls.gu_ptrs if m == 1 else [None] * 3
+            gu = ops.linear_groups(x, [w["gate"][0], w["up"][0]], [w["gate"][1], w["up"][1]],
+                                   [w["gate"][2], w["up"][2]], [ls.bits, ls.bits], ls.mcg, ls.mul1, *ptrs)
+            E.silu_mul(gu[:, :n], gu[:, n:], act)
+
+        row = {}
+        for tag, fn in (("fused_us", fused), ("unfused_us", unfused)):
+            with torch.cuda.stream(s):
+                for ls in sets:
+                    fn(ls)
+            s.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                for r in range(reps):
+                    fn(sets[r % len(sets)])
+            with torch.cuda.stream(s):
+                g.replay()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(s)
+                for _ in range(3):
+                    g.replay()
+                e1.record(s)
+            s.synchronize()
+            row[tag] = round(e0.elapsed_time(e1) * 1e3 / (3 * reps), 2)
+            del g
+        out[f"m{m}"] = row
+    return out
+
+
 def cpu_baseline(base, bits, budget_s=12.0):
     """The C oracle's faithful GEMV over the layer's 7 linears (M = 1), repeated within a time
     budget on the host cores; GB/s of the same algorithmic bytes."""
@@ -367,6 +416,8 @@ def main() -> int:
     extra = {"launches_per_step": lps, "step_bytes": step_bytes, "wall_s": round(wall, 3)}
     log("per-shape GEMV timing")
     extra["per_shape_m1"] = per_shape_gemv(torch, sets, x5120, x17408)
+    log("gated MLP input (gate/up + SiLU-and-mul)")
+    extra["gated_mlp"] = gated_mlp(torch, sets, x5120)
     if not args.no_sweep:
         log("small-batch crossover")
         extra["config3_small_batch"] = small_batch(torch, sets)

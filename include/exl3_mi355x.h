@@ -122,6 +122,13 @@ int exl3_gemv_mr_grouped_widths(const void* x, int64_t ldx, const void* const* t
  * counterpart, as exl3_gemv_workspace_size. */
 size_t exl3_gemv_workspace_size_widths(int m, int k, const int* widths, int groups);
 
+/* Self-check of the GEMV's stream-K unit split (host only, no GPU): the kernels' 32-bit
+ * multiply-high division forms of lo(w) and owner(u) against 64-bit arithmetic and brute force for
+ * U units over G workgroups (h of them weighted wa, the rest wb), plus the divider at its range
+ * edges.  Returns the number of mismatches (0), or -1 for arguments outside the split's domain.
+ * No reference counterpart.  Callers: the CPU tests. */
+int exl3_gemv_split_check(int U, int G, int h, int wa, int wb);
+
 /* Gated MLP input, 1 <= m <= 32: the gate (group 0) and up (group 1) linears of one module, equal
  * K and width n, share x and one stream-K launch; y[m, n] (rows ldy apart, ldy >= n) receives
  * fp16(fp16(silu(gate)) * up), where gate and up are exactly what exl3_gemv_mr_grouped writes

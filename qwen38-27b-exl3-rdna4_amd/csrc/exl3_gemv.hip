@@ -151,6 +151,7 @@ struct GridPlan {
     int64_t slots;
     int max_per;                         // most units any workgroup owns
     int h[EXL3_MAX_GROUPS], wa, wb;      // unit-split weights (Split)
+    Split split[EXL3_MAX_GROUPS];
 };
 
 // Unit-split weights of first-dispatched / second workgroups on a CU: the measured issue share of
@@ -201,7 +202,8 @@ GridPlan plan_grid(int k, const int* widths, int groups)
         // contributes to it)
         const bool weighted = (int64_t) Ui * std::min(p.wa, p.wb) >= (int64_t) std::max(p.wa, p.wb) * Gs[i];
         p.h[i] = weighted ? std::min(std::max(first - wg, 0), Gs[i]) : Gs[i];
-        const Split sp{Ui, Gs[i], p.h[i], p.wa, p.wb};
+        const Split sp = Split::make(Ui, Gs[i], p.h[i], p.wa, p.wb);
+        p.split[i] = sp;
         const int per = sp.max_units();
         p.max_seg[i] = (per + UPB - 1) / UPB + 1;
         p.cnt_off[i] = cnt;
@@ -221,7 +223,9 @@ GridPlan plan_grid(int k, const int* widths, int groups)
 // is not the last one holds whole ring turns (RING / 2 units)
 int chunk_units(int m, int max_per)
 {
-    const int64_t fit = std::max<int64_t>(RING / 2, ((LDS_BUDGET / (2 * A_ROW) - 2 * m) / (m + 1)) / (RING / 2) * (RING / 2));
+    // the C rows of the output transform: at most max(2m, 4) (gated pairs side by side at m == 1)
+    const int c_rows = std::max(2 * m, 4);
+    const int64_t fit = std::max<int64_t>(RING / 2, ((LDS_BUDGET / (2 * A_ROW) - c_rows) / (m + 1)) / (RING / 2) * (RING / 2));
     return (int) std::max<int64_t>(1, std::min<int64_t>(max_per, fit));
 }
 
@@ -268,6 +272,8 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
     }
     const GridPlan p = plan_grid(k, widths, groups);
     if ((size_t) p.counters * 4 > COUNTER_BYTES) return EXL3_DECLINED;
+    for (int i = 0; i < groups; ++i)
+        if (!p.split[i].fits32()) return EXL3_DECLINED;   // unreachable below the 4 GiB trellis limit
     if (!ws || ws_bytes < COUNTER_BYTES + (size_t) p.slots * m * 128 * 4) return EXL3_EWORKSPACE;
     GemvArgs a{};
     a.x = (const uint16_t*) x;
@@ -281,9 +287,13 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
         a.g[i].part_off = p.slot_off[i] * m * 128;
         a.g[i].cnt_off = p.cnt_off[i];
         a.g[i].h = p.h[i];
+        a.g[i].d_sg = p.split[i].d_sg;
+        a.g[i].d_u = p.split[i].d_u;
     }
     a.wa = p.wa;
     a.wb = p.wb;
+    a.d_wa = UDiv::of((uint32_t) p.wa);
+    a.d_wb = UDiv::of((uint32_t) p.wb);
     if (tabs) {
         a.tab_trellis = tabs[0];
         a.tab_suh = tabs[1];
@@ -331,6 +341,33 @@ size_t exl3_gemv_workspace_size_widths(int m, int k, const int* widths, int grou
     for (int i = 0; i < groups; ++i)
         if (!shape_ok(m, k, widths[i], 1)) return 0;
     return gemv_ws_bytes(m, k, widths, groups);
+}
+
+int exl3_gemv_split_check(int U, int G, int h, int wa, int wb)
+{
+    if (U < 1 || G < 1 || h < 0 || h > G || wa < 1 || wb < 1) return -1;
+    const Split sp = Split::make(U, G, h, wa, wb);
+    if (!sp.fits32()) return -1;
+    // 64-bit restatement: lo(w) = floor(U S(w) / S(G)), owner(u) = the largest w < G with lo(w) <= u
+    auto S64 = [&](int w) { return (int64_t) wa * std::min(w, h) + (int64_t) wb * std::max(w - h, 0); };
+    auto lo64 = [&](int w) { return (int) ((int64_t) U * S64(w) / S64(G)); };
+    int bad = 0;
+    for (int w = 0; w <= G; ++w) bad += sp.lo(w) != lo64(w);
+    int w = 0;
+    for (int u = 0; u < U; ++u) {
+        while (w + 1 < G && lo64(w + 1) <= u) ++w;
+        bad += sp.owner(u) != w;
+    }
+    // the divider at the edges of its range for each divisor
+    const UDiv ds[4] = {sp.d_sg, sp.d_u, sp.d_wa, sp.d_wb};
+    const uint32_t dv[4] = {sp.S(G), (uint32_t) U, (uint32_t) wa, (uint32_t) wb};
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t d = dv[i];
+        const uint32_t ns[] = {0u, 1u, d - 1u, d, d + 1u, 2u * d - 1u, 2u * d, 0x7FFFFFFFu, 0x80000000u, 0xFFFFFFFEu, 0xFFFFFFFFu,
+                               0xFFFFFFFFu / d * d, 0xFFFFFFFFu / d * d - 1u};
+        for (uint32_t n : ns) bad += ds[i].div(n) != n / d;
+    }
+    return bad;
 }
 
 int exl3_gemv_mr_supported(int m, int k, int n, int K, int mcg, int mul1)

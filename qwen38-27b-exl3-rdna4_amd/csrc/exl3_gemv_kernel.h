@@ -29,6 +29,30 @@ __device__ __forceinline__ void static_for(std::integer_sequence<int, I...>, F&&
 // workgroups and the last one sums the partials in workgroup order (fixed for the shape, hence
 // deterministic), rounds C to fp16 and applies the output Hadamard and svh.
 // ============================================================================================
+// n / d for 32-bit unsigned n and an invariant divisor d >= 1 in a multiply-high, a subtract and
+// two shifts (Granlund and Montgomery, "Division by invariant integers using multiplication",
+// PLDI 1994, figure 4.1): m = floor(2^32 (2^l - d) / d) + 1 with l = ceil(log2 d).  The unit
+// split's divisions run on the completion path of every launch; 64-bit divisions there cost
+// hundreds of instructions each.
+struct UDiv {
+    uint32_t m, s1, s2;
+    static UDiv of(uint32_t d)
+    {
+        int l = 0;
+        while ((1ull << l) < d) ++l;
+        UDiv r;
+        r.m = (uint32_t) (((1ull << 32) * ((1ull << l) - d)) / d + 1);
+        r.s1 = l > 0 ? 1u : 0u;
+        r.s2 = l > 0 ? (uint32_t) (l - 1) : 0u;
+        return r;
+    }
+    __host__ __device__ uint32_t div(uint32_t n) const
+    {
+        const uint32_t t = (uint32_t) (((uint64_t) m * n) >> 32);
+        return (t + ((n - t) >> s1)) >> s2;
+    }
+};
+
 struct GemvGroup {
     const uint32_t* trellis;   // tile words
     const uint16_t* suh;
@@ -41,6 +65,7 @@ struct GemvGroup {
     int64_t part_off;          // first partial (floats) of this group
     int cnt_off;               // first completion counter of this group
     int h;                     // its workgroups dispatched first on their CU (weight wa; the rest wb)
+    UDiv d_sg, d_u;            // its split's divisions by S(G) and U
 };
 
 struct GemvArgs {
@@ -52,6 +77,7 @@ struct GemvArgs {
     const int64_t* tab_svh;
     int groups, M, k, UPB;
     int wa, wb;                // unit-split weights of first-dispatched / second workgroups on a CU
+    UDiv d_wa, d_wb;
     int chunk_units;           // units whose rotated input fits the LDS at once
     int64_t ldy;
     float* part;               // per group: [G][max_seg][M][128] fp32 partials
@@ -103,21 +129,33 @@ __device__ __forceinline__ int64_t uniform_i64(int64_t v)
 // function of the shape only (never of m): rows stay bitwise equal to the m == 1 call.
 struct Split {
     int U, G, h, wa, wb;
-    __host__ __device__ int64_t S(int w) const
+    UDiv d_sg, d_u, d_wa, d_wb;          // divisions by S(G), U, wa and wb
+    static Split make(int U, int G, int h, int wa, int wb)
     {
-        return (int64_t) wa * (w < h ? w : h) + (int64_t) wb * (w > h ? w - h : 0);
+        Split s{U, G, h, wa, wb, {}, {}, {}, {}};
+        s.d_sg = UDiv::of(s.S(G));
+        s.d_u = UDiv::of((uint32_t) U);
+        s.d_wa = UDiv::of((uint32_t) wa);
+        s.d_wb = UDiv::of((uint32_t) wb);
+        return s;
     }
-    __host__ __device__ int lo(int w) const { return (int) ((int64_t) U * S(w) / S(G)); }
+    __host__ __device__ uint32_t S(int w) const
+    {
+        return (uint32_t) wa * (uint32_t) (w < h ? w : h) + (uint32_t) wb * (uint32_t) (w > h ? w - h : 0);
+    }
+    __host__ __device__ int lo(int w) const { return (int) d_sg.div((uint32_t) U * S(w)); }
     // the workgroup owning unit u: the largest w in [0, G) with lo(w) <= u, i.e. S(w) <= T
     __host__ __device__ int owner(int u) const
     {
-        const int64_t SG = S(G);
-        const int64_t T = ((int64_t) (u + 1) * SG + U - 1) / U - 1;
-        const int w = T < (int64_t) wa * h ? (int) (T / wa) : h + (int) ((T - (int64_t) wa * h) / wb);
+        const uint32_t T = d_u.div((uint32_t) (u + 1) * S(G) + (uint32_t) (U - 1)) - 1u;
+        const uint32_t wah = (uint32_t) wa * (uint32_t) h;
+        const int w = T < wah ? (int) d_wa.div(T) : h + (int) d_wb.div(T - wah);
         return w < G - 1 ? w : G - 1;
     }
+    // the 32-bit forms above hold: every numerator is at most U * S(G) + U - 1
+    bool fits32() const { return (uint64_t) U * S(G) + (uint64_t) U < (1ull << 32); }
     // most units any workgroup owns
-    __host__ __device__ int max_units() const
+    int max_units() const
     {
         const int wmax = wa > wb ? wa : wb;
         return (int) (((int64_t) U * wmax + S(G) - 1) / S(G)) + 1;
@@ -136,6 +174,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     __shared__ int s_last[256];
     __shared__ int s_list[256];
     __shared__ int s_nred;
+    // per block of a counting batch: first contributor, contributor count, the first contributor's
+    // segment holding the block (gated: for gate, then up)
+    __shared__ int s_own[GATED ? 6 : 3][256];
     // the group of this workgroup: a flattened grid, each group its own range of workgroups
     int grp = 0;
     if (a.groups > 1 && (int) blockIdx.x >= a.g[1].wg0) grp = 1;
@@ -147,7 +188,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     const int w = blockIdx.x - gg.wg0;
     const int G = gg.G, UPB = a.UPB, M = a.M;
     const int NB = gg.n / 128, NT = gg.n / 16, U = NB * UPB;
-    const Split sp{U, G, gg.h, a.wa, a.wb};
+    const Split sp{U, G, gg.h, a.wa, a.wb, gg.d_sg, gg.d_u, a.d_wa, a.d_wb};
     const uint32_t* trel = gg.trellis;
     const uint16_t* suh = gg.suh;
     const uint16_t* svh = gg.svh;
@@ -386,27 +427,45 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     wait_stores_complete();
     __syncthreads();
     const int nblk = cb_cur - seg0_cb + 1;
-    // completed blocks reduced side by side; a gated pair is reduced alone, as 2M rows (gate, up)
-    const int RB = gated ? 1 : (M == 1 ? 2 : 1);
+    // completed blocks (gated: block pairs, 2M rows each: gate, then up) reduced side by side
+    const int RB = M == 1 ? 2 : 1;
     const int RM = gated ? 2 * M : M;
-    const Split sp0{U, a.g[0].G, a.g[0].h, a.wa, a.wb}, sp1{U, a.g[1].G, a.g[1].h, a.wa, a.wb};
+    const Split sp0{U, a.g[0].G, a.g[0].h, a.wa, a.wb, a.g[0].d_sg, a.g[0].d_u, a.d_wa, a.d_wb};
+    const Split sp1{U, a.g[1].G, a.g[1].h, a.wa, a.wb, a.g[1].d_sg, a.g[1].d_u, a.d_wa, a.d_wb};
     for (int b0 = 0; b0 < nblk; b0 += 256) {
         const int nb = min(256, nblk - b0);
         if ((int) threadIdx.x < nb) {                         // one counter per thread, all in flight
-            const int cb = seg0_cb + b0 + threadIdx.x;
-            const int uf = cb * UPB, ul = cb * UPB + UPB - 1;
-            // contributors before the last one
-            const int before = gated ? sp0.owner(ul) - sp0.owner(uf) + sp1.owner(ul) - sp1.owner(uf) + 1
-                                     : sp.owner(ul) - sp.owner(uf);
+            const int t = threadIdx.x;
+            const int cb = seg0_cb + b0 + t;
             const uint32_t prev = __hip_atomic_fetch_add(&counters[cb], 1u, __ATOMIC_RELAXED,
                                                          __HIP_MEMORY_SCOPE_AGENT);
-            s_last[threadIdx.x] = prev == (uint32_t) before ? 1 : 0;
+            // the block's contributors (integer divisions) while the counter round trip is in flight
+            __builtin_amdgcn_sched_barrier(0);
+            const int uf = cb * UPB, ul = cb * UPB + UPB - 1;
+            int before;                                       // contributors before the last one
+            if constexpr (GATED) {
+                const int wf0 = sp0.owner(uf), wl0 = sp0.owner(ul), wf1 = sp1.owner(uf), wl1 = sp1.owner(ul);
+                s_own[0][t] = wf0;
+                s_own[1][t] = wl0 - wf0 + 1;
+                s_own[2][t] = cb - sp0.lo(wf0) / UPB;
+                s_own[3][t] = wf1;
+                s_own[4][t] = wl1 - wf1 + 1;
+                s_own[5][t] = cb - sp1.lo(wf1) / UPB;
+                before = wl0 - wf0 + wl1 - wf1 + 1;
+            } else {
+                const int wf = sp.owner(uf), wl = sp.owner(ul);
+                s_own[0][t] = wf;
+                s_own[1][t] = wl - wf + 1;
+                s_own[2][t] = cb - sp.lo(wf) / UPB;
+                before = wl - wf;
+            }
+            s_last[t] = prev == (uint32_t) before ? 1 : 0;
         }
         __syncthreads();
         if (threadIdx.x == 0) {
             int c = 0;
             for (int bi = 0; bi < nb; ++bi)
-                if (s_last[bi]) s_list[c++] = seg0_cb + b0 + bi;
+                if (s_last[bi]) s_list[c++] = bi;             // index in the batch (block seg0_cb + b0 + bi)
             s_nred = c;
         }
         __syncthreads();
@@ -420,61 +479,109 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             {
                 const int rr = threadIdx.x >> 4;
                 if (gated) {
-                    if (rr < M) {
-                        sv_first = *reinterpret_cast<gc_u32x4*>(as_global(a.g[0].svh) + s_list[r0] * 128 + 8 * l16);
-                        sv_first_u = *reinterpret_cast<gc_u32x4*>(as_global(a.g[1].svh) + s_list[r0] * 128 + 8 * l16);
+                    if (rr < rb * M) {
+                        const int cb = seg0_cb + b0 + s_list[r0 + rr / M];
+                        sv_first = *reinterpret_cast<gc_u32x4*>(as_global(a.g[0].svh) + cb * 128 + 8 * l16);
+                        sv_first_u = *reinterpret_cast<gc_u32x4*>(as_global(a.g[1].svh) + cb * 128 + 8 * l16);
                     }
                 } else if (rr < rb * M) {
-                    sv_first = *reinterpret_cast<gc_u32x4*>(gsvh + s_list[r0 + rr / M] * 128 + 8 * l16);
+                    sv_first = *reinterpret_cast<gc_u32x4*>(gsvh + (seg0_cb + b0 + s_list[r0 + rr / M]) * 128 + 8 * l16);
                 }
             }
             // contributor wf holds block cb in its segment cb - first_cb(wf); every later
             // contributor starts inside cb, so its segment is 0.  Loads go out in batches of
-            // RED_BATCH; the sum runs in contributor order.
-            for (int e = threadIdx.x; e < rb * RM * 128; e += 256) {
+            // RED_BATCH and each sum runs in contributor order; the gated form sums two elements at
+            // a time with both elements' loads in flight together (its passes hold twice the rows).
+            const int total = rb * RM * 128;
+            // element e of the pass: contributor 0's partial, contributor 1's (the rest follow
+            // cstride floats apart), the contributor count and the element's LDS slot
+            auto elem = [&](int e, const float*& p0, const float*& p1, int64_t& cstride, int& nc, int& lofs)
+                __attribute__((always_inline)) {
                 const int r = e / (RM * 128);
                 int el = e - r * (RM * 128);
-                const int cb = s_list[r0 + r];
+                const int bi = s_list[r0 + r];
                 // the group whose partials hold element el: this workgroup's, or gate / up rows
                 const bool up = gated && el >= M * 128;
                 if (up) el -= M * 128;
-                const Split spr = !gated ? sp : up ? sp1 : sp0;
                 const int max_seg = !gated ? gg.max_seg : up ? a.g[1].max_seg : a.g[0].max_seg;
                 const float* pr = !gated ? part_grp : a.part + (up ? a.g[1].part_off : a.g[0].part_off);
-                const int wf = spr.owner(cb * UPB), wl = spr.owner(cb * UPB + UPB - 1);
-                const int seg_f = cb - spr.lo(wf) / UPB;
-                const int nc = wl - wf + 1;
-                float sum = 0.f;
-                for (int cc0 = 0; cc0 < nc; cc0 += RED_BATCH) {
-                    float v[RED_BATCH];
+                const int wf = s_own[up ? 3 : 0][bi], seg_f = s_own[up ? 5 : 2][bi];
+                nc = s_own[up ? 4 : 1][bi];
+                cstride = (int64_t) max_seg * M * 128;
+                p0 = pr + ((int64_t) wf * max_seg + seg_f) * M * 128 + el;
+                p1 = pr + (int64_t) (wf + 1) * cstride + el;
+                lofs = (r * RM + (up ? M : 0) + (el >> 7)) * A_ROW + (el & 127);
+            };
+            auto part_load = [&](const float* p0, const float* p1, int64_t cstride, int c) __attribute__((always_inline)) {
+                return __hip_atomic_load(c == 0 ? p0 : p1 + (int64_t) (c - 1) * cstride, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+            };
+            if constexpr (!GATED) {
+                for (int e = threadIdx.x; e < total; e += 256) {
+                    const int r = e / (M * 128), el = e - r * (M * 128);
+                    const int bi = s_list[r0 + r];
+                    const int wf = s_own[0][bi], nc = s_own[1][bi], seg_f = s_own[2][bi];
+                    float sum = 0.f;
+                    for (int cc0 = 0; cc0 < nc; cc0 += RED_BATCH) {
+                        float v[RED_BATCH];
 #pragma unroll
-                    for (int ii = 0; ii < RED_BATCH; ++ii) {
-                        const int c = cc0 + ii;
-                        const int64_t slot = c == 0 ? (int64_t) wf * max_seg + seg_f : (int64_t) (wf + c) * max_seg;
-                        v[ii] = c < nc ? __hip_atomic_load(pr + slot * M * 128 + el, __ATOMIC_RELAXED,
-                                                           __HIP_MEMORY_SCOPE_AGENT)
-                                       : 0.f;
+                        for (int ii = 0; ii < RED_BATCH; ++ii) {
+                            const int c = cc0 + ii;
+                            const int64_t slot = c == 0 ? (int64_t) wf * gg.max_seg + seg_f : (int64_t) (wf + c) * gg.max_seg;
+                            v[ii] = c < nc ? __hip_atomic_load(part_grp + slot * M * 128 + el, __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_AGENT)
+                                           : 0.f;
+                        }
+#pragma unroll
+                        for (int ii = 0; ii < RED_BATCH; ++ii)
+                            if (cc0 + ii < nc) sum += v[ii];
                     }
-#pragma unroll
-                    for (int ii = 0; ii < RED_BATCH; ++ii)
-                        if (cc0 + ii < nc) sum += v[ii];
+                    lds_c[(r * M + (el >> 7)) * A_ROW + (el & 127)] = f16_bits((f16) sum);
                 }
-                lds_c[(r * RM + (up ? M : 0) + (el >> 7)) * A_ROW + (el & 127)] = f16_bits((f16) sum);
+            } else {
+                for (int e0 = threadIdx.x; e0 < total; e0 += 512) {
+                    const bool has_b = e0 + 256 < total;
+                    const float *pa0, *pa1, *pb0 = nullptr, *pb1 = nullptr;
+                    int64_t csa, csb = 0;
+                    int na, nb = 0, la, lb = 0;
+                    elem(e0, pa0, pa1, csa, na, la);
+                    if (has_b) elem(e0 + 256, pb0, pb1, csb, nb, lb);
+                    float sa = 0.f, sb = 0.f;
+                    const int nmax = na > nb ? na : nb;
+                    for (int cc0 = 0; cc0 < nmax; cc0 += RED_BATCH) {
+                        float va[RED_BATCH], vb[RED_BATCH];
+#pragma unroll
+                        for (int ii = 0; ii < RED_BATCH; ++ii) {
+                            const int c = cc0 + ii;
+                            va[ii] = c < na ? part_load(pa0, pa1, csa, c) : 0.f;
+                            vb[ii] = c < nb ? part_load(pb0, pb1, csb, c) : 0.f;
+                        }
+#pragma unroll
+                        for (int ii = 0; ii < RED_BATCH; ++ii) {
+                            if (cc0 + ii < na) sa += va[ii];
+                            if (cc0 + ii < nb) sb += vb[ii];
+                        }
+                    }
+                    lds_c[la] = f16_bits((f16) sa);
+                    if (has_b) lds_c[lb] = f16_bits((f16) sb);
+                }
             }
             if ((int) threadIdx.x < rb)                        // ready for the next call (stream order)
-                __hip_atomic_store(&counters[s_list[r0 + threadIdx.x]], 0u, __ATOMIC_RELAXED,
+                __hip_atomic_store(&counters[seg0_cb + b0 + s_list[r0 + threadIdx.x]], 0u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
             __syncthreads();
             if (gated) {
-                // gate and up rows m: output Hadamard + svh each, then SiLU-and-mul into g[0].y
-                const int cb = s_list[r0];
-                for (int rr0 = 0; rr0 < M; rr0 += 16) {
-                    const int m = rr0 + (threadIdx.x >> 4);
-                    const bool live = m < M;
+                // gate and up rows m of pair r: output Hadamard + svh each, then SiLU-and-mul
+                // into g[0].y
+                for (int rr0 = 0; rr0 < rb * M; rr0 += 16) {
+                    const int rr = rr0 + (threadIdx.x >> 4);
+                    const bool live = rr < rb * M;
+                    const int r = live ? rr / M : 0, m = live ? rr - r * M : 0;
+                    const int cb = seg0_cb + b0 + s_list[r0 + r];
                     u32x4 cg = {0u, 0u, 0u, 0u}, cu = cg, svg = cg, svu = cg;
                     if (live) {
-                        cg = *reinterpret_cast<const u32x4*>(lds_c + m * A_ROW + 8 * l16);
-                        cu = *reinterpret_cast<const u32x4*>(lds_c + (M + m) * A_ROW + 8 * l16);
+                        cg = *reinterpret_cast<const u32x4*>(lds_c + (r * RM + m) * A_ROW + 8 * l16);
+                        cu = *reinterpret_cast<const u32x4*>(lds_c + (r * RM + M + m) * A_ROW + 8 * l16);
                         svg = rr0 == 0 ? sv_first : *reinterpret_cast<gc_u32x4*>(as_global(a.g[0].svh) + cb * 128 + 8 * l16);
                         svu = rr0 == 0 ? sv_first_u : *reinterpret_cast<gc_u32x4*>(as_global(a.g[1].svh) + cb * 128 + 8 * l16);
                     }
@@ -492,7 +599,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 const int rr = rr0 + (threadIdx.x >> 4);
                 const bool live = rr < rb * M;
                 const int r = live ? rr / M : 0, m = live ? rr - r * M : 0;
-                const int cb = s_list[r0 + r];
+                const int cb = seg0_cb + b0 + s_list[r0 + r];
                 u32x4 c = {0u, 0u, 0u, 0u}, sv = c;
                 if (live) {
                     c = *reinterpret_cast<const u32x4*>(lds_c + rr * A_ROW + 8 * l16);
@@ -507,7 +614,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
 }
 
 // LDS: chunk_units x (m + 1) input rows, then the C rows of the blocks reduced side by side
-inline size_t lds_bytes(int M, int cu, bool gated) { return ((size_t) cu * (M + 1) + (gated || M == 1 ? 2 * M : M)) * A_ROW * 2; }
+inline size_t lds_bytes(int M, int cu, bool gated)
+{
+    const int c_rows = (M == 1 ? 2 : 1) * (gated ? 2 * M : M);    // side-by-side blocks (pairs) x rows
+    return ((size_t) cu * (M + 1) + c_rows) * A_ROW * 2;
+}
 
 template <int BITS, int CB, int MT, bool GATED>
 int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t stream)

@@ -107,3 +107,21 @@ def test_check_raises_on_errors():
     with pytest.raises(_lib.Exl3Error):
         _lib.check(_lib.EINVAL, "x")
     assert _lib.check(_lib.DECLINED, "x") == _lib.DECLINED
+
+
+def test_gemv_split_fast_division_matches_brute_force():
+    """The kernels' unit split (lo / owner with 32-bit multiply-high division) against 64-bit
+    arithmetic and brute force, on the launch shapes of config 1 and random splits."""
+    import random
+    L = _lib.lib()
+    cases = [(1600, 512, 256, 3, 2), (5440, 256, 256, 3, 2), (5440, 256, 0, 3, 2), (320, 160, 160, 3, 2),
+             (18496, 512, 256, 3, 2), (77600, 512, 256, 3, 2), (2 ** 21, 512, 256, 3, 2), (40, 2, 2, 1, 1),
+             (1, 1, 1, 1, 1), (7, 7, 3, 1, 64)]
+    rng = random.Random(7)
+    for _ in range(150):
+        G = rng.randint(1, 600)
+        cases.append((rng.randint(G, 150000), G, rng.randint(0, G), rng.randint(1, 8), rng.randint(1, 8)))
+    for c in cases:
+        assert L.exl3_gemv_split_check(*c) == 0, c
+    assert L.exl3_gemv_split_check(0, 1, 0, 1, 1) == -1
+    assert L.exl3_gemv_split_check(2 ** 22, 512, 256, 64, 64) == -1      # beyond the 32-bit domain
