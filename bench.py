@@ -176,8 +176,9 @@ def per_shape_gemv(torch, sets, x5120, x17408, reps=64):
 
 def gated_mlp(torch, sets, x5120, ms=(1, 8), reps=32):
     """The MLP input of config 1: gate/up + SiLU-and-mul fused into one GEMV launch
-    (linear_silu_mul) against the unfused pair (linear_groups, then the elementwise kernel);
-    mean duration per call from a graph of `reps` calls over the weight copies."""
+    (exl3_gemv_silu_mul) against the unfused pair (linear_groups, then the elementwise kernel,
+    linear_silu_mul's default route); mean duration per call from a graph of `reps` calls over
+    the weight copies."""
     from exl3rocm import kernels as E
     ops = torch.ops.exl3rocm
     n = INTER
@@ -189,8 +190,8 @@ def gated_mlp(torch, sets, x5120, ms=(1, 8), reps=32):
 
         def fused(ls):
             w = ls.w
-            ops.linear_silu_mul(x, [w["gate"][0], w["up"][0]], [w["gate"][1], w["up"][1]],
-                                [w["gate"][2], w["up"][2]], [ls.bits, ls.bits], ls.mcg, ls.mul1)
+            E.exl3_gemv_silu_mul(x, [w["gate"][0], w["up"][0]], act, [w["gate"][1], w["up"][1]],
+                                 [w["gate"][2], w["up"][2]], ls.bits, ls.mcg, ls.mul1)
 
         def unfused(ls):
             w = ls.w

@@ -145,7 +145,8 @@ constexpr int RESIDENT_WGS = NUM_CUS * WAVES_PER_SIMD;   // workgroups per CU x 
 
 struct GridPlan {
     int groups;
-    int G[EXL3_MAX_GROUPS], wg0[EXL3_MAX_GROUPS], max_seg[EXL3_MAX_GROUPS], cnt_off[EXL3_MAX_GROUPS];
+    int G[EXL3_MAX_GROUPS], o0[EXL3_MAX_GROUPS], nold[EXL3_MAX_GROUPS], y0[EXL3_MAX_GROUPS];
+    int max_seg[EXL3_MAX_GROUPS], cnt_off[EXL3_MAX_GROUPS], first;
     int64_t slot_off[EXL3_MAX_GROUPS];   // first partial slot (one slot = m * 128 floats)
     int total_wgs, counters;
     int64_t slots;
@@ -188,20 +189,34 @@ GridPlan plan_grid(int k, const int* widths, int groups)
         Gs[i] = (int) std::max<int64_t>(1, std::min<int64_t>(Ui, (Gt * Ui + Utot / 2) / Utot));
         gsum += Gs[i];
     }
-    // workgroups [0, NUM_CUS) of the grid are the first on their CU; with at most one per CU all
-    // are, and the split is uniform
+    // grid slots [0, NUM_CUS) are the first workgroups on their CU (with at most one per CU all
+    // are, and the split is uniform); each group gets a share of them in proportion to its size
     const int first = gsum > NUM_CUS ? NUM_CUS : gsum;
-    int wg = 0, cnt = 0;
+    p.first = first;
+    int given = 0;
+    for (int i = 0; i < groups; ++i) {
+        p.nold[i] = (int) ((int64_t) first * Gs[i] / gsum);
+        given += p.nold[i];
+    }
+    for (int i = 0; i < groups && given < first; ++i)
+        if (p.nold[i] < Gs[i]) {
+            ++p.nold[i];
+            ++given;
+        }
+    int cnt = 0, o = 0, y = first;
     int64_t slots = 0;
     for (int i = 0; i < groups; ++i) {
         const int Ui = (widths[i] / 128) * UPB;
         p.G[i] = Gs[i];
-        p.wg0[i] = wg;
+        p.o0[i] = o;
+        p.y0[i] = y;
+        o += p.nold[i];
+        y += Gs[i] - p.nold[i];
         // weighted only where every workgroup still gets a unit (U * min(wa, wb) >= max(wa, wb) * G;
         // the completion count assumes each workgroup between a block's first and last owner
         // contributes to it)
         const bool weighted = (int64_t) Ui * std::min(p.wa, p.wb) >= (int64_t) std::max(p.wa, p.wb) * Gs[i];
-        p.h[i] = weighted ? std::min(std::max(first - wg, 0), Gs[i]) : Gs[i];
+        p.h[i] = weighted ? p.nold[i] : Gs[i];
         const Split sp = Split::make(Ui, Gs[i], p.h[i], p.wa, p.wb);
         p.split[i] = sp;
         const int per = sp.max_units();
@@ -209,11 +224,10 @@ GridPlan plan_grid(int k, const int* widths, int groups)
         p.cnt_off[i] = cnt;
         p.slot_off[i] = slots;
         p.max_per = std::max(p.max_per, per);
-        wg += p.G[i];
         cnt += widths[i] / 128;
         slots += (int64_t) p.G[i] * p.max_seg[i];
     }
-    p.total_wgs = wg;
+    p.total_wgs = gsum;
     p.counters = cnt;
     p.slots = slots;
     return p;
@@ -282,7 +296,11 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
         a.g[i] = gs[i];
         a.g[i].n = widths[i];
         a.g[i].G = p.G[i];
-        a.g[i].wg0 = p.wg0[i];
+        a.g[i].o0 = p.o0[i];
+        a.g[i].nold = p.nold[i];
+        a.g[i].y0 = p.y0[i];
+        a.slot_o[i] = p.o0[i];
+        a.slot_y[i] = p.y0[i];
         a.g[i].max_seg = p.max_seg[i];
         a.g[i].part_off = p.slot_off[i] * m * 128;
         a.g[i].cnt_off = p.cnt_off[i];
@@ -290,6 +308,7 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
         a.g[i].d_sg = p.split[i].d_sg;
         a.g[i].d_u = p.split[i].d_u;
     }
+    a.first = p.first;
     a.wa = p.wa;
     a.wb = p.wb;
     a.d_wa = UDiv::of((uint32_t) p.wa);

@@ -9,6 +9,8 @@
 
 using namespace exl3;
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
 // f(integral_constant<int, I>) for I in the sequence: ring slots are indexed by constants in the
 // source, so the ring always lives in registers (a loop index here could leave it in scratch memory)
 template <class F, int... I>
@@ -60,7 +62,8 @@ struct GemvGroup {
     uint16_t* y;               // output columns of this group (row stride ldy)
     int n;                     // width (columns)
     int G;                     // workgroups of this group
-    int wg0;                   // its first workgroup in the flattened grid
+    int o0, nold, y0;          // its workgroups: grid slots [o0, o0 + nold) among the first
+                               // `first` (dispatched first on their CU), then [y0, y0 + G - nold)
     int max_seg;               // partial slots per workgroup
     int64_t part_off;          // first partial (floats) of this group
     int cnt_off;               // first completion counter of this group
@@ -76,6 +79,8 @@ struct GemvArgs {
     const int64_t* tab_suh;     // replace g[i].trellis / suh / svh
     const int64_t* tab_svh;
     int groups, M, k, UPB;
+    int first;                 // grid slots dispatched first on their CU (one per CU)
+    i32x4 slot_o, slot_y;      // g[i].o0 and g[i].y0 as vectors, read whole by every workgroup
     int wa, wb;                // unit-split weights of first-dispatched / second workgroups on a CU
     UDiv d_wa, d_wb;
     int chunk_units;           // units whose rotated input fits the LDS at once
@@ -165,9 +170,10 @@ struct Split {
 
 // Two workgroups (8 waves) per CU are resident at once: up to 256 registers per lane, enough for
 // a ring deep enough that one wave alone keeps its SIMD busy.
-// GATED: groups 0 (gate) and 1 (up) of equal width; the workgroup completing a block of both
-// writes fp16(fp16(silu(gate)) * up) to g[0].y instead of the two outputs.
-template <int BITS, int CB, int MT, bool GATED>
+// MT: 16-row MFMA tiles of the input rows (0: exactly one row, a compile-time M).  GATED: groups
+// 0 (gate) and 1 (up) of equal width; the workgroup completing a block of both writes
+// fp16(fp16(silu(gate)) * up) to g[0].y instead of the two outputs.
+template <int BITS, int CB, int MT_, bool GATED>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_SIMD, WAVES_PER_SIMD))) gemv_kernel(GemvArgs a)
 {
     extern __shared__ __align__(16) uint16_t smem[];
@@ -178,15 +184,26 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // segment holding the block (gated: for gate, then up)
     __shared__ int s_own[GATED ? 6 : 3][256];
     // the group of this workgroup: a flattened grid, each group its own range of workgroups
+    // Every group owns slots among the first-dispatched workgroups (older waves, favoured by the
+    // SIMD arbiter) and among the second ones, in proportion to its size, so the weighted unit
+    // split balances each group's two kinds of workgroups.
+    // (The thresholds come as two vectors selected element-wise: a select between two scalar
+    // argument loads would become one load from a selected address, a dependent round trip at
+    // the start of every workgroup.)
+    const int b = blockIdx.x;
+    const bool older = b < a.first;
+    const i32x4 so = a.slot_o, sy = a.slot_y;
+    const int t1 = older ? so[1] : sy[1], t2 = older ? so[2] : sy[2], t3 = older ? so[3] : sy[3];
     int grp = 0;
-    if (a.groups > 1 && (int) blockIdx.x >= a.g[1].wg0) grp = 1;
-    if (a.groups > 2 && (int) blockIdx.x >= a.g[2].wg0) grp = 2;
-    if (a.groups > 3 && (int) blockIdx.x >= a.g[3].wg0) grp = 3;
+    if (a.groups > 1 && b >= t1) grp = 1;
+    if (a.groups > 2 && b >= t2) grp = 2;
+    if (a.groups > 3 && b >= t3) grp = 3;
     // constant indices only: a runtime index into the kernel-argument struct would copy it to
     // scratch memory, and every later read of it would be a vector-memory load
     const GemvGroup gg = grp == 0 ? a.g[0] : grp == 1 ? a.g[1] : grp == 2 ? a.g[2] : a.g[3];
-    const int w = blockIdx.x - gg.wg0;
-    const int G = gg.G, UPB = a.UPB, M = a.M;
+    const int w = older ? b - gg.o0 : gg.nold + (b - gg.y0);
+    constexpr int MT = MT_ == 0 ? 1 : MT_;
+    const int G = gg.G, UPB = a.UPB, M = MT_ == 0 ? 1 : a.M;
     const int NB = gg.n / 128, NT = gg.n / 16, U = NB * UPB;
     const Split sp{U, G, gg.h, a.wa, a.wb, gg.d_sg, gg.d_u, a.d_wa, a.d_wb};
     const uint32_t* trel = gg.trellis;
@@ -620,17 +637,18 @@ inline size_t lds_bytes(int M, int cu, bool gated)
     return ((size_t) cu * (M + 1) + c_rows) * A_ROW * 2;
 }
 
-template <int BITS, int CB, int MT, bool GATED>
+template <int BITS, int CB, int MT_, bool GATED>
 int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t stream)
 {
-    hipLaunchKernelGGL((gemv_kernel<BITS, CB, MT, GATED>), dim3(wgs), dim3(256), lds_bytes(a.M, a.chunk_units, GATED), stream, a);
+    hipLaunchKernelGGL((gemv_kernel<BITS, CB, MT_, GATED>), dim3(wgs), dim3(256), lds_bytes(a.M, a.chunk_units, GATED), stream, a);
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 
 template <int BITS, int CB, bool GATED>
 int launch_gemv_m(const GemvArgs& a, int wgs, hipStream_t s)
 {
-    return a.M <= 16 ? launch_gemv_t<BITS, CB, 1, GATED>(a, wgs, s) : launch_gemv_t<BITS, CB, 2, GATED>(a, wgs, s);
+    return a.M == 1 ? launch_gemv_t<BITS, CB, 0, GATED>(a, wgs, s)
+         : a.M <= 16 ? launch_gemv_t<BITS, CB, 1, GATED>(a, wgs, s) : launch_gemv_t<BITS, CB, 2, GATED>(a, wgs, s);
 }
 
 template <int BITS, bool GATED>

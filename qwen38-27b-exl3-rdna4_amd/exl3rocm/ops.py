@@ -27,6 +27,9 @@ MR_MAX = min(int(os.environ.get("EXL3_MR_MAX", str(_lib.GEMV_MAX_ROWS))), _lib.G
 # widest non-lm_head layer (17408): the shared reconstruction buffer of the `recon` prefill route
 RECON_SLICE_N = int(os.environ.get("EXL3_RECON_SLICE_N", "17408"))
 PREFILL_ROUTE = os.environ.get("EXL3_PREFILL", "fused")
+# linear_silu_mul at M <= MR_MAX: "unfused" (grouped GEMV + elementwise kernel) or "fused" (one
+# gated GEMV launch)
+GATED_ROUTE = os.environ.get("EXL3_GATED", "unfused")
 
 _wbuf: dict = {}
 
@@ -187,9 +190,10 @@ def exl3_linear_silu_mul(x: torch.Tensor, trellis: list[torch.Tensor], suh: list
     computes them.  No counterpart in the reference plugin, whose MLP runs linear_groups and then
     a separate SiluAndMul (the fusion is proposed in reference docs/EFFICIENCY_INVESTIGATION.md:36-66).
 
-    M <= EXL3_MR_MAX with equal K and width: one GEMV launch, the activation applied by the
-    workgroup that completes a 128-column block of both groups; otherwise linear_groups and an
-    elementwise SiLU-and-mul kernel."""
+    Routes: linear_groups, then an elementwise SiLU-and-mul kernel (the default: measured faster
+    on MI355X); or, with EXL3_GATED=fused and M <= EXL3_MR_MAX, equal K and width, one GEMV launch
+    whose workgroup completing a 128-column block of both groups applies the activation.  Both
+    routes give bitwise the same result."""
     if not (len(trellis) == 2 and len(suh) == 2 and len(svh) == 2 and len(K) == 2):
         raise RuntimeError("exl3rocm: linear_silu_mul takes exactly two groups (gate, up)")
     n = svh[0].shape[0]
@@ -200,7 +204,7 @@ def exl3_linear_silu_mul(x: torch.Tensor, trellis: list[torch.Tensor], suh: list
     act = torch.empty((M, n), dtype=torch.float16, device=x.device)
     if M == 0:
         return act.view(*x.shape[:-1], n)
-    if M <= MR_MAX and K[0] == K[1]:
+    if GATED_ROUTE == "fused" and M <= MR_MAX and K[0] == K[1]:
         E.exl3_gemv_silu_mul(x2, list(trellis), act, list(suh), list(svh), K[0], mcg, mul1)
     else:
         gu = exl3_linear_groups(x2, trellis, suh, svh, K, mcg, mul1)

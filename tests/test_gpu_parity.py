@@ -455,7 +455,10 @@ def test_gemv_silu_mul_matches_unfused(m, k, n, bits):
     torch's fp16 silu * up), bitwise, and every row == its m == 1 call."""
     x, mats, T, SU, SV = gate_up(k, n, bits, m)
     X = to_dev(x)[0]
-    act = torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True)
+    act = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    E.exl3_gemv_silu_mul(X, T, act, SU, SV, bits, False, True)            # the fused GEMV itself
+    assert torch.equal(act.view(torch.int16),
+                       torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True).view(torch.int16))
     gu = torch.ops.exl3rocm.linear_groups(X, T, SU, SV, [bits, bits], False, True)
     ours = torch.empty_like(act)
     E.silu_mul(gu[:, :n], gu[:, n:], ours)
@@ -466,9 +469,11 @@ def test_gemv_silu_mul_matches_unfused(m, k, n, bits):
     ulp = (ref.abs() * 2.0 ** -10).clamp_min(2.0 ** -24)
     assert (same | ((a - ref).abs() <= ulp)).all(), "vs torch silu * up: within one fp16 ulp"
     assert (~same).float().mean().item() <= 1e-3, "vs torch silu * up: last-place flips are rare"
-    a1 = torch.ops.exl3rocm.linear_silu_mul(X[:1], T, SU, SV, [bits, bits], False, True)
+    a1 = torch.empty(1, n, dtype=torch.float16, device=DEV)
+    E.exl3_gemv_silu_mul(X[:1], T, a1, SU, SV, bits, False, True)
     assert torch.equal(act[:1].view(torch.int16), a1.view(torch.int16))
-    again = torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True)
+    again = torch.empty_like(act)
+    E.exl3_gemv_silu_mul(X, T, again, SU, SV, bits, False, True)
     assert torch.equal(act.view(torch.int16), again.view(torch.int16))       # counters reset
 
 
@@ -477,7 +482,8 @@ def test_gemv_silu_mul_vs_oracle():
     float64 (one rounding each)."""
     m, k, n, bits = 3, 1024, 1536, 4
     x, mats, T, SU, SV = gate_up(k, n, bits, m, tag="gated-oracle")
-    act = torch.ops.exl3rocm.linear_silu_mul(to_dev(x)[0], T, SU, SV, [bits, bits], False, True)
+    act = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    E.exl3_gemv_silu_mul(to_dev(x)[0], T, act, SU, SV, bits, False, True)
     g, u = (cpu.linear(x, tr, bits, su, sv, 2) for tr, su, sv in mats)
     with np.errstate(over="ignore"):                  # exp(-g) = inf for very negative g: silu -> -0
         ref = O.to_f16(O.to_f16(g / (1.0 + np.exp(-g))) * u)
@@ -524,21 +530,25 @@ def test_gemv_silu_mul_graph_replays():
     m, k, n, bits = 1, 1024, 2048, 4
     x, mats, T, SU, SV = gate_up(k, n, bits, m, tag="gated-graph")
     X = to_dev(x)[0]
-    eager = torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True)
+    eager = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    E.exl3_gemv_silu_mul(X, T, eager, SU, SV, bits, False, True)
+    y = torch.empty_like(eager)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
         ops.reserve_workspace(DEV, k, n, bits, groups=2)
-        torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True)
+        E.exl3_gemv_silu_mul(X, T, y, SU, SV, bits, False, True)
     torch.cuda.current_stream().wait_stream(s)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
-        y = torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True)
+        E.exl3_gemv_silu_mul(X, T, y, SU, SV, bits, False, True)
     for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(y.view(torch.int16), eager.view(torch.int16))
-        torch.ops.exl3rocm.linear_silu_mul(X, T, SU, SV, [bits, bits], False, True)
+        E.exl3_gemv_silu_mul(X, T, eager, SU, SV, bits, False, True)
         torch.cuda.synchronize()
 
 
