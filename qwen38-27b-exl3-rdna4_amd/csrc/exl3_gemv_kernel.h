@@ -262,9 +262,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // workgroups on the same SIMDs run VALU-heavy decode loops: give them issue priority.
     __builtin_amdgcn_s_setprio(2);
 
-    // ---- first input chunk: its x / suh loads go out before the trellis ring ----------------
+    // ---- first input chunk: the x / suh loads of its first two 16-lane job passes go out before
+    // the trellis ring (a pass requested after the ring waits behind every workgroup's ring)
     const int nfirst = min(a.chunk_units, uhi - ulo) * M;
-    u32x4 px = {0u, 0u, 0u, 0u}, ps = px;
+    u32x4 px = {0u, 0u, 0u, 0u}, ps = px, px2 = px, ps2 = px;
     {
         const int i = threadIdx.x >> 4;
         if (i < nfirst) {
@@ -272,6 +273,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             job_src(ulo, i, m, col);
             px = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
             ps = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+        }
+        if (i + 16 < nfirst) {
+            int m, col;
+            job_src(ulo, i + 16, m, col);
+            px2 = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
+            ps2 = *reinterpret_cast<gc_u32x4*>(gsuh + col);
         }
     }
     // ---- the trellis ring: RING steps in flight per wave ----------------------------------------
@@ -296,8 +303,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
         load_qblock_buf<BITS>(trsrc, off_main, off_prev, lp + (i & 1) * STEP_D, Wr[i]);
         if (i & 1) advance_load();
     });
-    // rotated input of units [c0, c1) -> LDS; the first 16-lane job of each lane uses (x0, s0)
-    auto rotate_chunk = [&](int c0, int c1, u32x4 x0, u32x4 s0, bool have_first) __attribute__((always_inline)) {
+    // rotated input of units [c0, c1) -> LDS; with have_first the lane's first two 16-lane jobs use
+    // (x0, s0) and (x1, s1)
+    auto rotate_chunk = [&](int c0, int c1, u32x4 x0, u32x4 s0, u32x4 x1, u32x4 s1, bool have_first)
+        __attribute__((always_inline)) {
         const int njobs = (c1 - c0) * M;
         const int i = threadIdx.x >> 4;
         if (i - (threadIdx.x & 63) / 16 < njobs) {            // waves with a job (whole 16-lane groups)
@@ -318,8 +327,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 int m = 0, col = 0;
                 if (i2 < njobs) {
                     job_src(c0, i2, m, col);
-                    xv = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
-                    sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+                    if (have_first && i2 == i + 16) {
+                        xv = x1;
+                        sv = s1;
+                    } else {
+                        xv = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
+                        sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+                    }
                 }
                 const u32x4 r2 = had128_x8(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
                 if (i2 < njobs)
@@ -328,7 +342,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
         }
     };
     int c0 = ulo, c1 = min(ulo + a.chunk_units, uhi);
-    rotate_chunk(c0, c1, px, ps, true);
+    rotate_chunk(c0, c1, px, ps, px2, ps2, true);
     // zero rows: never overwritten by later chunks
     for (int t = threadIdx.x; t < a.chunk_units * (A_ROW / 8); t += 256)
         *reinterpret_cast<u32x4*>(lds_a + ((t / (A_ROW / 8)) * UROWS + M) * A_ROW + 8 * (t % (A_ROW / 8))) =
@@ -412,7 +426,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             c0 = c1;
             c1 = min(c0 + a.chunk_units, uhi);
             __syncthreads();
-            rotate_chunk(c0, c1, px, ps, false);
+            rotate_chunk(c0, c1, px, ps, px2, ps2, false);
             __syncthreads();
         }
     };
