@@ -94,6 +94,10 @@ int exl3_gemv(const void* x, int64_t ldx, const void* trellis, void* y, int64_t 
               void* stream);
 
 /* 1 <= m <= 32 EXL3 linear, output rows with stride ldy.
+ * A_had: optional fp16 scratch of m * k elements (groups * m * k for the grouped forms).  When
+ * given and m >= 12 (EXL3_GEMV_PREROT_M), the input is rotated once per group into it,
+ * A_had = fp16(Had128(fp16(x * suh))) as in the reference, and the GEMV reads those rows; otherwise
+ * every workgroup rotates its own k-range in LDS.  Either way the output is the same, bitwise.
  * Replaces `exl3_gemv_mr(A, B, C, suh, A_had, svh, K, mcg, mul1)` (reference ops.py:85;
  * 0002-gemv-multirow.patch:409-422). */
 int exl3_gemv_mr(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh, void* A_had,
@@ -115,8 +119,9 @@ int exl3_gemv_mr_grouped(const void* x, int64_t ldx, const void* const* trellis,
  * (reference ops.py:157-169).  Callers: exl3rocm's linear_groups for mixed-width runs.  The
  * groups share one stream-K grid, so a module pays one launch, prologue and completion. */
 int exl3_gemv_mr_grouped_widths(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
-                                const void* const* suh, const void* const* svh, const int* widths, int groups, int m,
-                                int k, int K, int mcg, int mul1, void* workspace, size_t ws_bytes, void* stream);
+                                const void* const* suh, void* A_had, const void* const* svh, const int* widths,
+                                int groups, int m, int k, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
+                                void* stream);
 
 /* Workspace bytes exl3_gemv_mr_grouped_widths needs (0 for an ineligible shape).  No reference
  * counterpart, as exl3_gemv_workspace_size. */
@@ -133,15 +138,16 @@ int exl3_gemv_split_check(int U, int G, int h, int wa, int wb);
  * K and width n, share x and one stream-K launch; y[m, n] (rows ldy apart, ldy >= n) receives
  * fp16(fp16(silu(gate)) * up), where gate and up are exactly what exl3_gemv_mr_grouped writes
  * (fp16 C, output Hadamard, svh) and silu is g / (1 + exp(-g)) in fp32 (the SiluAndMul
- * roundings).  trellis / suh / svh: host arrays of 2 device pointers.  Workspace as
+ * roundings).  trellis / suh / svh: host arrays of 2 device pointers; A_had as exl3_gemv_mr
+ * (2 * m * k).  Workspace as
  * exl3_gemv_workspace_size(m, k, n, K, 2).  No counterpart in the reference: its gated MLP runs
  * the gate/up linear_groups, then a separate SiLU-and-mul (reference
  * docs/EFFICIENCY_INVESTIGATION.md:36-66 proposes this fusion).  Callers: model code that owns
  * the gate/up module and its activation (exl3rocm's linear_silu_mul op).  Removes the [m, 2n]
  * intermediate and the activation launch. */
 int exl3_gemv_silu_mul(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
-                       const void* const* suh, const void* const* svh, int m, int k, int n, int K, int mcg, int mul1,
-                       void* workspace, size_t ws_bytes, void* stream);
+                       const void* const* suh, void* A_had, const void* const* svh, int m, int k, int n, int K, int mcg,
+                       int mul1, void* workspace, size_t ws_bytes, void* stream);
 
 /* Elementwise SiLU-and-mul: out[r][c] = fp16(fp16(silu(gate[r][c])) * up[r][c]) for r < rows,
  * c < n (n % 8 == 0; gate and up rows ld_in apart, out rows ld_out apart; 16-byte aligned).

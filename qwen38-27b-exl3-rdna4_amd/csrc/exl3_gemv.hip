@@ -262,9 +262,20 @@ bool shape_ok(int m, int k, int n, int K)
 
 // gs[i].y: group i's first output column (rows ldy apart); with pointer tables only gs[i].y is
 // read from gs, the table entries are the caller's contract
+// rows from which the input is rotated once per group by a separate pass into the caller's A_had
+// scratch, instead of by every workgroup for its own k-range (EXL3_GEMV_PREROT_M overrides): at
+// M = 32 the per-workgroup rotation is more VALU work than the decode; at M = 8 the extra pass
+// costs more than it saves (measured on config-1 gate and down)
+int prerot_rows()
+{
+    static const int v = env_int("EXL3_GEMV_PREROT_M", 12);
+    return v;
+}
+
+// xr: the caller's scratch of groups * m * k fp16 for pre-rotated input (may be null)
 int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widths, int groups,
                 const int64_t* const* tabs, int64_t ldy, int m, int k, int K, int mcg, int mul1, void* ws,
-                size_t ws_bytes, void* stream, bool gated = false)
+                size_t ws_bytes, void* stream, bool gated = false, void* xr = nullptr)
 {
     if (gated && (groups != 2 || tabs || widths[0] != widths[1] || ldy < widths[0])) return EXL3_EINVAL;
     if (!x || groups < 1 || groups > EXL3_MAX_GROUPS || ldx < k) return EXL3_EINVAL;
@@ -292,6 +303,15 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
     GemvArgs a{};
     a.x = (const uint16_t*) x;
     a.ldx = ldx;
+    if (xr && !tabs && m > 1 && m >= prerot_rows()) {
+        if (((uintptr_t) xr) & 15) return EXL3_EINVAL;
+        for (int i = 0; i < groups; ++i) {
+            const int rc = exl3_had_r_128(x, ldx, (uint16_t*) xr + (int64_t) i * m * k, k, m, k, gs[i].suh, nullptr,
+                                          1.0f, stream);
+            if (rc != EXL3_OK) return rc;
+        }
+        a.xr = (const uint16_t*) xr;
+    }
     for (int i = 0; i < groups; ++i) {
         a.g[i] = gs[i];
         a.g[i].n = widths[i];
@@ -411,17 +431,15 @@ int exl3_gemv_mr(const void* x, int64_t ldx, const void* trellis, void* y, int64
                  const void* svh, int m, int k, int n, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
                  void* stream)
 {
-    (void) A_had;
     if (!trellis || !y || !suh || !svh) return EXL3_EINVAL;
     GemvGroup g{(const uint32_t*) trellis, (const uint16_t*) suh, (const uint16_t*) svh, (uint16_t*) y};
-    return gemv_common(x, ldx, &g, &n, 1, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream);
+    return gemv_common(x, ldx, &g, &n, 1, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream, false, A_had);
 }
 
 int exl3_gemv_mr_grouped(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
                          const void* const* suh, void* A_had, const void* const* svh, int groups, int m, int k, int n,
                          int K, int mcg, int mul1, int bszm_for_warps, void* workspace, size_t ws_bytes, void* stream)
 {
-    (void) A_had;
     (void) bszm_for_warps;
     if (!trellis || !suh || !svh || !y || groups < 1 || groups > EXL3_MAX_GROUPS) return EXL3_EINVAL;
     GemvGroup gs[EXL3_MAX_GROUPS];
@@ -431,12 +449,14 @@ int exl3_gemv_mr_grouped(const void* x, int64_t ldx, const void* const* trellis,
                  (uint16_t*) y + (int64_t) i * n};
         widths[i] = n;
     }
-    return gemv_common(x, ldx, gs, widths, groups, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream);
+    return gemv_common(x, ldx, gs, widths, groups, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream,
+                       false, A_had);
 }
 
 int exl3_gemv_mr_grouped_widths(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
-                                const void* const* suh, const void* const* svh, const int* widths, int groups, int m,
-                                int k, int K, int mcg, int mul1, void* workspace, size_t ws_bytes, void* stream)
+                                const void* const* suh, void* A_had, const void* const* svh, const int* widths,
+                                int groups, int m, int k, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
+                                void* stream)
 {
     if (!trellis || !suh || !svh || !y || !widths || groups < 1 || groups > EXL3_MAX_GROUPS) return EXL3_EINVAL;
     GemvGroup gs[EXL3_MAX_GROUPS];
@@ -446,19 +466,21 @@ int exl3_gemv_mr_grouped_widths(const void* x, int64_t ldx, const void* const* t
         n0 += widths[i];
     }
     if (ldy < n0) return EXL3_EINVAL;
-    return gemv_common(x, ldx, gs, widths, groups, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream);
+    return gemv_common(x, ldx, gs, widths, groups, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream,
+                       false, A_had);
 }
 
 int exl3_gemv_silu_mul(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
-                       const void* const* suh, const void* const* svh, int m, int k, int n, int K, int mcg, int mul1,
-                       void* workspace, size_t ws_bytes, void* stream)
+                       const void* const* suh, void* A_had, const void* const* svh, int m, int k, int n, int K, int mcg,
+                       int mul1, void* workspace, size_t ws_bytes, void* stream)
 {
     if (!trellis || !suh || !svh || !y) return EXL3_EINVAL;
     GemvGroup gs[2];
     const int widths[2] = {n, n};
     for (int i = 0; i < 2; ++i)
         gs[i] = {(const uint32_t*) trellis[i], (const uint16_t*) suh[i], (const uint16_t*) svh[i], (uint16_t*) y};
-    return gemv_common(x, ldx, gs, widths, 2, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream, true);
+    return gemv_common(x, ldx, gs, widths, 2, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream, true,
+                       A_had);
 }
 
 int exl3_mgemm(const void* x, const int64_t* ptrs_trellis, void* y, const int64_t* ptrs_suh, void* xh,

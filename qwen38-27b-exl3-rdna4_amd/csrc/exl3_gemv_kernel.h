@@ -73,6 +73,9 @@ struct GemvGroup {
 
 struct GemvArgs {
     const uint16_t* x;         // [M][ldx] fp16
+    const uint16_t* xr;        // or, when set, every group's rotated input fp16(Had128(fp16(x * suh))):
+                               // group i's rows at xr + i * M * k, k apart (computed by one pass per
+                               // group before the launch)
     int64_t ldx;
     GemvGroup g[EXL3_MAX_GROUPS];
     const int64_t* tab_trellis; // optional device pointer tables (grouped M=1 `mgemm` form): they
@@ -226,7 +229,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
         const_cast<uint32_t*>(trel), 0, (int) (uint32_t) trel_bytes, RAW_BUFFER_FLAGS);
     gc_u16* const gsuh = as_global(suh);
     gc_u16* const gsvh = as_global(svh);
-    gc_u16* const gx = as_global(a.x);
+    // the input rows: x (rotated here, per workgroup) or the group's pre-rotated rows
+    const bool pre = MT_ != 0 && a.xr != nullptr;
+    gc_u16* const gx = as_global(pre ? a.xr + (int64_t) grp * M * a.k : a.x);
+    const int64_t ldx = pre ? (int64_t) a.k : a.ldx;
     g_u16* const gy = as_global(y);
     // LDS: the rotated input of a chunk of units, M rows per unit followed by one zero row (the A
     // operand of MFMA rows >= M), then the fp16 C of one block for the output transform
@@ -271,14 +277,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
         if (i < nfirst) {
             int m, col;
             job_src(ulo, i, m, col);
-            px = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
-            ps = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+            px = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * ldx + col);
+            if (!pre) ps = *reinterpret_cast<gc_u32x4*>(gsuh + col);
         }
         if (i + 16 < nfirst) {
             int m, col;
             job_src(ulo, i + 16, m, col);
-            px2 = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
-            ps2 = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+            px2 = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * ldx + col);
+            if (!pre) ps2 = *reinterpret_cast<gc_u32x4*>(gsuh + col);
         }
     }
     // ---- the trellis ring: RING steps in flight per wave ----------------------------------------
@@ -313,10 +319,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             if (!have_first && i < njobs) {
                 int m, col;
                 job_src(c0, i, m, col);
-                x0 = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
-                s0 = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+                x0 = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * ldx + col);
+                if (!pre) s0 = *reinterpret_cast<gc_u32x4*>(gsuh + col);
             }
-            const u32x4 r = had128_x8(x0, s0, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
+            const u32x4 r = pre ? x0 : had128_x8(x0, s0, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
             if (i < njobs) {
                 int m, col;
                 job_src(c0, i, m, col);
@@ -331,11 +337,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                         xv = x1;
                         sv = s1;
                     } else {
-                        xv = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * a.ldx + col);
-                        sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
+                        xv = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * ldx + col);
+                        if (!pre) sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
                     }
                 }
-                const u32x4 r2 = had128_x8(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
+                const u32x4 r2 = pre ? xv : had128_x8(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
                 if (i2 < njobs)
                     *reinterpret_cast<u32x4*>(lds_a + ((i2 / M) * UROWS + m) * A_ROW + 8 * (threadIdx.x & 15)) = r2;
             }

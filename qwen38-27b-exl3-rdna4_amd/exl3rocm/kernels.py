@@ -166,14 +166,26 @@ def exl3_gemv(A, B, C, suh, A_had, svh, mcg: bool, mul1: bool) -> int:
                                      _stream(A)), "exl3_gemv")
 
 
+def _rot_scratch(A_had, device, groups: int, m: int, k: int):
+    """The A_had scratch for the multi-row GEMV (groups * m * k fp16): the caller's when it is large
+    enough, else a fresh one; none at m == 1 (the kernel rotates in LDS)."""
+    if m <= 1:
+        return None
+    if A_had is not None and A_had.dtype == torch.float16 and A_had.is_contiguous() and A_had.numel() >= groups * m * k:
+        return A_had
+    return torch.empty(groups * m * k, dtype=torch.float16, device=device)
+
+
 def exl3_gemv_mr(A, B, C, suh, A_had, svh, K: int, mcg: bool, mul1: bool) -> int:
     _cuda(A, B, C, suh, svh)
     x2, m, k = _rows(A)
     n = svh.shape[0]
     _need(B.shape[-1] == 16 * K, "exl3_gemv_mr: trellis last dim must be 16*K")
     ws = workspace(A.device, gemv_workspace_bytes(m, k, n, K))
+    xr = _rot_scratch(A_had, A.device, 1, m, k)
     return L.check(L.lib().exl3_gemv_mr(x2.data_ptr(), x2.stride(0) if m > 1 else k, B.data_ptr(), C.data_ptr(),
-                                        _ldy(C, n), suh.data_ptr(), None, svh.data_ptr(), m, k, n, K,
+                                        _ldy(C, n), suh.data_ptr(), xr.data_ptr() if xr is not None else None,
+                                        svh.data_ptr(), m, k, n, K,
                                         *_cb_flags(mcg, mul1), ws.data_ptr(), ws.numel(), _stream(A)),
                    "exl3_gemv_mr")
 
@@ -188,17 +200,19 @@ def exl3_gemv_mr_grouped(A, B: Sequence[torch.Tensor], C, suh: Sequence[torch.Te
     _need(all(s.shape[0] == n for s in svh), "grouped: groups must share n")
     _need(C.shape[-1] >= g * n, "grouped: output narrower than groups * n")
     ws = workspace(A.device, gemv_workspace_bytes(m, k, n, K, g))
+    xr = _rot_scratch(A_had, A.device, g, m, k)
     pt, _a = L.ptr_array([b.data_ptr() for b in B])
     ps, _b = L.ptr_array([s.data_ptr() for s in suh])
     pv, _c = L.ptr_array([s.data_ptr() for s in svh])
     return L.check(L.lib().exl3_gemv_mr_grouped(x2.data_ptr(), x2.stride(0) if m > 1 else k, pt, C.data_ptr(),
-                                                _ldy(C, g * n), ps, None, pv, g, m, k, n, K, *_cb_flags(mcg, mul1),
+                                                _ldy(C, g * n), ps, xr.data_ptr() if xr is not None else None, pv,
+                                                g, m, k, n, K, *_cb_flags(mcg, mul1),
                                                 bszm_for_warps, ws.data_ptr(), ws.numel(), _stream(A)),
                    "exl3_gemv_mr_grouped")
 
 
 def exl3_gemv_mr_grouped_widths(A, B: Sequence[torch.Tensor], C, suh: Sequence[torch.Tensor],
-                                svh: Sequence[torch.Tensor], K: int, mcg: bool, mul1: bool) -> int:
+                                svh: Sequence[torch.Tensor], K: int, mcg: bool, mul1: bool, A_had=None) -> int:
     """Groups of any widths sharing x and K (q/k/v) in one launch; group i writes the columns after
     groups 0..i-1 of C.  No counterpart in the reference extension (it launches these one by one)."""
     _cuda(A, C, *B, *suh, *svh)
@@ -209,11 +223,13 @@ def exl3_gemv_mr_grouped_widths(A, B: Sequence[torch.Tensor], C, suh: Sequence[t
     _need(C.shape[-1] >= sum(widths), "grouped: output narrower than the groups")
     wa = (C_int * g)(*widths)
     ws = workspace(A.device, int(L.lib().exl3_gemv_workspace_size_widths(m, k, wa, g)))
+    xr = _rot_scratch(A_had, A.device, g, m, k)
     pt, _a = L.ptr_array([b.data_ptr() for b in B])
     ps, _b = L.ptr_array([s.data_ptr() for s in suh])
     pv, _c = L.ptr_array([s.data_ptr() for s in svh])
     return L.check(L.lib().exl3_gemv_mr_grouped_widths(x2.data_ptr(), x2.stride(0) if m > 1 else k, pt, C.data_ptr(),
-                                                       _ldy(C, sum(widths)), ps, pv, wa, g, m, k, K,
+                                                       _ldy(C, sum(widths)), ps,
+                                                       xr.data_ptr() if xr is not None else None, pv, wa, g, m, k, K,
                                                        *_cb_flags(mcg, mul1), ws.data_ptr(), ws.numel(), _stream(A)),
                    "exl3_gemv_mr_grouped_widths")
 
@@ -229,11 +245,13 @@ def exl3_gemv_silu_mul(A, B: Sequence[torch.Tensor], C, suh: Sequence[torch.Tens
           "silu_mul: gate and up of equal width")
     _need(C.shape[-1] >= n, "silu_mul: output narrower than n")
     ws = workspace(A.device, gemv_workspace_bytes(m, k, n, K, 2))
+    xr = _rot_scratch(None, A.device, 2, m, k)
     pt, _a = L.ptr_array([b.data_ptr() for b in B])
     ps, _b = L.ptr_array([s.data_ptr() for s in suh])
     pv, _c = L.ptr_array([s.data_ptr() for s in svh])
     return L.check(L.lib().exl3_gemv_silu_mul(x2.data_ptr(), x2.stride(0) if m > 1 else k, pt, C.data_ptr(),
-                                              _ldy(C, n), ps, pv, m, k, n, K, *_cb_flags(mcg, mul1), ws.data_ptr(),
+                                              _ldy(C, n), ps, xr.data_ptr() if xr is not None else None, pv, m, k, n,
+                                              K, *_cb_flags(mcg, mul1), ws.data_ptr(),
                                               ws.numel(), _stream(A)), "exl3_gemv_silu_mul")
 
 

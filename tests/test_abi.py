@@ -69,8 +69,8 @@ def test_widths_workspace_sizes():
     dummy = ctypes.c_void_p(0x1000)
     arr = (ctypes.c_void_p * 3)(0x1000, 0x1000, 0x1000)
     # output row narrower than the groups' total width
-    assert L.exl3_gemv_mr_grouped_widths(dummy, 5120, arr, dummy, 5120, arr, arr, qkv, 3, 2, 5120, 4, 0, 1, dummy,
-                                         1 << 30, None) == _lib.EINVAL
+    assert L.exl3_gemv_mr_grouped_widths(dummy, 5120, arr, dummy, 5120, arr, None, arr, qkv, 3, 2, 5120, 4, 0, 1,
+                                         dummy, 1 << 30, None) == _lib.EINVAL
 
 
 def test_mr_supported_predicate():

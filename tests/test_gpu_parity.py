@@ -146,6 +146,7 @@ GEMV_CASES = [
     (5120, 5120, 2, 2), (5120, 5120, 4, 2), (5120, 1024, 4, 2), (5120, 17408, 3, 2), (17408, 5120, 3, 2),
     (5120, 1024, 5, 2), (5120, 1024, 6, 2), (5120, 1024, 8, 2), (1024, 768, 7, 0), (1024, 512, 1, 1),
     (5120, 5120, 4, 0), (5120, 5120, 4, 1),
+    (256, 32896, 3, 2),                        # the reference's single-warp form: n / 16 > 2048
 ]
 
 
