@@ -127,6 +127,11 @@ int exl3_gemv_mr_grouped_widths(const void* x, int64_t ldx, const void* const* t
  * counterpart, as exl3_gemv_workspace_size. */
 size_t exl3_gemv_workspace_size_widths(int m, int k, const int* widths, int groups);
 
+/* Rows from which the multi-row GEMV entry points rotate the input once per group into A_had
+ * (EXL3_GEMV_PREROT_M, default 12); callers need not provide A_had below it.  No reference
+ * counterpart.  Callers: exl3rocm's kernel wrappers. */
+int exl3_gemv_prerot_rows(void);
+
 /* Self-check of the GEMV's stream-K unit split (host only, no GPU): the kernels' 32-bit
  * multiply-high division forms of lo(w) and owner(u) against 64-bit arithmetic and brute force for
  * U units over G workgroups (h of them weighted wa, the rest wb), plus the divider at its range

@@ -382,6 +382,8 @@ size_t exl3_gemv_workspace_size_widths(int m, int k, const int* widths, int grou
     return gemv_ws_bytes(m, k, widths, groups);
 }
 
+int exl3_gemv_prerot_rows(void) { return prerot_rows(); }
+
 int exl3_gemv_split_check(int U, int G, int h, int wa, int wb)
 {
     if (U < 1 || G < 1 || h < 0 || h > G || wa < 1 || wb < 1) return -1;

@@ -553,7 +553,41 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 return __hip_atomic_load(c == 0 ? p0 : p1 + (int64_t) (c - 1) * cstride, __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
             };
-            if constexpr (!GATED) {
+            if (!GATED && MT_ != 0 && M > 1) {
+                // one block per pass (rb == 1): every element shares the block's contributors, so a
+                // thread keeps 4 elements x 8 contributors of loads in flight (sums in contributor order)
+                const int bi = s_list[r0];
+                const int wf = s_own[0][bi], nc = s_own[1][bi];
+                const int64_t cs = (int64_t) gg.max_seg * M * 128;
+                const float* p0 = part_grp + ((int64_t) wf * gg.max_seg + s_own[2][bi]) * M * 128;
+                const float* p1 = part_grp + (int64_t) (wf + 1) * cs;
+                for (int e0 = threadIdx.x; e0 < total; e0 += 1024) {
+                    float sum[4] = {0.f, 0.f, 0.f, 0.f};
+                    for (int c0 = 0; c0 < nc; c0 += 8) {
+                        float v[4][8];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+#pragma unroll
+                            for (int cc = 0; cc < 8; ++cc) {
+                                const int c = c0 + cc, e = e0 + 256 * j;
+                                const float* src = (c == 0 ? p0 : p1 + (int64_t) (c - 1) * cs) + e;
+                                v[j][cc] = c < nc && e < total
+                                               ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                               : 0.f;
+                            }
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+#pragma unroll
+                            for (int cc = 0; cc < 8; ++cc)
+                                if (c0 + cc < nc) sum[j] += v[j][cc];
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int e = e0 + 256 * j;
+                        if (e < total) lds_c[(e >> 7) * A_ROW + (e & 127)] = f16_bits((f16) sum[j]);
+                    }
+                }
+            } else if constexpr (!GATED) {
                 for (int e = threadIdx.x; e < total; e += 256) {
                     const int r = e / (M * 128), el = e - r * (M * 128);
                     const int bi = s_list[r0 + r];

@@ -38,6 +38,7 @@ SIGNATURES = {
                                          _sz, _p]),
     "exl3_gemv_workspace_size_widths": (_sz, [_i, _i, _ip, _i]),
     "exl3_gemv_split_check": (_i, [_i, _i, _i, _i, _i]),
+    "exl3_gemv_prerot_rows": (_i, []),
     "exl3_gemv_silu_mul": (_i, [_p, _i64, _pp, _p, _i64, _pp, _p, _pp, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "exl3_silu_mul": (_i, [_p, _p, _i64, _p, _i64, _i, _i, _p]),
     "exl3_mgemm": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),

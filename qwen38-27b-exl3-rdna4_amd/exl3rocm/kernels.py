@@ -166,10 +166,17 @@ def exl3_gemv(A, B, C, suh, A_had, svh, mcg: bool, mul1: bool) -> int:
                                      _stream(A)), "exl3_gemv")
 
 
+_prerot = None
+
+
 def _rot_scratch(A_had, device, groups: int, m: int, k: int):
     """The A_had scratch for the multi-row GEMV (groups * m * k fp16): the caller's when it is large
-    enough, else a fresh one; none at m == 1 (the kernel rotates in LDS)."""
-    if m <= 1:
+    enough, else a fresh one; none below the library's pre-rotation row count (the kernel rotates
+    in LDS there)."""
+    global _prerot
+    if _prerot is None:
+        _prerot = int(L.lib().exl3_gemv_prerot_rows())
+    if m <= 1 or m < _prerot:
         return None
     if A_had is not None and A_had.dtype == torch.float16 and A_had.is_contiguous() and A_had.numel() >= groups * m * k:
         return A_had
