@@ -304,11 +304,15 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             }
         }
     };
-    static_for(std::make_integer_sequence<int, RING>{}, [&](auto I) __attribute__((always_inline)) {
+    // the first half of the ring goes out now, the second after the first input rotation: a wave
+    // stalls at issue once its CU's load queue is full, so the rotation's VALU work would otherwise
+    // wait for the whole ring to be issued
+    auto fill = [&](auto I) __attribute__((always_inline)) {
         constexpr int i = decltype(I)::value;
         load_qblock_buf<BITS>(trsrc, off_main, off_prev, lp + (i & 1) * STEP_D, Wr[i]);
         if (i & 1) advance_load();
-    });
+    };
+    static_for(std::make_integer_sequence<int, RING / 2>{}, fill);
     // rotated input of units [c0, c1) -> LDS; with have_first the lane's first two 16-lane jobs use
     // (x0, s0) and (x1, s1)
     auto rotate_chunk = [&](int c0, int c1, u32x4 x0, u32x4 s0, u32x4 x1, u32x4 s1, bool have_first)
@@ -349,6 +353,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     };
     int c0 = ulo, c1 = min(ulo + a.chunk_units, uhi);
     rotate_chunk(c0, c1, px, ps, px2, ps2, true);
+    static_for(std::make_integer_sequence<int, RING / 2>{}, [&](auto I) __attribute__((always_inline)) {
+        fill(std::integral_constant<int, RING / 2 + decltype(I)::value>{});
+    });
     // zero rows: never overwritten by later chunks
     for (int t = threadIdx.x; t < a.chunk_units * (A_ROW / 8); t += 256)
         *reinterpret_cast<u32x4*>(lds_a + ((t / (A_ROW / 8)) * UROWS + M) * A_ROW + 8 * (t % (A_ROW / 8))) =
