@@ -39,7 +39,7 @@ extern "C" {
 #define EXL3_ABI_VERSION 1
 #define EXL3_MAX_GROUPS 4       /* groups per grouped launch (reference EXL3_GEMV_MRG_MAX) */
 #define EXL3_GEMV_MAX_ROWS 32   /* rows handled by the fused GEMV */
-#define EXL3_GEMV_COUNTER_BYTES 65536  /* workspace head reserved for completion counters */
+#define EXL3_GEMV_COUNTER_BYTES 262144 /* workspace head reserved for completion counters (one per 128-byte line) */
 
 #define EXL3_OK 0
 #define EXL3_DECLINED 1

@@ -296,7 +296,7 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
         if ((uint64_t) k * widths[i] * K / 8 > 0xFFFFFFFFull) return EXL3_DECLINED;   // one raw buffer per trellis
     }
     const GridPlan p = plan_grid(k, widths, groups);
-    if ((size_t) p.counters * 4 > COUNTER_BYTES) return EXL3_DECLINED;
+    if ((size_t) p.counters * 4 * CNT_STRIDE > COUNTER_BYTES) return EXL3_DECLINED;
     for (int i = 0; i < groups; ++i)
         if (!p.split[i].fits32()) return EXL3_DECLINED;   // unreachable below the 4 GiB trellis limit
     if (!ws || ws_bytes < COUNTER_BYTES + (size_t) p.slots * m * 128 * 4) return EXL3_EWORKSPACE;

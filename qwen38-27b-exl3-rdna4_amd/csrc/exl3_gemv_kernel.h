@@ -93,6 +93,9 @@ struct GemvArgs {
 };
 
 constexpr int RED_BATCH = 16;                   // partial loads in flight per thread in the reduction
+// completion counters one per 128-byte line: every contributor of every block increments its block's
+// counter at about the same time, and atomics to one line serialize at its L2 channel
+constexpr int CNT_STRIDE = 32;
 constexpr int A_ROW = 136;                      // LDS row of one rotated 128-block (padded, halves)
 constexpr int LDS_BUDGET = 64 * 1024;           // per workgroup: 2 workgroups per CU
 constexpr int RING = 8;                         // 64-row k steps in flight per wave (even)
@@ -222,7 +225,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     }
     // a gated launch counts both groups' contributions to block cb in group 0's counter cb
     constexpr bool gated = GATED;
-    uint32_t* const counters = a.counters + (gated ? a.g[0].cnt_off : gg.cnt_off);
+    uint32_t* const counters = a.counters + (int64_t) (gated ? a.g[0].cnt_off : gg.cnt_off) * CNT_STRIDE;
     // the trellis as one raw buffer (layers of 4 GiB and more are declined on the host)
     const uint64_t trel_bytes = (uint64_t) a.k * gg.n * BITS / 8;
     const __amdgpu_buffer_rsrc_t trsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -481,7 +484,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
         if ((int) threadIdx.x < nb) {                         // one counter per thread, all in flight
             const int t = threadIdx.x;
             const int cb = seg0_cb + b0 + t;
-            const uint32_t prev = __hip_atomic_fetch_add(&counters[cb], 1u, __ATOMIC_RELAXED,
+            const uint32_t prev = __hip_atomic_fetch_add(&counters[cb * CNT_STRIDE], 1u, __ATOMIC_RELAXED,
                                                          __HIP_MEMORY_SCOPE_AGENT);
             // the block's contributors (integer divisions) while the counter round trip is in flight
             __builtin_amdgcn_sched_barrier(0);
@@ -645,7 +648,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 }
             }
             if ((int) threadIdx.x < rb)                        // ready for the next call (stream order)
-                __hip_atomic_store(&counters[seg0_cb + b0 + s_list[r0 + threadIdx.x]], 0u, __ATOMIC_RELAXED,
+                __hip_atomic_store(&counters[(seg0_cb + b0 + s_list[r0 + threadIdx.x]) * CNT_STRIDE], 0u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
             __syncthreads();
             if (gated) {
