@@ -304,27 +304,37 @@ def prefill_chunk(torch, layers=64, m=2048, bits=4, iters=2):
             "frac_mfma_fp16": round(tf / MFMA_FP16_PEAK_TFLOPS, 4), "flops_per_chunk": flops}
 
 
-def small_batch(torch, sets, ms=(1, 4, 8, 16, 32)):
-    """Configuration 3: gate/up and down at M in {1, 4, 8, 16, 32}, heavy-tail activations."""
+def small_batch(torch, sets, ms=(1, 4, 8, 16, 32), reps=32):
+    """Configuration 3: gate/up and down at M in {1, 4, 8, 16, 32}, heavy-tail activations; mean
+    duration per call from a graph of `reps` calls over the weight copies (HIP events on the replay
+    stream)."""
     from exl3rocm import synth
     res = {}
+    s = torch.cuda.Stream()
     for name in ("gate", "down"):
         k = INTER if name == "down" else HIDDEN
         row = {}
         for m in ms:
             x = torch.from_numpy(synth.activations(synth.key_of("cfg3", k, m), m, k, heavy_tail=True)).cuda()
             fn = (lambda ls, x=x: torch.ops.exl3rocm.linear(x, *ls.w[name], ls.bits, ls.mcg, ls.mul1))
-            for ls in sets:
-                fn(ls)
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            reps = 4 * len(sets)
-            e0.record()
-            for i in range(reps):
-                fn(sets[i % len(sets)])
-            e1.record()
-            torch.cuda.synchronize()
-            row[f"m{m}_us"] = round(e0.elapsed_time(e1) * 1e3 / reps, 2)
+            with torch.cuda.stream(s):
+                for ls in sets:
+                    fn(ls)
+            s.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                for r in range(reps):
+                    fn(sets[r % len(sets)])
+            with torch.cuda.stream(s):
+                g.replay()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(s)
+                for _ in range(3):
+                    g.replay()
+                e1.record(s)
+            s.synchronize()
+            row[f"m{m}_us"] = round(e0.elapsed_time(e1) * 1e3 / (3 * reps), 2)
+            del g
         res[name] = row
     return res
 

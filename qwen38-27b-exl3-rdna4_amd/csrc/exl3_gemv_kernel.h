@@ -563,7 +563,52 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 return __hip_atomic_load(c == 0 ? p0 : p1 + (int64_t) (c - 1) * cstride, __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
             };
-            if (!GATED && MT_ != 0 && M > 1) {
+            if (GATED && MT_ != 0 && M > 1) {
+                // a pair per pass: gate rows then up rows, each group's contributors shared by its
+                // elements; 4 elements x 8 contributors of loads in flight per thread
+                const int bi = s_list[r0];
+                const int half = M * 128;
+                const int64_t csa = (int64_t) a.g[0].max_seg * M * 128, csb = (int64_t) a.g[1].max_seg * M * 128;
+                const int nca = s_own[1][bi], ncb = s_own[4][bi];
+                const float* a0 = a.part + a.g[0].part_off + ((int64_t) s_own[0][bi] * a.g[0].max_seg + s_own[2][bi]) * M * 128;
+                const float* b0 = a.part + a.g[1].part_off + ((int64_t) s_own[3][bi] * a.g[1].max_seg + s_own[5][bi]) * M * 128;
+                const float* a1 = a.part + a.g[0].part_off + (int64_t) (s_own[0][bi] + 1) * csa;
+                const float* b1 = a.part + a.g[1].part_off + (int64_t) (s_own[3][bi] + 1) * csb;
+                const int ncmax = nca > ncb ? nca : ncb;
+                for (int e0 = threadIdx.x; e0 < total; e0 += 1024) {
+                    float sum[4] = {0.f, 0.f, 0.f, 0.f};
+                    for (int c0 = 0; c0 < ncmax; c0 += 8) {
+                        float v[4][8];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const int e = e0 + 256 * j;
+                            const bool up = e >= half;
+                            const int el = up ? e - half : e;
+                            const int nc = e < total ? (up ? ncb : nca) : 0;
+#pragma unroll
+                            for (int cc = 0; cc < 8; ++cc) {
+                                const int c = c0 + cc;
+                                const float* src = (c == 0 ? (up ? b0 : a0)
+                                                           : (up ? b1 + (int64_t) (c - 1) * csb : a1 + (int64_t) (c - 1) * csa)) + el;
+                                v[j][cc] = c < nc ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+                            }
+                        }
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const int e = e0 + 256 * j;
+                            const int nc = e < total ? (e >= half ? ncb : nca) : 0;
+#pragma unroll
+                            for (int cc = 0; cc < 8; ++cc)
+                                if (c0 + cc < nc) sum[j] += v[j][cc];
+                        }
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int e = e0 + 256 * j;
+                        if (e < total) lds_c[(e >> 7) * A_ROW + (e & 127)] = f16_bits((f16) sum[j]);
+                    }
+                }
+            } else if (!GATED && MT_ != 0 && M > 1) {
                 // one block per pass (rb == 1): every element shares the block's contributors, so a
                 // thread keeps 4 elements x 8 contributors of loads in flight (sums in contributor order)
                 const int bi = s_list[r0];
