@@ -337,6 +337,9 @@ __device__ __forceinline__ void load_qblock_at(gc_u8* __restrict__ base, uint32_
 // format), the unit's byte offset a scalar, the lane's byte offsets fixed VGPRs.  No address
 // arithmetic per load, and the hardware range check turns any stray offset into zeros.
 constexpr int RAW_BUFFER_FLAGS = 0x00020000;
+// cache-policy operand of buffer loads / stores: device scope (sc1).  Stores write through the
+// XCD's L2; loads miss it, so they see device-scope stores from any XCD.
+constexpr int SC1 = 0x10;
 
 template <int BITS>
 __device__ __forceinline__ void load_qblock_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t off_main, uint32_t off_prev,

@@ -461,7 +461,7 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
                     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), prs,
-                                                           part_off(q, i * 8 + j), 0, 0x10);
+                                                           part_off(q, i * 8 + j), 0, SC1);
             __builtin_amdgcn_s_waitcnt(0x0F70);            // vmcnt(0): the partial has landed
             __syncthreads();
             if (t == 0) {
@@ -481,7 +481,7 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
                     for (int pq = 0; pq < a.split; ++pq) {
                         const f32x4 v = pq == q ? acc[i][j]
                                                 : __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                                prs, part_off(pq, i * 8 + j), 0, 0x10));
+                                                                                prs, part_off(pq, i * 8 + j), 0, SC1));
                         sum = pq == 0 ? v : sum + v;
                     }
                     acc[i][j] = sum;
@@ -600,12 +600,16 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
     const uint16_t* ct = reinterpret_cast<const uint16_t*>(lds);
     const int l16 = t & 15;
     const u32x4 sv = *reinterpret_cast<gc_u32x4*>(as_global(gg.svh) + col0 + 8 * l16);
-    g_u16* const gy = as_global(gg.y);
+    // the tile's rows as one raw buffer from row row0 (offsets below 256 * ldy * 2 bytes); the
+    // stores write through L2 (device scope), so the end-of-kernel writeback finds no dirty output
+    const __amdgpu_buffer_rsrc_t ysrc = __builtin_amdgcn_make_buffer_rsrc(gg.y + (int64_t) row0 * a.ldy, 0, 0x7FFFFFFF,
+                                                                          RAW_BUFFER_FLAGS);
     for (int r0 = 0; r0 < PC::MT; r0 += PC::THREADS / 16) {
         const int r = r0 + (t >> 4);
         const u32x4 c = *reinterpret_cast<const u32x4*>(ct + r * PC::C_ROW + 8 * l16);
         const u32x4 res = had128_x8(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, R_SCALE);
-        if (row0 + r < M) *reinterpret_cast<g_u32x4*>(gy + (int64_t) (row0 + r) * a.ldy + col0 + 8 * l16) = res;
+        if (row0 + r < M)
+            __builtin_amdgcn_raw_buffer_store_b128(res, ysrc, (uint32_t) (((int64_t) r * a.ldy + col0 + 8 * l16) * 2), 0, SC1);
     }
 }
 
@@ -658,7 +662,7 @@ int launch_trellis_gemm(const uint16_t* const* xh, int64_t ldx, const void* cons
                         int64_t ldy, const uint16_t* const* svh, const int* widths, int groups, int M, int K,
                         void* ws, size_t ws_bytes, hipStream_t s)
 {
-    bool fits = (uint64_t) M * (uint64_t) ldx * 2 < (1ull << 31);
+    bool fits = (uint64_t) M * (uint64_t) ldx * 2 < (1ull << 31) && (uint64_t) PC::MT * (uint64_t) ldy * 2 < (1ull << 31);
     for (int i = 0; i < groups; ++i) fits = fits && (uint64_t) K * widths[i] * BITS / 8 < (1ull << 31);
     const char* e = getenv("EXL3_GEMM_KERNEL");              // "tile": the 128 x 128 kernel (comparison)
     if (!fits || (e && e[0] == 't')) {
