@@ -163,6 +163,64 @@ __device__ __forceinline__ u32x4 had128_x8(u32x4 in, u32x4 pre, bool has_pre, u3
     return __builtin_bit_cast(u32x4, y);
 }
 
+// 64-bit value of lane (lane ^ 16): ds_swizzle within 32-lane halves (and 0x1F, xor 0x10)
+__device__ __forceinline__ double swz16_f64(double x)
+{
+    const uint64_t u = (uint64_t) __double_as_longlong(x);
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_ds_swizzle((int) (uint32_t) u, 0x401F);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_ds_swizzle((int) (uint32_t) (u >> 32), 0x401F);
+    return __longlong_as_double((long long) (((uint64_t) hi << 32) | lo));
+}
+
+// One 128-block per wave, two elements per lane (lane l holds elements 2l and 2l + 1): element
+// bit 0 in the lane, bits 1..4 lane xor 1, 2, 4, 8 (DPP as in wht128_x8), bit 5 lane xor 16
+// (ds_swizzle), bit 6 lane xor 32 (v_permlane32_swap).  A fourth of wht128_x8's instructions per
+// lane: the latency of the GEMV's single-row output transform, which is on every launch's
+// critical path.  Same exact float64 sums, so the same fp16 results as had128_x8.
+__device__ __forceinline__ uint32_t had128_x2(uint32_t in, uint32_t post, double scale)
+{
+    const f16x2 x = __builtin_bit_cast(f16x2, in);
+    const double a = (double) x[0], b = (double) x[1];
+    double v[2] = {a + b, a - b};
+    const int l = __lane_id();
+    double p[2];
+    auto stage = [&](bool upper) __attribute__((always_inline)) {
+        const double sg = upper ? -1.0 : 1.0;
+        v[0] = __builtin_fma(sg, v[0], p[0]);
+        v[1] = __builtin_fma(sg, v[1], p[1]);
+    };
+#pragma unroll
+    for (int i = 0; i < 2; ++i) p[i] = dpp_f64<DPP_QP_XOR1>(v[i]);
+    stage(l & 1);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) p[i] = dpp_f64<DPP_QP_XOR2>(v[i]);
+    stage(l & 2);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) p[i] = dpp_f64<DPP_QP_REV>(dpp_f64<DPP_HALF_MIRROR>(v[i]));
+    stage(l & 4);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) p[i] = dpp_f64<DPP_ROR8>(v[i]);
+    stage(l & 8);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) p[i] = swz16_f64(v[i]);
+    stage(l & 16);
+    // v_permlane32_swap(x, x) swaps the upper half of its first operand with the lower half of
+    // its second: the first result holds the lower half's values in both halves of the wave, the
+    // second the upper half's.  Lower lanes take lo + hi, upper lanes lo - hi.
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint64_t u = (uint64_t) __double_as_longlong(v[i]);
+        const auto w0 = __builtin_amdgcn_permlane32_swap((uint32_t) u, (uint32_t) u, false, false);
+        const auto w1 = __builtin_amdgcn_permlane32_swap((uint32_t) (u >> 32), (uint32_t) (u >> 32), false, false);
+        const double lo = __longlong_as_double((long long) (((uint64_t) w1[0] << 32) | w0[0]));
+        const double hi = __longlong_as_double((long long) (((uint64_t) w1[1] << 32) | w0[1]));
+        v[i] = __builtin_fma(l & 32 ? -1.0 : 1.0, hi, lo);
+    }
+    f16x2 y = {f64_to_f16_rto(v[0] * scale), f64_to_f16_rto(v[1] * scale)};
+    y = y * __builtin_bit_cast(f16x2, post);
+    return __builtin_bit_cast(uint32_t, y);
+}
+
 // ------------------------------------------------------------------------------------------
 // Codebook constants
 // ------------------------------------------------------------------------------------------

@@ -534,6 +534,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                         sv_first = *reinterpret_cast<gc_u32x4*>(as_global(a.g[0].svh) + cb * 128 + 8 * l16);
                         sv_first_u = *reinterpret_cast<gc_u32x4*>(as_global(a.g[1].svh) + cb * 128 + 8 * l16);
                     }
+                } else if (MT_ == 0) {
+                    // single row: block r of the pair goes to wave r, two columns a lane
+                    if (wave < rb)
+                        sv_first.x = *reinterpret_cast<gc_u32*>(gsvh + (seg0_cb + b0 + s_list[r0 + wave]) * 128 + 2 * lane);
                 } else if (rr < rb * M) {
                     sv_first = *reinterpret_cast<gc_u32x4*>(gsvh + (seg0_cb + b0 + s_list[r0 + rr / M]) * 128 + 8 * l16);
                 }
@@ -721,6 +725,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                                                                (uint32_t) (((int64_t) m * a.ldy + cb * 128 + 8 * l16) * 2), 0, SC1);
                 }
                 __syncthreads();
+                continue;
+            }
+            if constexpr (MT_ == 0) {
+                // output Hadamard + svh of a single row: one wave per block, two columns a lane
+                if (wave < rb) {
+                    const int cb = seg0_cb + b0 + s_list[r0 + wave];
+                    const uint32_t c = *reinterpret_cast<const uint32_t*>(lds_c + wave * A_ROW + 2 * lane);
+                    __builtin_amdgcn_raw_buffer_store_b32(had128_x2(c, sv_first.x, R_SCALE), ysrc,
+                                                          (uint32_t) ((cb * 128 + 2 * lane) * 2), 0, SC1);
+                }
+                __syncthreads();                               // lds_c free for the next blocks
                 continue;
             }
             // output Hadamard + svh: 16 lanes per (block, row)
