@@ -125,6 +125,20 @@ __device__ __forceinline__ u32x4 silu_mul_x8(u32x4 g, u32x4 u)
     return __builtin_bit_cast(u32x4, r);
 }
 
+// the same for two elements (one 32-bit register)
+__device__ __forceinline__ uint32_t silu_mul_x2(uint32_t g, uint32_t u)
+{
+    const f16x2 gh = __builtin_bit_cast(f16x2, g), uh = __builtin_bit_cast(f16x2, u);
+    f16x2 r;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float gf = (float) gh[i];
+        const f16 act = (f16) (gf / (1.0f + expf(-gf)));
+        r[i] = (f16) ((float) act * (float) uh[i]);
+    }
+    return __builtin_bit_cast(uint32_t, r);
+}
+
 // a wave-uniform 64-bit value as a scalar (readfirstlane of both halves)
 __device__ __forceinline__ int64_t uniform_i64(int64_t v)
 {
@@ -528,7 +542,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             u32x4 sv_first = {0u, 0u, 0u, 0u}, sv_first_u = sv_first;
             {
                 const int rr = threadIdx.x >> 4;
-                if (gated) {
+                if (gated && MT_ == 0) {
+                    // single row: pair r goes to wave r, two columns a lane
+                    if (wave < rb) {
+                        const int cb = seg0_cb + b0 + s_list[r0 + wave];
+                        sv_first.x = *reinterpret_cast<gc_u32*>(as_global(a.g[0].svh) + cb * 128 + 2 * lane);
+                        sv_first_u.x = *reinterpret_cast<gc_u32*>(as_global(a.g[1].svh) + cb * 128 + 2 * lane);
+                    }
+                } else if (gated) {
                     if (rr < rb * M) {
                         const int cb = seg0_cb + b0 + s_list[r0 + rr / M];
                         sv_first = *reinterpret_cast<gc_u32x4*>(as_global(a.g[0].svh) + cb * 128 + 8 * l16);
@@ -703,6 +724,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 __hip_atomic_store(&counters[(seg0_cb + b0 + s_list[r0 + threadIdx.x]) * CNT_STRIDE], 0u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
             __syncthreads();
+            if (gated && MT_ == 0) {
+                // single row: pair r on wave r, two columns a lane (gate and up transforms
+                // interleave), SiLU-and-mul into g[0].y
+                if (wave < rb) {
+                    const int cb = seg0_cb + b0 + s_list[r0 + wave];
+                    const uint32_t cg = *reinterpret_cast<const uint32_t*>(lds_c + (wave * RM) * A_ROW + 2 * lane);
+                    const uint32_t cu = *reinterpret_cast<const uint32_t*>(lds_c + (wave * RM + 1) * A_ROW + 2 * lane);
+                    const uint32_t rg = had128_x2(cg, sv_first.x, R_SCALE);
+                    const uint32_t ru = had128_x2(cu, sv_first_u.x, R_SCALE);
+                    __builtin_amdgcn_raw_buffer_store_b32(silu_mul_x2(rg, ru), y0src, (uint32_t) ((cb * 128 + 2 * lane) * 2), 0,
+                                                          SC1);
+                }
+                __syncthreads();
+                continue;
+            }
             if (gated) {
                 // gate and up rows m of pair r: output Hadamard + svh each, then SiLU-and-mul
                 // into g[0].y
