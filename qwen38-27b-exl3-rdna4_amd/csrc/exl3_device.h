@@ -175,11 +175,14 @@ __device__ __forceinline__ double swz16_f64(double x)
 // One 128-block per wave, two elements per lane (lane l holds elements 2l and 2l + 1): element
 // bit 0 in the lane, bits 1..4 lane xor 1, 2, 4, 8 (DPP as in wht128_x8), bit 5 lane xor 16
 // (ds_swizzle), bit 6 lane xor 32 (v_permlane32_swap).  A fourth of wht128_x8's instructions per
-// lane: the latency of the GEMV's single-row output transform, which is on every launch's
-// critical path.  Same exact float64 sums, so the same fp16 results as had128_x8.
-__device__ __forceinline__ uint32_t had128_x2(uint32_t in, uint32_t post, double scale)
+// lane: the latency of the GEMV's single-row input and output transforms, which are on every
+// launch's critical path.  Same exact float64 sums and roundings, so the same fp16 results as
+// had128_x8.
+__device__ __forceinline__ uint32_t had128_x2(uint32_t in, uint32_t pre, bool has_pre, uint32_t post, bool has_post,
+                                              double scale)
 {
-    const f16x2 x = __builtin_bit_cast(f16x2, in);
+    f16x2 x = __builtin_bit_cast(f16x2, in);
+    if (has_pre) x = x * __builtin_bit_cast(f16x2, pre);
     const double a = (double) x[0], b = (double) x[1];
     double v[2] = {a + b, a - b};
     const int l = __lane_id();
@@ -217,7 +220,7 @@ __device__ __forceinline__ uint32_t had128_x2(uint32_t in, uint32_t post, double
         v[i] = __builtin_fma(l & 32 ? -1.0 : 1.0, hi, lo);
     }
     f16x2 y = {f64_to_f16_rto(v[0] * scale), f64_to_f16_rto(v[1] * scale)};
-    y = y * __builtin_bit_cast(f16x2, post);
+    if (has_post) y = y * __builtin_bit_cast(f16x2, post);
     return __builtin_bit_cast(uint32_t, y);
 }
 

@@ -292,7 +292,17 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // the trellis ring (a pass requested after the ring waits behind every workgroup's ring)
     const int nfirst = min(a.chunk_units, uhi - ulo) * M;
     u32x4 px = {0u, 0u, 0u, 0u}, ps = px, px2 = px, ps2 = px;
-    {
+    // a single row of at most 4 jobs: one job per wave, two columns a lane (had128_x2, a fourth
+    // of the 16-lane transform's latency)
+    const bool wide = MT_ == 0 && nfirst <= 4;
+    if (wide) {
+        if (wave < nfirst) {
+            const int u = ulo + wave;
+            const int col = (u - (u / UPB) * UPB) * 128 + 2 * lane;
+            px.x = *reinterpret_cast<gc_u32*>(gx + col);
+            ps.x = *reinterpret_cast<gc_u32*>(gsuh + col);
+        }
+    } else {
         const int i = threadIdx.x >> 4;
         if (i < nfirst) {
             int m, col;
@@ -372,7 +382,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
         }
     };
     int c0 = ulo, c1 = min(ulo + a.chunk_units, uhi);
-    rotate_chunk(c0, c1, px, ps, px2, ps2, true);
+    if (wide) {
+        if (wave < nfirst)
+            *reinterpret_cast<uint32_t*>(lds_a + (wave * UROWS) * A_ROW + 2 * lane) =
+                had128_x2(px.x, ps.x, true, 0u, false, R_SCALE);
+    } else {
+        rotate_chunk(c0, c1, px, ps, px2, ps2, true);
+    }
     static_for(std::make_integer_sequence<int, RING / 2>{}, [&](auto I) __attribute__((always_inline)) {
         fill(std::integral_constant<int, RING / 2 + decltype(I)::value>{});
     });
@@ -731,8 +747,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                     const int cb = seg0_cb + b0 + s_list[r0 + wave];
                     const uint32_t cg = *reinterpret_cast<const uint32_t*>(lds_c + (wave * RM) * A_ROW + 2 * lane);
                     const uint32_t cu = *reinterpret_cast<const uint32_t*>(lds_c + (wave * RM + 1) * A_ROW + 2 * lane);
-                    const uint32_t rg = had128_x2(cg, sv_first.x, R_SCALE);
-                    const uint32_t ru = had128_x2(cu, sv_first_u.x, R_SCALE);
+                    const uint32_t rg = had128_x2(cg, 0u, false, sv_first.x, true, R_SCALE);
+                    const uint32_t ru = had128_x2(cu, 0u, false, sv_first_u.x, true, R_SCALE);
                     __builtin_amdgcn_raw_buffer_store_b32(silu_mul_x2(rg, ru), y0src, (uint32_t) ((cb * 128 + 2 * lane) * 2), 0,
                                                           SC1);
                 }
@@ -768,7 +784,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 if (wave < rb) {
                     const int cb = seg0_cb + b0 + s_list[r0 + wave];
                     const uint32_t c = *reinterpret_cast<const uint32_t*>(lds_c + wave * A_ROW + 2 * lane);
-                    __builtin_amdgcn_raw_buffer_store_b32(had128_x2(c, sv_first.x, R_SCALE), ysrc,
+                    __builtin_amdgcn_raw_buffer_store_b32(had128_x2(c, 0u, false, sv_first.x, true, R_SCALE), ysrc,
                                                           (uint32_t) ((cb * 128 + 2 * lane) * 2), 0, SC1);
                 }
                 __syncthreads();                               // lds_c free for the next blocks
