@@ -394,6 +394,20 @@ __device__ __forceinline__ void load_qblock_at(gc_u8* __restrict__ base, uint32_
     W[0] = *reinterpret_cast<gc_u32*>(base + off_prev);
 }
 
+// s_waitcnt immediate waiting for vmcnt <= n (n < 64) only (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, expcnt 6:4 and lgkmcnt 11:8 at their no-wait maxima)
+constexpr int vmcnt_imm(int n)
+{
+    return (n & 0xF) | ((n >> 4) << 14) | 0x0F70;
+}
+
+// vector-memory instructions of one load_qblock_buf call (for explicit vmcnt waits)
+template <int BITS>
+constexpr int qblock_loads()
+{
+    return (BITS % 4 == 0 ? BITS / 4 : BITS % 2 == 0 ? BITS / 2 : BITS) + 1;
+}
+
 // Buffer-resource form: the trellis is one raw buffer (dword 3 of the resource: gfx9 raw 32-bit
 // format), the unit's byte offset a scalar, the lane's byte offsets fixed VGPRs.  No address
 // arithmetic per load, and the hardware range check turns any stray offset into zeros.

@@ -287,23 +287,27 @@ int launch_gemm(const uint16_t* xh, int64_t ldx, BSRC b, const uint16_t* Wd, int
 //     columns (4 x 8 MFMA tiles of 16 x 16, fp32 accumulators in registers); it only reads A and B
 //     fragments from LDS and issues v_mfma_f32_16x16x32_f16;
 //   waves 4-7 (producers, one per SIMD) decode the trellis tiles of the next K step (one q-block
-//     per lane) into LDS in B-fragment order and stage its xh rows into LDS in A-fragment order.
+//     per lane) into LDS in B-fragment order and request the xh rows of the step after it
+//     straight into LDS (buffer loads with the lds bit: no registers, no LDS store instructions).
 // Every SIMD pairs one MFMA wave with one VALU wave for the whole loop, so matrix and vector work
 // overlap by construction.
 // xh rows are read with whole 128-byte lines per instruction (8 lanes per row: 8 rows x 64 k per
 // wave load), which halves the memory-pipeline line requests of a fragment-shaped load (16 rows x
 // 64 bytes); the row tile's 2 KB of LDS holds (row r, 16-byte chunk c) in slot
-// (r >> 1) * 16 + 8 (r & 1) + (c ^ (r >> 1)), so both the producers' row-chunk stores and the
-// consumers' fragment reads (16 rows of one chunk) hit 16 distinct 16-byte bank groups.
-// Pipeline: two LDS stages and one workgroup barrier B_s per K step.  Between B_{s-1} and B_s the
-// producers stage step s + 1 (its trellis words and xh rows were requested two intervals earlier
-// into register rings) and request step s + 3; the consumers run the step's four 16-MFMA
-// sub-blocks on stage s & 1, each sub-block's fragments read during the previous sub-block, and
-// pass B_s before the last sub-block so that the first fragments of step s + 1 are read under its
-// MFMAs.
+// (r >> 1) * 16 + 8 (r & 1) + (c ^ (r >> 1)), so the consumers' fragment reads (16 rows of one
+// chunk) hit 16 distinct 16-byte bank groups, and a load's 64 consecutive slots (the lds bit
+// writes lane l at slot base + l) are 8 whole rows.
+// Pipeline: three LDS stages and one workgroup barrier B_s per K step.  Between B_{s-1} and B_s
+// the producers decode step s + 1 (its trellis words were requested three intervals earlier into
+// a register ring), request the xh rows of step s + 2 into the stage step s - 1 used and the
+// trellis words of step s + 3, then wait for the xh rows of step s + 1; the consumers run the
+// step's four 16-MFMA sub-blocks on stage s % 3, each sub-block's fragments read during the
+// previous sub-block, and pass B_s before the last sub-block so that the first fragments of step
+// s + 1 are read under its MFMAs.
 // Groups (the checkpoint tensors of a fused module: one x, a rotated input per group) are
-// flattened into one tile list, so a module pays one GEMM launch and fills the GPU as one.  Each output element sees the MFMA sequence of gemm_kernel (k
-// steps in order, two k-substeps each) on the same operands: both kernels give bitwise-equal C.
+// flattened into one tile list, so a module pays one GEMM launch and fills the GPU as one.  Each
+// output element sees the MFMA sequence of gemm_kernel (k steps in order, two k-substeps each) on
+// the same operands: both kernels give bitwise-equal C.
 // ============================================================================================
 struct PcGroup {
     const uint16_t* xh;         // [M][ldx] rotated input of the group (M * ldx * 2 < 2^31)
@@ -334,7 +338,7 @@ struct PC {
     static constexpr int A_BYTES = (MT / 16) * RT_BYTES;   // 32 KB
     static constexpr int B_BYTES = 2 * 8 * FRAG;       // 16 KB
     static constexpr int BUF = A_BYTES + B_BYTES;      // one stage
-    static constexpr int STAGES = 2;
+    static constexpr int STAGES = 3;
     static constexpr int C_ROW = 136;                  // LDS row (halves) of the epilogue's C tile
     static constexpr int LDS = STAGES * BUF > MT * C_ROW * 2 ? STAGES * BUF : MT * C_ROW * 2;
 };
@@ -385,7 +389,7 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
     const int sb = piece ? q * all_steps / a.split : 0;
     const int steps = piece ? (q + 1) * all_steps / a.split - sb : all_steps;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
-    auto stage = [&](int s) __attribute__((always_inline)) { return lds + (s & 1) * PC::BUF; };
+    auto stage = [&](int s) __attribute__((always_inline)) { return lds + (s % PC::STAGES) * PC::BUF; };
     // partial tile of piece pq of this tile: consumer thread t's 32 accumulator quads, 16 B apart
     // per thread (coalesced); system-coherent (sc1) accesses, read by another CU after the counter
     const int tile_r = u - a.n_full;
@@ -504,27 +508,28 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
         // the producer is the longer path of a step: its VALU issue goes first (measured faster)
         __builtin_amdgcn_s_setprio(3);
         const int pw = wave - 4, pt = t - 256;
-        // xh rows 64 pw + 8 i + (lane >> 3), 16-byte chunk lane & 7 (whole 128-byte lines); rows
-        // past M read row M - 1 (their outputs are never stored, and rows do not interact)
+        // xh rows go straight to LDS (buffer loads with the lds bit, 16 bytes a lane): wave pw's
+        // load j fills the 1 KB block L = 8 pw + j of the stage's A tiles, row tile L >> 1, slots
+        // 64 (L & 1) + lane.  Inverting slot = a_slot(r, c) gives lane's row r and chunk c: each
+        // group of 8 lanes reads one row's 8 chunks, a whole 128-byte line.  Rows past M read row
+        // M - 1 (their outputs are never stored, and rows do not interact)
         const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint16_t*>(gg.xh), 0, (int) ((uint32_t) M * (uint32_t) a.ldx * 2u), RAW_BUFFER_FLAGS);
         uint32_t aoff[8];
-        int adst[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int r = 64 * pw + 8 * i + (lane >> 3);                // row in the tile
+        for (int j = 0; j < 8; ++j) {
+            const int L = 8 * pw + j;
+            const int qq = 4 * (L & 1) + (lane >> 4), rem = lane & 15;
+            const int r = (L >> 1) * 16 + 2 * qq + (rem >> 3);             // row in the tile
+            const int c = (rem & 7) ^ qq;                                 // 16-byte chunk
             const int gr = min(row0 + r, M - 1);
-            aoff[i] = ((uint32_t) gr * (uint32_t) a.ldx + (lane & 7) * 8) * 2u;
-            adst[i] = (r >> 4) * PC::RT_BYTES + a_slot(r & 15, lane & 7);
+            aoff[j] = ((uint32_t) gr * (uint32_t) a.ldx + c * 8) * 2u;
         }
-        auto load_a = [&](int st, u32x4* A) __attribute__((always_inline)) {
+        auto dma_a = [&](int st, char* stg) __attribute__((always_inline)) {
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
-                A[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, aoff[i], (sb + st) * (KSTEP * 2), 0));
-        };
-        auto store_a = [&](char* stg, const u32x4* A) __attribute__((always_inline)) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) *reinterpret_cast<u32x4*>(stg + adst[i]) = A[i];
+            for (int j = 0; j < 8; ++j)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (__attribute__((address_space(3))) void*) (stg + (8 * pw + j) * 1024),
+                                                         16, aoff[j], (sb + st) * (KSTEP * 2), 0, 0);
         };
         const int ktl = pt >> 6, ntl = (pt >> 3) & 7, q = pt & 7;
         const int nt_total = gg.n / 16;
@@ -555,38 +560,43 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
                     *reinterpret_cast<u32x4*>(bf + ((ks * 8 + ntl) * 64 + ln) * 16) = val;
                 }
         };
-        // step j's xh rows and trellis words live in register ring slot j % 3 (compile-time slot
-        // indices: the loop is unrolled by 3), requested two intervals before they are staged
-        u32x4 X0[8], X1[8], X2[8];
+        // step j's trellis words live in register ring slot j % 3 (compile-time slot indices: the
+        // loop is unrolled by 3), requested three intervals before they are decoded; its xh rows
+        // go to stage j % 3 two intervals before it is read
+        constexpr int NW = qblock_loads<BITS>();
         uint32_t R0[BITS + 1], R1[BITS + 1], R2[BITS + 1];
-        load_a(0, X0);
+        dma_a(0, stage(0));
         fetch(0, R0);
-        load_a(min(1, steps - 1), X1);
+        dma_a(min(1, steps - 1), stage(1));
         fetch(min(1, steps - 1), R1);
-        load_a(min(2, steps - 1), X2);
         fetch(min(2, steps - 1), R2);
         decode_store(R0, stage(0));
-        store_a(stage(0), X0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(8 + 2 * NW));  // xh rows of step 0 in LDS
         barrier_lds();                                     // B_-1
-        // interval s (between B_s-1 and B_s): stage step s + 1, then request step s + 3 into the
-        // freed slot; the last intervals stage the last step again into a stage no longer read
-        auto interval = [&](int s, const uint32_t* Wd, const u32x4* Xd, uint32_t* Wf, u32x4* Xf) __attribute__((always_inline)) {
+        // interval s (between B_s-1 and B_s): decode step s + 1, request the xh rows of step s + 2
+        // into the stage step s - 1 used (read before B_s-1) and the trellis words of step s + 3,
+        // then wait for the xh rows of step s + 1 (requested one interval earlier; the loads
+        // complete in order and 8 + 2 NW were requested after them).  The last intervals restage
+        // the last step into stages no longer read, so every interval has the same requests in
+        // flight; the last one waits for all of them (the epilogue reuses the stages' LDS).
+        auto interval = [&](int s, const uint32_t* Wd, uint32_t* Wf) __attribute__((always_inline)) {
             decode_store(Wd, stage(s + 1));
-            store_a(stage(s + 1), Xd);
             __builtin_amdgcn_sched_barrier(0);
-            const int s3 = min(s + 3, steps - 1);
-            load_a(s3, Xf);
-            fetch(s3, Wf);
+            dma_a(min(s + 2, steps - 1), stage(s + 2));
+            fetch(min(s + 3, steps - 1), Wf);
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 1 < steps) __builtin_amdgcn_s_waitcnt(vmcnt_imm(8 + 2 * NW));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             barrier_lds();                                 // B_s
         };
         int s = 0;
         for (; s + 2 < steps; s += 3) {
-            interval(s, R1, X1, R0, X0);
-            interval(s + 1, R2, X2, R1, X1);
-            interval(s + 2, R0, X0, R2, X2);
+            interval(s, R1, R0);
+            interval(s + 1, R2, R1);
+            interval(s + 2, R0, R2);
         }
-        if (s < steps) interval(s, R1, X1, R0, X0);
-        if (s + 1 < steps) interval(s + 1, R2, X2, R1, X1);
+        if (s < steps) interval(s, R1, R0);
+        if (s + 1 < steps) interval(s + 1, R2, R1);
         __builtin_amdgcn_s_setprio(0);
         if (piece) {                                       // the consumers' two completion barriers
             __syncthreads();
