@@ -476,20 +476,30 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
             }
             __syncthreads();
             if (!s_last) return;                           // uniform: the whole workgroup leaves
-            // C = sum of the pieces' partials in piece order (this piece's own from registers)
+            // C = sum of the pieces' partials in piece order (this piece's own from registers), 8
+            // accumulator quads at a time: their 8 loads of one piece go out together, one round
+            // trip per piece and batch (a load per quad and piece in turn was 32 x (split - 1)
+            // dependent round trips at the end of the launch)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i) {
+                f32x4 sum[8];
+                for (int pq = 0; pq < a.split; ++pq) {
+                    f32x4 v[8];
+                    if (pq == q) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    f32x4 sum = {0.f, 0.f, 0.f, 0.f};
-                    for (int pq = 0; pq < a.split; ++pq) {
-                        const f32x4 v = pq == q ? acc[i][j]
-                                                : __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                                prs, part_off(pq, i * 8 + j), 0, SC1));
-                        sum = pq == 0 ? v : sum + v;
+                        for (int j = 0; j < 8; ++j) v[j] = acc[i][j];
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            v[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, part_off(pq, i * 8 + j),
+                                                                                                  0, SC1));
                     }
-                    acc[i][j] = sum;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) sum[j] = pq == 0 ? v[j] : sum[j] + v[j];
                 }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc[i][j] = sum[j];
+            }
         }
         // C = fp16(acc) into LDS: every read and write of the stages finished before the last B_s
         uint16_t* ct = reinterpret_cast<uint16_t*>(lds);
