@@ -163,6 +163,63 @@ __device__ __forceinline__ u32x4 had128_x8(u32x4 in, u32x4 pre, bool has_pre, u3
     return __builtin_bit_cast(u32x4, y);
 }
 
+// One 128-block per 8 lanes, 16 elements per lane (lane r = lane & 7 holds elements 16r ..
+// 16r + 15): element bits 0..3 are butterflies inside the lane, bits 4..6 lane xor 1, 2, 4
+// (quad_perm, then row_half_mirror + quad_perm reverse).  Same exact float64 sums and roundings,
+// so the same fp16 results as had128_x8, with fewer cross-lane moves per element.
+__device__ __forceinline__ void had128_x16(const u32x4 (&in)[2], const u32x4 (&pre)[2], bool has_pre,
+                                           const u32x4 (&post)[2], bool has_post, double scale, u32x4 (&out)[2])
+{
+    double v[16];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        f16x8 x = __builtin_bit_cast(f16x8, in[c]);
+        if (has_pre) x = x * __builtin_bit_cast(f16x8, pre[c]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[8 * c + i] = (double) x[i];
+    }
+#pragma unroll
+    for (int h = 1; h < 16; h <<= 1)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (!(i & h)) {
+                const double a = v[i], b = v[i + h];
+                v[i] = a + b;
+                v[i + h] = a - b;
+            }
+    const int r = __lane_id() & 7;
+    double p[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = dpp_f64<DPP_QP_XOR1>(v[i]);
+    {
+        const double sg = (r & 1) ? -1.0 : 1.0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = __builtin_fma(sg, v[i], p[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = dpp_f64<DPP_QP_XOR2>(v[i]);
+    {
+        const double sg = (r & 2) ? -1.0 : 1.0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = __builtin_fma(sg, v[i], p[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = dpp_f64<DPP_QP_REV>(dpp_f64<DPP_HALF_MIRROR>(v[i]));
+    {
+        const double sg = (r & 4) ? -1.0 : 1.0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = __builtin_fma(sg, v[i], p[i]);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        f16x8 y;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = f64_to_f16_rto(v[8 * c + i] * scale);
+        if (has_post) y = y * __builtin_bit_cast(f16x8, post[c]);
+        out[c] = __builtin_bit_cast(u32x4, y);
+    }
+}
+
 // 64-bit value of lane (lane ^ 16): ds_swizzle within 32-lane halves (and 0x1F, xor 0x10)
 __device__ __forceinline__ double swz16_f64(double x)
 {

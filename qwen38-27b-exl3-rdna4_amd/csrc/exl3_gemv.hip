@@ -85,28 +85,37 @@ __global__ void __launch_bounds__(256) reconstruct_kernel(const uint32_t* __rest
 }
 
 // ============================================================================================
-// had_r_128: out = fp16(Had128(in [* pre]) * r * scale) [* post]; one 16-lane group per 128-block,
-// 4 blocks per wave (reference binding `had_r_128`, vllm_plugin/exl3rocm/ops.py:88,97)
+// had_r_128: out = fp16(Had128(in [* pre]) * r * scale) [* post]; one 8-lane group per 128-block,
+// 8 blocks per wave (reference binding `had_r_128`, vllm_plugin/exl3rocm/ops.py:88,97)
 // ============================================================================================
 __global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ in, int64_t ld_in, uint16_t* __restrict__ out,
                                                   int64_t ld_out, int rows, int cols, const uint16_t* __restrict__ pre,
                                                   const uint16_t* __restrict__ post, double scale)
 {
     const int blocks_per_row = cols / 128;
-    const int64_t job = ((int64_t) blockIdx.x * 256 + threadIdx.x) >> 4;     // one 128-block per 16 lanes
+    const int64_t job = ((int64_t) blockIdx.x * 256 + threadIdx.x) >> 3;     // one 128-block per 8 lanes
     const bool live = job < (int64_t) rows * blocks_per_row;
-    const int r = threadIdx.x & 15;
+    const int r = threadIdx.x & 7;
     const int64_t row = live ? job / blocks_per_row : 0;
-    const int col = live ? (int) (job % blocks_per_row) * 128 + 8 * r : 0;
-    u32x4 v = {0u, 0u, 0u, 0u}, pv = v, qv = v;
+    const int col = live ? (int) (job % blocks_per_row) * 128 + 16 * r : 0;
+    u32x4 v[2], pv[2], qv[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) v[c] = pv[c] = qv[c] = u32x4{0u, 0u, 0u, 0u};
     if (live) {
-        v = *reinterpret_cast<const u32x4*>(in + row * ld_in + col);
-        if (pre) pv = *reinterpret_cast<const u32x4*>(pre + col);
-        if (post) qv = *reinterpret_cast<const u32x4*>(post + col);
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            v[c] = *reinterpret_cast<const u32x4*>(in + row * ld_in + col + 8 * c);
+            if (pre) pv[c] = *reinterpret_cast<const u32x4*>(pre + col + 8 * c);
+            if (post) qv[c] = *reinterpret_cast<const u32x4*>(post + col + 8 * c);
+        }
     }
     // every lane takes part in the DPP exchanges; only live lanes store
-    const u32x4 res = had128_x8(v, pv, pre != nullptr, qv, post != nullptr, R_SCALE * scale);
-    if (live) *reinterpret_cast<u32x4*>(out + row * ld_out + col) = res;
+    u32x4 res[2];
+    had128_x16(v, pv, pre != nullptr, qv, post != nullptr, R_SCALE * scale, res);
+    if (live) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) *reinterpret_cast<u32x4*>(out + row * ld_out + col + 8 * c) = res[c];
+    }
 }
 
 // SiLU-and-mul of fp16 rows: out[r][c] = fp16(fp16(silu(gate[r][c])) * up[r][c]), 8 columns a thread
@@ -568,8 +577,8 @@ int exl3_had_r_128(const void* in, int64_t ld_in, void* out, int64_t ld_out, int
         (((uintptr_t) in) & 15) || (((uintptr_t) out) & 15) || (((uintptr_t) pre) & 15) || (((uintptr_t) post) & 15))
         return EXL3_EINVAL;
     if (rows == 0) return EXL3_OK;
-    const int64_t jobs = (int64_t) rows * (cols / 128);           // 16 lanes each
-    hipLaunchKernelGGL(had_kernel, dim3((unsigned) ((jobs + 15) / 16)), dim3(256), 0, (hipStream_t) stream,
+    const int64_t jobs = (int64_t) rows * (cols / 128);           // 8 lanes each
+    hipLaunchKernelGGL(had_kernel, dim3((unsigned) ((jobs + 31) / 32)), dim3(256), 0, (hipStream_t) stream,
                        (const uint16_t*) in, ld_in, (uint16_t*) out, ld_out, rows, cols, (const uint16_t*) pre,
                        (const uint16_t*) post, (double) scale);
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
