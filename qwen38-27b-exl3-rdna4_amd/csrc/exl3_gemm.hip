@@ -18,6 +18,10 @@
 
 using namespace exl3;
 
+// had_r_128 of one input into several outputs in one launch (exl3_gemv.hip)
+int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, int rows, int cols, const void* const* pre,
+               int groups, const void* post, float scale, void* stream);
+
 namespace {
 
 constexpr int NT_COLS = 128, KSTEP = 64;
@@ -740,13 +744,16 @@ int gemm_trellis_common(const void* x, int64_t ldx, const void* const* trellis, 
 {
     const uint16_t* xhs[EXL3_MAX_GROUPS];
     const uint16_t* svs[EXL3_MAX_GROUPS];
+    void* xo[EXL3_MAX_GROUPS];
     for (int i = 0; i < groups; ++i) {
         uint16_t* xi = xh + (int64_t) i * m * k;
-        const int rc = exl3_had_r_128(x, ldx, xi, k, m, k, suh[i], nullptr, 1.0f, s);
-        if (rc) return rc;
+        xo[i] = xi;
         xhs[i] = xi;
         svs[i] = (const uint16_t*) svh[i];
     }
+    // the groups' input transforms (one x, each group's suh) in one launch
+    const int rc = launch_had(x, ldx, xo, k, m, k, suh, groups, nullptr, 1.0f, s);
+    if (rc) return rc;
     const int cb = codebook_of(mcg, mul1);
     switch (K) {
         case 1: return launch_trellis_gemm_cb<1>(cb, xhs, k, trellis, y, ldy, svs, widths, groups, m, k, ws, wsb, s);

@@ -88,10 +88,19 @@ __global__ void __launch_bounds__(256) reconstruct_kernel(const uint32_t* __rest
 // had_r_128: out = fp16(Had128(in [* pre]) * r * scale) [* post]; one 8-lane group per 128-block,
 // 8 blocks per wave (reference binding `had_r_128`, vllm_plugin/exl3rocm/ops.py:88,97)
 // ============================================================================================
-__global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ in, int64_t ld_in, uint16_t* __restrict__ out,
-                                                  int64_t ld_out, int rows, int cols, const uint16_t* __restrict__ pre,
-                                                  const uint16_t* __restrict__ post, double scale)
+// the (pre, out) pair of each group of one launch (a fused module's input transforms read one x);
+// blockIdx.y selects the group, with constant indices only
+struct HadGroups {
+    const uint16_t* pre[EXL3_MAX_GROUPS];
+    uint16_t* out[EXL3_MAX_GROUPS];
+};
+
+__global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ in, int64_t ld_in, HadGroups hg, int64_t ld_out,
+                                                  int rows, int cols, const uint16_t* __restrict__ post, double scale)
 {
+    const int gy = blockIdx.y;
+    const uint16_t* pre = gy == 0 ? hg.pre[0] : gy == 1 ? hg.pre[1] : gy == 2 ? hg.pre[2] : hg.pre[3];
+    uint16_t* out = gy == 0 ? hg.out[0] : gy == 1 ? hg.out[1] : gy == 2 ? hg.out[2] : hg.out[3];
     const int blocks_per_row = cols / 128;
     const int64_t job = ((int64_t) blockIdx.x * 256 + threadIdx.x) >> 3;     // one 128-block per 8 lanes
     const bool live = job < (int64_t) rows * blocks_per_row;
@@ -116,6 +125,28 @@ __global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ i
 #pragma unroll
         for (int c = 0; c < 2; ++c) *reinterpret_cast<u32x4*>(out + row * ld_out + col + 8 * c) = res[c];
     }
+}
+
+// had_r_128 of one input into `groups` outputs, group i scaled by pre[i] (may be null): one launch
+// (the prefill's input transforms of a fused module)
+int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, int rows, int cols, const void* const* pre,
+               int groups, const void* post, float scale, void* stream)
+{
+    if (!in || !out || rows < 0 || cols % 128 || cols < 128 || ld_in < cols || ld_out < cols || ld_in % 8 || ld_out % 8 ||
+        groups < 1 || groups > EXL3_MAX_GROUPS || (((uintptr_t) in) & 15) || (((uintptr_t) post) & 15))
+        return EXL3_EINVAL;
+    HadGroups hg{};
+    for (int i = 0; i < groups; ++i) {
+        const void* p = pre ? pre[i] : nullptr;
+        if (!out[i] || (((uintptr_t) out[i]) & 15) || (((uintptr_t) p) & 15)) return EXL3_EINVAL;
+        hg.pre[i] = (const uint16_t*) p;
+        hg.out[i] = (uint16_t*) out[i];
+    }
+    if (rows == 0) return EXL3_OK;
+    const int64_t jobs = (int64_t) rows * (cols / 128);           // 8 lanes each
+    hipLaunchKernelGGL(had_kernel, dim3((unsigned) ((jobs + 31) / 32), (unsigned) groups), dim3(256), 0, (hipStream_t) stream,
+                       (const uint16_t*) in, ld_in, hg, ld_out, rows, cols, (const uint16_t*) post, (double) scale);
+    return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 
 // SiLU-and-mul of fp16 rows: out[r][c] = fp16(fp16(silu(gate[r][c])) * up[r][c]), 8 columns a thread
@@ -573,15 +604,9 @@ int exl3_silu_mul(const void* gate, const void* up, int64_t ld_in, void* out, in
 int exl3_had_r_128(const void* in, int64_t ld_in, void* out, int64_t ld_out, int rows, int cols, const void* pre,
                    const void* post, float scale, void* stream)
 {
-    if (!in || !out || rows < 0 || cols % 128 || cols < 128 || ld_in < cols || ld_out < cols || ld_in % 8 || ld_out % 8 ||
-        (((uintptr_t) in) & 15) || (((uintptr_t) out) & 15) || (((uintptr_t) pre) & 15) || (((uintptr_t) post) & 15))
-        return EXL3_EINVAL;
-    if (rows == 0) return EXL3_OK;
-    const int64_t jobs = (int64_t) rows * (cols / 128);           // 8 lanes each
-    hipLaunchKernelGGL(had_kernel, dim3((unsigned) ((jobs + 31) / 32)), dim3(256), 0, (hipStream_t) stream,
-                       (const uint16_t*) in, ld_in, (uint16_t*) out, ld_out, rows, cols, (const uint16_t*) pre,
-                       (const uint16_t*) post, (double) scale);
-    return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
+    void* const outs[1] = {out};
+    const void* const pres[1] = {pre};
+    return launch_had(in, ld_in, outs, ld_out, rows, cols, pres, 1, post, scale, stream);
 }
 
 }  // extern "C"
