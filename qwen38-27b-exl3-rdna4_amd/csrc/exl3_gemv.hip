@@ -195,12 +195,13 @@ struct GridPlan {
     Split split[EXL3_MAX_GROUPS];
 };
 
-// Unit-split weights of first-dispatched / second workgroups on a CU: the measured issue share of
-// an older wave on a SIMD shared by two (EXL3_GEMV_WEIGHTS="a,b" overrides, for measurement)
+// Unit-split weights of first-dispatched / second workgroups on a CU: the second runs its loop at
+// the higher wave priority and takes the larger share (EXL3_GEMV_WEIGHTS="a,b" overrides, for
+// measurement)
 void split_weights(int& wa, int& wb)
 {
-    wa = 3;
-    wb = 2;
+    wa = 2;
+    wb = 3;
     const char* e = getenv("EXL3_GEMV_WEIGHTS");
     int a = 0, b = 0;
     if (e && sscanf(e, "%d,%d", &a, &b) == 2 && a >= 1 && b >= 1 && a <= 64 && b <= 64) {

@@ -480,7 +480,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
         }
     };
 
-    __builtin_amdgcn_s_setprio(0);
+    // In the loop the second-dispatched workgroup of a CU runs at the higher priority (and takes
+    // the larger unit share, weights 2 : 3): it starts later, and at equal priority the arbiter
+    // favours the older wave, so the younger one's loop ended last (timeline probe).
+    if (older) __builtin_amdgcn_s_setprio(0);
+    else __builtin_amdgcn_s_setprio(1);
     // Full ring turns run without per-step conditions (a conditional step would make the compiler
     // wait for every load in flight); the last, partial turn only drains the ring.
     const int S = 2 * (uhi - ulo);                            // 64-row k steps of this workgroup

@@ -116,7 +116,8 @@ def test_gemv_split_fast_division_matches_brute_force():
     L = _lib.lib()
     cases = [(1600, 512, 256, 3, 2), (5440, 256, 256, 3, 2), (5440, 256, 0, 3, 2), (320, 160, 160, 3, 2),
              (18496, 512, 256, 3, 2), (77600, 512, 256, 3, 2), (2 ** 21, 512, 256, 3, 2), (40, 2, 2, 1, 1),
-             (1, 1, 1, 1, 1), (7, 7, 3, 1, 64)]
+             (1, 1, 1, 1, 1), (7, 7, 3, 1, 64), (1600, 512, 256, 2, 3), (2240, 512, 256, 2, 3), (5440, 512, 256, 2, 3),
+             (10880, 512, 256, 2, 3)]
     rng = random.Random(7)
     for _ in range(150):
         G = rng.randint(1, 600)
