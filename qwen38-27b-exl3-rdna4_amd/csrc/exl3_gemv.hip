@@ -346,11 +346,15 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
     a.ldx = ldx;
     if (xr && !tabs && m > 1 && m >= prerot_rows()) {
         if (((uintptr_t) xr) & 15) return EXL3_EINVAL;
+        // every group's rotated rows in one launch
+        void* outs[EXL3_MAX_GROUPS];
+        const void* pres[EXL3_MAX_GROUPS];
         for (int i = 0; i < groups; ++i) {
-            const int rc = exl3_had_r_128(x, ldx, (uint16_t*) xr + (int64_t) i * m * k, k, m, k, gs[i].suh, nullptr,
-                                          1.0f, stream);
-            if (rc != EXL3_OK) return rc;
+            outs[i] = (uint16_t*) xr + (int64_t) i * m * k;
+            pres[i] = gs[i].suh;
         }
+        const int rc = launch_had(x, ldx, outs, k, m, k, pres, groups, nullptr, 1.0f, stream);
+        if (rc != EXL3_OK) return rc;
         a.xr = (const uint16_t*) xr;
     }
     for (int i = 0; i < groups; ++i) {

@@ -209,12 +209,14 @@ def test_grouped_rows_and_pointer_table_form():
     assert_close(rows1.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("m", [6, 16])
 @pytest.mark.parametrize("widths,bits,cb", [((2048, 512, 512), 4, 2), ((1024, 256, 384, 128), 3, 1)])
-def test_grouped_widths_parity_and_rows(widths, bits, cb):
+def test_grouped_widths_parity_and_rows(widths, bits, cb, m):
     """Mixed-width groups sharing x (q/k/v) in one launch: every group's columns match the
     oracle to the parity bar, every row of an m-row call == its m = 1 call bitwise, and
-    linear_groups routes the module through this form."""
-    k, m = 2048, 6
+    linear_groups routes the module through this form.  m = 16 takes the pre-rotated input (all
+    groups' rows rotated by one transform launch)."""
+    k = 2048
     mats = [synth.layer("wid", i, k, n, bits) for i, n in enumerate(widths)]
     x = synth.activations(synth.key_of("wid", "x", bits), m, k)
     X = to_dev(x)[0]
