@@ -458,11 +458,14 @@ constexpr int vmcnt_imm(int n)
     return (n & 0xF) | ((n >> 4) << 14) | 0x0F70;
 }
 
-// vector-memory instructions of one load_qblock_buf call (for explicit vmcnt waits)
+// Vector-memory instructions of one load_qblock_buf call (for explicit vmcnt waits).  The main
+// words go out as the fewest loads that can carry them (16-byte loads, then one 12/8/4-byte load
+// of the rest), so no load of the call can be merged with another (no load is wider than 16 bytes)
+// and the count cannot shrink under the compiler; the ring predecessor is one more.
 template <int BITS>
 constexpr int qblock_loads()
 {
-    return (BITS % 4 == 0 ? BITS / 4 : BITS % 2 == 0 ? BITS / 2 : BITS) + 1;
+    return (BITS + 3) / 4 + 1;
 }
 
 // Buffer-resource form: the trellis is one raw buffer (dword 3 of the resource: gfx9 raw 32-bit
@@ -473,25 +476,29 @@ constexpr int RAW_BUFFER_FLAGS = 0x00020000;
 // XCD's L2; loads miss it, so they see device-scope stores from any XCD.
 constexpr int SC1 = 0x10;
 
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+
+// The lane's BITS main words as BITS / 4 16-byte loads and one load of the BITS % 4 remaining
+// words (dword-aligned multi-word buffer loads), then the ring predecessor: qblock_loads<BITS>()
+// instructions exactly.
 template <int BITS>
 __device__ __forceinline__ void load_qblock_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t off_main, uint32_t off_prev,
                                                 uint32_t soff, uint32_t* W)
 {
-    if constexpr (BITS % 4 == 0) {
 #pragma unroll
-        for (int i = 0; i < BITS / 4; ++i) {
-            const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off_main + 16 * i, soff, 0));
-            W[1 + 4 * i] = v[0]; W[2 + 4 * i] = v[1]; W[3 + 4 * i] = v[2]; W[4 + 4 * i] = v[3];
-        }
-    } else if constexpr (BITS % 2 == 0) {
-#pragma unroll
-        for (int i = 0; i < BITS / 2; ++i) {
-            const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, off_main + 8 * i, soff, 0));
-            W[1 + 2 * i] = v[0]; W[2 + 2 * i] = v[1];
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < BITS; ++i) W[1 + i] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, off_main + 4 * i, soff, 0);
+    for (int i = 0; i < BITS / 4; ++i) {
+        const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off_main + 16 * i, soff, 0));
+        W[1 + 4 * i] = v[0]; W[2 + 4 * i] = v[1]; W[3 + 4 * i] = v[2]; W[4 + 4 * i] = v[3];
+    }
+    constexpr int B = 4 * (BITS / 4), R = BITS % 4;
+    if constexpr (R == 3) {
+        const u32x3 v = __builtin_bit_cast(u32x3, __builtin_amdgcn_raw_buffer_load_b96(rsrc, off_main + 4 * B, soff, 0));
+        W[1 + B] = v[0]; W[2 + B] = v[1]; W[3 + B] = v[2];
+    } else if constexpr (R == 2) {
+        const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, off_main + 4 * B, soff, 0));
+        W[1 + B] = v[0]; W[2 + B] = v[1];
+    } else if constexpr (R == 1) {
+        W[1 + B] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, off_main + 4 * B, soff, 0);
     }
     W[0] = __builtin_amdgcn_raw_buffer_load_b32(rsrc, off_prev, soff, 0);
 }

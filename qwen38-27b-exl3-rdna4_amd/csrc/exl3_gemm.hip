@@ -577,15 +577,24 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
         // step j's trellis words live in register ring slot j % 3 (compile-time slot indices: the
         // loop is unrolled by 3), requested three intervals before they are decoded; its xh rows
         // go to stage j % 3 two intervals before it is read
+        // The explicit waits below count vector-memory instructions: 8 per dma_a and exactly NW per
+        // fetch (no fetch load can merge with another, qblock_loads), issued in the order written
+        // (sched_barrier between every request group).  tests/isa_waits.py checks the built code
+        // object: on every path into every barrier, only the most recent 8 row loads may be in flight.
         constexpr int NW = qblock_loads<BITS>();
         uint32_t R0[BITS + 1], R1[BITS + 1], R2[BITS + 1];
         dma_a(0, stage(0));
+        __builtin_amdgcn_sched_barrier(0);
         fetch(0, R0);
+        __builtin_amdgcn_sched_barrier(0);
         dma_a(min(1, steps - 1), stage(1));
+        __builtin_amdgcn_sched_barrier(0);
         fetch(min(1, steps - 1), R1);
         fetch(min(2, steps - 1), R2);
+        __builtin_amdgcn_sched_barrier(0);
         decode_store(R0, stage(0));
-        __builtin_amdgcn_s_waitcnt(vmcnt_imm(8 + 2 * NW));  // xh rows of step 0 in LDS
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(8 + 2 * NW));  // xh rows of step 0 in LDS (8 + 3 NW after them)
         barrier_lds();                                     // B_-1
         // interval s (between B_s-1 and B_s): decode step s + 1, request the xh rows of step s + 2
         // into the stage step s - 1 used (read before B_s-1) and the trellis words of step s + 3,
@@ -597,6 +606,7 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
             decode_store(Wd, stage(s + 1));
             __builtin_amdgcn_sched_barrier(0);
             dma_a(min(s + 2, steps - 1), stage(s + 2));
+            __builtin_amdgcn_sched_barrier(0);
             fetch(min(s + 3, steps - 1), Wf);
             __builtin_amdgcn_sched_barrier(0);
             if (s + 1 < steps) __builtin_amdgcn_s_waitcnt(vmcnt_imm(8 + 2 * NW));

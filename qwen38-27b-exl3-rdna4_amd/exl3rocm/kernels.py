@@ -42,19 +42,28 @@ def _bits_of(trellis: torch.Tensor) -> int:
 # workspace (GEMV split-K partials + completion counters), one per (device, stream)
 # ---------------------------------------------------------------------------------------------
 _workspaces: dict = {}
+_reserved: dict = {}        # device -> the largest workspace any reservation asked for
 
 
-def workspace(device: torch.device, nbytes: int, stream: Optional[int] = None) -> torch.Tensor:
-    """Grow-only zeroed workspace for the current (or given) stream of `device`.  Reserve it at
-    load time (Exl3LinearMethod.process_weights_after_loading) so graph capture never allocates."""
+def workspace(device: torch.device, nbytes: int, stream: Optional[int] = None, reserve: bool = False) -> torch.Tensor:
+    """Grow-only zeroed workspace for the current (or given) stream of `device`.
+
+    Layers reserve at load time (reserve=True, Exl3LinearMethod.process_weights_after_loading),
+    which also raises the device's reserved size.  A stream's first eager call then allocates
+    that whole reserved size, not just its own call's, so the serving sequence (load, eager
+    warm-up on stream S, graph capture on S) never needs an allocation during capture, on any
+    stream.  During capture a stream without a large enough workspace raises."""
     device = torch.device(device)
     if stream is None:
         stream = torch.cuda.current_stream(device).cuda_stream
+    if reserve:
+        _reserved[device] = max(_reserved.get(device, 0), nbytes)
     key = (device, stream)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
-        _need(not torch.cuda.is_current_stream_capturing(), "workspace must be reserved before graph capture")
-        buf = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
+        _need(not torch.cuda.is_current_stream_capturing(),
+              "GEMV workspace: this stream made no eager call of this size before graph capture")
+        buf = torch.zeros(max(nbytes, _reserved.get(device, 0), 4096), dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf
 

@@ -54,10 +54,13 @@ def _weight_buffer(device, numel):
 
 
 def reserve_workspace(device, k: int, n: int, K: int, groups: int = 1, m: int = MR_MAX):
-    """Reserve the GEMV workspace of the current stream for up to m rows (load time)."""
+    """Reserve the GEMV workspace for up to m rows (load time): the current stream gets it now, and
+    every other stream gets at least this much on its first eager call (so a later graph capture on
+    that stream never allocates)."""
     if m < 1:
         return
-    E.workspace(torch.device(device), E.gemv_workspace_bytes(min(m, _lib.GEMV_MAX_ROWS), k, n, K, groups))
+    E.workspace(torch.device(device), E.gemv_workspace_bytes(min(m, _lib.GEMV_MAX_ROWS), k, n, K, groups),
+                reserve=True)
 
 
 def _prep(x: torch.Tensor):
