@@ -40,6 +40,7 @@ extern "C" {
 #define EXL3_MAX_GROUPS 4       /* groups per grouped launch (reference EXL3_GEMV_MRG_MAX) */
 #define EXL3_GEMV_MAX_ROWS 32   /* rows handled by the fused GEMV */
 #define EXL3_GEMV_COUNTER_BYTES 262144 /* workspace head reserved for completion counters (one per 128-byte line) */
+#define EXL3_NOALLOC_SCRATCH_BYTES 17039360 /* 16.25 MiB: exl3_gemv_mr_noalloc's per-GPU device array */
 
 #define EXL3_OK 0
 #define EXL3_DECLINED 1
@@ -205,6 +206,18 @@ size_t exl3_gemm_trellis_workspace_size(int m, int k, const int* widths, int gro
 int exl3_gemm(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh, void* A_had,
               const void* svh, int m, int k, int n, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
               void* stream);
+
+/* exl3_gemv_mr without a workspace argument and without any allocation: the same kernels and the
+ * same output, bitwise, with the workspace in a file-scope device array of
+ * EXL3_NOALLOC_SCRATCH_BYTES that each GPU keeps until the process ends.  Shapes whose workspace
+ * (exl3_gemv_workspace_size(m, k, n, K, 1)) exceeds it return EXL3_EWORKSPACE before any launch:
+ * at m <= 32 every k, n <= 32768 with n <= 21760 fits (every Qwen-27B layer), the first that does
+ * not is k = 256, n = 21888.  Shapes the GEMV does not take return exl3_gemv_mr's status.  Calls that overlap on one GPU race on the
+ * array: serialize them (one stream, or one graph replay at a time).
+ * No counterpart in the reference.  For callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. */
+int exl3_gemv_mr_noalloc(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh,
+                         const void* svh, int m, int k, int n, int K, int mcg, int mul1, void* stream);
 
 #ifdef __cplusplus
 }

@@ -14,6 +14,7 @@ LIB_PATH = os.environ.get("EXL3_MI355X_LIB", os.path.join(HERE, "libexl3_mi355x.
 OK, DECLINED, EINVAL, ELAUNCH, EWORKSPACE = 0, 1, -1, -2, -3
 MAX_GROUPS = 4
 GEMV_MAX_ROWS = 32
+NOALLOC_SCRATCH_BYTES = 17039360
 ABI_VERSION = 1
 
 _p, _i, _i64, _sz, _f = C.c_void_p, C.c_int, C.c_int64, C.c_size_t, C.c_float
@@ -48,6 +49,7 @@ SIGNATURES = {
                                        _p]),
     "exl3_gemm_trellis_workspace_size": (_sz, [_i, _i, _ip, _i]),
     "exl3_gemm": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
+    "exl3_gemv_mr_noalloc": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
 }
 
 _lib = None

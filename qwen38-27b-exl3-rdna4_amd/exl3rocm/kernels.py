@@ -206,6 +206,22 @@ def exl3_gemv_mr(A, B, C, suh, A_had, svh, K: int, mcg: bool, mul1: bool) -> int
                    "exl3_gemv_mr")
 
 
+def exl3_gemv_mr_noalloc(A, B, C, suh, svh, K: int, mcg: bool, mul1: bool) -> int:
+    """exl3_gemv_mr with its workspace in the library's per-GPU device array: no allocation here
+    or in the library.  Calls that overlap on one GPU race (one stream at a time)."""
+    _cuda(A, B, C, suh, svh)
+    x2, m, k = _rows(A)
+    n = svh.shape[0]
+    _need(B.shape[-1] == 16 * K, "exl3_gemv_mr_noalloc: trellis last dim must be 16*K")
+    rc = L.lib().exl3_gemv_mr_noalloc(x2.data_ptr(), x2.stride(0) if m > 1 else k, B.data_ptr(), C.data_ptr(),
+                                      _ldy(C, n), suh.data_ptr(), svh.data_ptr(), m, k, n, K, *_cb_flags(mcg, mul1),
+                                      _stream(A))
+    if rc == L.EWORKSPACE:
+        raise L.Exl3Error(f"exl3rocm: exl3_gemv_mr_noalloc: m={m} k={k} n={n} needs more than the "
+                          f"{L.NOALLOC_SCRATCH_BYTES}-byte scratch array")
+    return L.check(rc, "exl3_gemv_mr_noalloc")
+
+
 def exl3_gemv_mr_grouped(A, B: Sequence[torch.Tensor], C, suh: Sequence[torch.Tensor], A_had,
                          svh: Sequence[torch.Tensor], K: int, mcg: bool, mul1: bool, bszm_for_warps: int = 1) -> int:
     _cuda(A, C, *B, *suh, *svh)
