@@ -37,6 +37,11 @@ sys.path.insert(0, os.path.join(REPO, "qwen38-27b-exl3-rdna4_amd"))
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 MFMA_FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
 HIDDEN, INTER, KV = 5120, 17408, 1024
+# VALU decode budget (diagnostic): vector lane-ops per second of the whole chip (256 CUs x 4 SIMDs x
+# 16 lanes x 2.4 GHz, one full-rate op per lane per clock) and the lane-ops per weight of the 4-bpw
+# mul1 GEMV loop (ISA count of the built loop: 129 VALU instructions per lane per 32 weights)
+VALU_LANE_OPS_PER_S = 256 * 4 * 16 * 2.4e9
+VALU_OPS_PER_WEIGHT_4BPW = 129 / 32
 LAYER = [("q", HIDDEN, HIDDEN), ("k", HIDDEN, KV), ("v", HIDDEN, KV), ("o", HIDDEN, HIDDEN),
          ("gate", HIDDEN, INTER), ("up", HIDDEN, INTER), ("down", INTER, HIDDEN)]
 
@@ -92,8 +97,10 @@ def build_layers(torch, bits, copies, mul1=True, tag="config1"):
     return base, sets
 
 
-def capture_steps(torch, sets, x5120, x17408):
-    """One HIP graph per weight copy (each replays one decode step)."""
+def capture_steps(torch, sets, x5120, x17408, steps):
+    """Graphs of the timed region: one graph of `block` consecutive steps cycling over the weight
+    copies (a layer stack, as a captured decode step replays it), replayed steps // block times,
+    plus one of the remaining steps % block; and one single-step graph per copy for the warmup."""
     from exl3rocm import ops as exl3_ops
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -104,36 +111,36 @@ def capture_steps(torch, sets, x5120, x17408):
             ls.step(x5120, x17408)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    graphs = []
-    for ls in sets:
+
+    def graph_of(first, count):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=s):
-            ls.step(x5120, x17408)
-        graphs.append(g)
-    # all copies' steps in one graph (one step per layer of an 8-layer stack), so host launches
-    # between replays are rare
-    stack = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(stack, stream=s):
-        for ls in sets:
-            ls.step(x5120, x17408)
+            for i in range(first, first + count):
+                sets[i % len(sets)].step(x5120, x17408)
+        return g
+
+    singles = [graph_of(i, 1) for i in range(len(sets))]
+    block = min(steps, 256)
+    full = graph_of(0, block) if steps >= block > 0 else None
+    rest = graph_of(0, steps % block) if steps % block else None
     torch.cuda.synchronize()
-    return graphs, stack
+    return {"singles": singles, "block": block, "full": full, "rest": rest}
 
 
 def time_graphs(torch, graphs, steps, warmup):
-    """Exactly `steps` steps: steps // copies replays of the stack graph, then single-step graphs."""
-    per, stack = graphs
-    n = len(per)
+    """Exactly `steps` steps after `warmup` untimed single steps: the block graph steps // block
+    times, then the remainder graph; HIP events on the replay stream, plus host wall time."""
+    per = graphs["singles"]
     for i in range(warmup):
-        per[i % n].replay()
+        per[i % len(per)].replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record()
-    for _ in range(steps // n):
-        stack.replay()
-    for i in range(steps % n):
-        per[i].replay()
+    for _ in range(steps // graphs["block"]):
+        graphs["full"].replay()
+    if graphs["rest"] is not None:
+        graphs["rest"].replay()
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -224,34 +231,68 @@ def gated_mlp(torch, sets, x5120, ms=(1, 8), reps=32):
     return out
 
 
-def cpu_baseline(base, bits, budget_s=12.0):
-    """The C oracle's faithful GEMV over the layer's 7 linears (M = 1), repeated within a time
-    budget on the host cores; GB/s of the same algorithmic bytes."""
+def cpu_baseline(base, bits, budget_s=8.0):
+    """The C oracle restatement on the host cores: the configuration-1 layer's 7 faithful GEMVs at
+    M = 1 repeated for `budget_s` on every thread of this process's CPU share (the headline
+    baseline), plus bounded side samples: one thread, decode only (reconstruct), configuration 0
+    (4096 x 4096 mcg), configuration 2 (gate shape at 2 / 3 / 5 / 6 / 8 bpw) and a configuration-4
+    subsample (q at M = 64).  Every figure is GB/s of the same algorithmic bytes as the GPU's."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import cpu  # noqa: E402  (oracle: test infrastructure, used here only as the baseline)
     from exl3rocm import synth
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, len(os.sched_getaffinity(0)))
+    affinity = len(os.sched_getaffinity(0))
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, affinity)
     x = {k: synth.activations(synth.key_of("cpu", k), 1, k) for k in (HIDDEN, INTER)}
     layer_bytes = sum(algo_bytes(1, k, n, bits) for _, k, n in LAYER)
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
+
+    def timed(fn, nbytes, budget, min_reps=1):
+        t0 = time.perf_counter()
+        reps = 0
+        while reps < min_reps or time.perf_counter() - t0 < budget:
+            fn()
+            reps += 1
+        dt = time.perf_counter() - t0
+        return {"gbs": round(reps * nbytes / dt / 1e9, 4), "us_per_call": round(dt / reps * 1e6, 1), "reps": reps}
+
+    def layer(th):
         for name, k, n in LAYER:
             tr, su, sv = base[name]
-            cpu.linear(x[k], tr, bits, su, sv, 2, threads=threads)
-        reps += 1
-        if time.perf_counter() - t0 > budget_s:
-            break
-    dt = time.perf_counter() - t0
+            cpu.linear(x[k], tr, bits, su, sv, 2, threads=th)
+
+    head = timed(lambda: layer(threads), layer_bytes, budget_s)
+    side = {"threads": threads, "affinity_cores": affinity}
+    gate_tr, gate_su, gate_sv = base["gate"]
+    side["config1_gate_1thread"] = timed(lambda: cpu.linear(x[HIDDEN], gate_tr, bits, gate_su, gate_sv, 2, threads=1),
+                                         algo_bytes(1, HIDDEN, INTER, bits), 2.0)
+    gate_bytes = HIDDEN * INTER * bits // 8
+    side["decode_only_gate"] = timed(lambda: cpu.reconstruct(gate_tr, bits, 2, threads=threads), gate_bytes, 2.0)
+    tr0, su0, sv0 = synth.layer("cpu-config0", 0, 4096, 4096, 4)
+    x0 = synth.activations(synth.key_of("cpu-config0", "x"), 1, 4096)
+    side["config0_mcg_4096"] = timed(lambda: cpu.linear(x0, tr0, 4, su0, sv0, 1, threads=threads),
+                                     algo_bytes(1, 4096, 4096, 4), 2.0)
+    sweep = {}
+    for b in (2, 3, 5, 6, 8):
+        trb, sub, svb = synth.layer("cpu-config2", b, HIDDEN, INTER, b)
+        sweep[f"{b}bpw"] = timed(lambda: cpu.linear(x[HIDDEN], trb, b, sub, svb, 2, threads=threads),
+                                 algo_bytes(1, HIDDEN, INTER, b), 0.0)
+    side["config2_gate_sweep"] = sweep
+    x64 = synth.activations(synth.key_of("cpu-config4", "x"), 64, HIDDEN)
+    trq, suq, svq = base["q"]
+    side["config4_q_m64"] = timed(lambda: cpu.linear(x64, trq, bits, suq, svq, 2, threads=threads),
+                                  algo_bytes(64, HIDDEN, HIDDEN, bits), 0.0)
+    side["config4_q_m64"]["tflops"] = round(2 * 64 * HIDDEN * HIDDEN / (side["config4_q_m64"]["us_per_call"] * 1e6), 6)
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
             model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
     except OSError:
         pass
-    return {"value": round(reps * layer_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} x the 7 linears of one layer at M=1, 4 bpw mul1 (C oracle, OpenMP {threads} "
-                      f"threads, {dt:.1f} s); cpu: {model}"}
+    side["cpu_model"] = model
+    return {"value": head["gbs"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{head['reps']} x the 7 linears of one configuration-1 layer at M=1, 4 bpw mul1 "
+                      f"(C oracle restatement, OpenMP {threads} threads of {affinity} in the affinity mask, "
+                      f"{head['reps'] * head['us_per_call'] / 1e6:.1f} s); cpu: {model}",
+            "side": side}
 
 
 def prefill_chunk(torch, layers=64, m=2048, bits=4, iters=2):
@@ -304,37 +345,55 @@ def prefill_chunk(torch, layers=64, m=2048, bits=4, iters=2):
             "frac_mfma_fp16": round(tf / MFMA_FP16_PEAK_TFLOPS, 4), "flops_per_chunk": flops}
 
 
-def small_batch(torch, sets, ms=(1, 4, 8, 16, 32), reps=32):
-    """Configuration 3: gate/up and down at M in {1, 4, 8, 16, 32}, heavy-tail activations; mean
-    duration per call from a graph of `reps` calls over the weight copies (HIP events on the replay
-    stream)."""
-    from exl3rocm import synth
+def small_batch(torch, sets, ms=(1, 4, 8, 16, 32), gemm_ms=(4, 8, 16, 32, 33, 64, 128, 256), reps=32):
+    """Configuration 3: gate (5120 -> 17408) and down (17408 -> 5120) at M in {1, 4, 8, 16, 32}
+    through the op (the fused GEMV), heavy-tail activations; and the prefill GEMM (the route for
+    M > 32) at M from 4 to 256, for the GEMV -> GEMM crossover: the smallest M at which the GEMM is
+    faster than the GEMV, or "none below 33" (the op routes M <= 32 to the GEMV).  Mean duration
+    per call from a graph of `reps` calls over the weight copies (HIP events on the replay stream)."""
+    from exl3rocm import kernels as E, synth
     res = {}
     s = torch.cuda.Stream()
+
+    def graph_us(fn):
+        with torch.cuda.stream(s):
+            for ls in sets:
+                fn(ls)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for r in range(reps):
+                fn(sets[r % len(sets)])
+        with torch.cuda.stream(s):
+            g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(3):
+                g.replay()
+            e1.record(s)
+        s.synchronize()
+        del g
+        return round(e0.elapsed_time(e1) * 1e3 / (3 * reps), 2)
+
     for name in ("gate", "down"):
         k = INTER if name == "down" else HIDDEN
+        n = HIDDEN if name == "down" else INTER
         row = {}
+        xs = {m: torch.from_numpy(synth.activations(synth.key_of("cfg3", k, m), m, k, heavy_tail=True)).cuda()
+              for m in sorted(set(ms) | set(gemm_ms))}
         for m in ms:
-            x = torch.from_numpy(synth.activations(synth.key_of("cfg3", k, m), m, k, heavy_tail=True)).cuda()
-            fn = (lambda ls, x=x: torch.ops.exl3rocm.linear(x, *ls.w[name], ls.bits, ls.mcg, ls.mul1))
-            with torch.cuda.stream(s):
-                for ls in sets:
-                    fn(ls)
-            s.synchronize()
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=s):
-                for r in range(reps):
-                    fn(sets[r % len(sets)])
-            with torch.cuda.stream(s):
-                g.replay()
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(s)
-                for _ in range(3):
-                    g.replay()
-                e1.record(s)
-            s.synchronize()
-            row[f"m{m}_us"] = round(e0.elapsed_time(e1) * 1e3 / (3 * reps), 2)
-            del g
+            x = xs[m]
+            row[f"m{m}_us"] = graph_us(lambda ls, x=x: torch.ops.exl3rocm.linear(x, *ls.w[name], ls.bits, ls.mcg, ls.mul1))
+        gemm = {}
+        for m in gemm_ms:
+            x = xs[m]
+            y = torch.empty(m, n, dtype=torch.float16, device="cuda")
+            xh = torch.empty(m, k, dtype=torch.float16, device="cuda")
+            gemm[f"m{m}_us"] = graph_us(lambda ls, x=x, y=y, xh=xh: E.exl3_gemm_trellis_grouped(
+                x, [ls.w[name][0]], y, [ls.w[name][1]], xh, [ls.w[name][2]], ls.bits, ls.mcg, ls.mul1))
+        row["prefill_gemm"] = gemm
+        cross = [m for m in ms if m in gemm_ms and gemm[f"m{m}_us"] < row[f"m{m}_us"]]
+        row["gemm_faster_from_m"] = min(cross) if cross else "none below 33"
         res[name] = row
     return res
 
@@ -389,6 +448,9 @@ def main() -> int:
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the configuration-4 prefill chunk (what the prefill PMC passes read); prints its dict")
     args = ap.parse_args()
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py: --steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this engine runs on one GPU; multi-GPU runs are not part of this build "
               "(see DESIGN.md for how the path would shard)", file=sys.stderr)
@@ -408,7 +470,7 @@ def main() -> int:
     from exl3rocm import synth
     x5120 = torch.from_numpy(synth.activations(synth.key_of("config1", "x", HIDDEN), 1, HIDDEN)).cuda()
     x17408 = torch.from_numpy(synth.activations(synth.key_of("config1", "x", INTER), 1, INTER)).cuda()
-    graphs = capture_steps(torch, sets, x5120, x17408)
+    graphs = capture_steps(torch, sets, x5120, x17408, args.steps)
     log("timing %d decode steps" % args.steps)
     elapsed, wall = time_graphs(torch, graphs, args.steps, args.warmup)
     step_bytes = sum(algo_bytes(1, k, n, bits) for _, k, n in LAYER)
@@ -424,6 +486,13 @@ def main() -> int:
                 "traffic_source": "profiles/gemv_traffic_config1.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
                 "kernel": "gemv_kernel<4,2,0,false> (every M=1 launch of the step)",
                 "bytes_per_launch": step_bytes / lps, "mean_launch_us": round(avg_launch_us, 3)}
+    weights = sum(k * n for _, k, n in LAYER)
+    valu_floor_us = weights * VALU_OPS_PER_WEIGHT_4BPW / VALU_LANE_OPS_PER_S * 1e6
+    roofline["valu_decode_roof"] = {
+        "ops_per_weight": round(VALU_OPS_PER_WEIGHT_4BPW, 3), "weights_per_step": weights,
+        "lane_ops_per_s": VALU_LANE_OPS_PER_S, "floor_us_per_step": round(valu_floor_us, 2),
+        "max_gbs": round(step_bytes / valu_floor_us / 1e3, 1),
+        "frac_of_valu_roof": round(valu_floor_us / (ms_per_step * 1e3), 4)}
     extra = {"launches_per_step": lps, "step_bytes": step_bytes, "wall_s": round(wall, 3)}
     log("per-shape GEMV timing")
     extra["per_shape_m1"] = per_shape_gemv(torch, sets, x5120, x17408)

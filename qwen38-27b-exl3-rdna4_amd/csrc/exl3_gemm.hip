@@ -681,6 +681,9 @@ PcPlan pc_plan(int M, int K, const int* widths, int groups)
     const int full = p.tiles / PC_CUS, tail = p.tiles - full * PC_CUS;
     p.split = 1;
     if (full >= 1 && tail > 0) p.split = std::min(PC_CUS / tail, (K / KSTEP) / 8);
+    // a launch of at most half a wave of tiles (small M: one row tile of few columns, e.g. the
+    // 40 tiles of a 17408 -> 5120 layer) splits every tile, so that the pieces fill the CUs
+    if (full == 0 && 2 * tail <= PC_CUS) p.split = std::min(PC_CUS / tail, (K / KSTEP) / 8);
     if (p.split < 2) p.split = 1;
     p.n_full = p.split > 1 ? full * PC_CUS : p.tiles;
     p.ws_bytes = p.split > 1 ? PC_COUNTER_BYTES + (size_t) (p.tiles - p.n_full) * p.split * PC_PIECE_BYTES : 0;

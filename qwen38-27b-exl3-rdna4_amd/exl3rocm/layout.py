@@ -1,9 +1,11 @@
-"""Checkpoint layout discovery from safetensors headers (no tensor data is read).
+"""Where the EXL3 modules of a checkpoint are and what shape they have, from the safetensors
+headers alone (tensor data is never read here).
 
-Restates the reference's `_norm_key` and `_read_checkpoint_layout`
-(vllm_plugin/exl3rocm/plugin.py:48-79): for every `<module>.trellis` tensor the EXL3 bitrate
-K = shape[-1] // 16 and the layer shape k = shape[0] * 16, n = shape[1] * 16 are recorded
-under a normalized module name shared by checkpoint keys and vLLM prefixes.
+A trellis tensor is (k / 16, n / 16, 16 K) 16-bit words, so its header shape gives the module's
+input width k, output width n and bitrate K.  Checkpoint tensor names and vLLM module prefixes
+spell the same module differently ("model.language_model.layers.3..." against
+"model.layers.3..."); both are reduced to one key.  Same behaviour as the reference's
+`_norm_key` / `_read_checkpoint_layout` (vllm_plugin/exl3rocm/plugin.py:48-79).
 """
 from __future__ import annotations
 
@@ -13,7 +15,8 @@ import os
 import re
 import struct
 
-# vLLM fused module -> checkpoint constituents, in output order (reference plugin.py:38-44)
+# modules vLLM fuses, and the checkpoint modules they hold, in output-column order (the
+# reference plugin's table, plugin.py:38-44: the checkpoint's naming)
 FUSED = {
     "gate_up_proj": ["gate_proj", "up_proj"],
     "qkv_proj": ["q_proj", "k_proj", "v_proj"],
@@ -25,9 +28,8 @@ QKV_IDS = {"q": 0, "k": 1, "v": 2}
 
 
 def norm_key(k: str) -> str:
-    """'model.language_model.layers.3.mlp.gate_proj' -> 'layers.3.mlp.gate_proj';
-    '...mtp.layers.0.x' -> 'mtp.layers.0.x'; '...visual.blocks.0.y' -> 'visual.blocks.0.y';
-    anything else -> its last component (e.g. 'lm_head')."""
+    """The key of a module name: decoder layers from "layers.<i>" on, the MTP head and the vision
+    tower under "mtp." / "visual.", and any other module by its last name component."""
     parts = k.split(".")
     if "visual" in parts:
         return "visual." + ".".join(parts[parts.index("visual") + 1:])
@@ -50,8 +52,8 @@ def read_header(path: str) -> dict:
 
 
 def read_checkpoint_layout(model_dir: str):
-    """({normalized module: (K, k, n)} for every '<module>.trellis' tensor,
-        {tensor name: dtype string}, {tensor name: shape}) over every *.safetensors file."""
+    """Three maps over all *.safetensors files of the directory: module key -> (K, k, n) of each
+    module that has a trellis, and tensor name -> dtype string / shape for every tensor."""
     out, dtypes, shapes = {}, {}, {}
     for f in sorted(glob.glob(os.path.join(model_dir, "*.safetensors"))):
         for name, v in read_header(f).items():
@@ -66,8 +68,9 @@ def read_checkpoint_layout(model_dir: str):
 
 
 def groups_for(modules: dict, prefix: str, vision_qkv_bf16: bool = False):
-    """Checkpoint members of the (possibly fused) module at `prefix` as [(member, K, k, n)], or
-    None when the module is not EXL3 (reference plugin.py:133-147)."""
+    """The checkpoint modules behind vLLM module `prefix` (its FUSED members in output order, or
+    itself) as [(key, K, k, n)]; None when none of them is EXL3, an error when only some are
+    (the reference's Exl3Config._groups_for, plugin.py:133-147)."""
     key = norm_key(prefix)
     if key.endswith(".attn.qkv") and key.startswith("visual.") and vision_qkv_bf16:
         return None

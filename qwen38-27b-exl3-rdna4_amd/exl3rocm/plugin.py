@@ -1,21 +1,36 @@
 """
-vLLM quantization plugin surface for EXL3 weights on MI355X: `Exl3Config` and
-`Exl3LinearMethod` with the reference's create_weights / weight loading /
-process_weights_after_loading / apply contract (vllm_plugin/exl3rocm/plugin.py:82-372).
+vLLM quantization surface for EXL3 weights on MI355X: `Exl3Config` and `Exl3LinearMethod`.
 
-Weights are kept per checkpoint tensor ("group") with that group's own K, trellis, suh and svh,
-because vLLM fuses sibling projections (qkv, gate/up) whose checkpoint tensors may differ in
-bitrate; the fused output is the concatenation of per-group results, computed inside the
-opaque `exl3rocm::linear_groups` op.
+The contract is the reference plugin's (vllm_plugin/exl3rocm/plugin.py:82-372): vLLM calls
+`create_weights`, streams checkpoint tensors through the registered parameters' `weight_loader`
+(with vLLM's shard ids), then `process_weights_after_loading`, then `apply` per forward.
+
+Storage is per checkpoint tensor ("group"): vLLM fuses sibling projections (qkv_proj, gate_up_proj,
+in_proj_qkvz) whose checkpoint tensors may differ in bitrate (the reference checkpoint pairs a 2-bit
+q with 5-bit k / v), so each group keeps its own K, trellis, suh and svh, and the fused output is the
+concatenation of the groups' outputs, computed inside one opaque `exl3rocm::linear_groups` op.
+
+Design here:
+  * a layer's groups are described by their cumulative column offsets; vLLM's output partitions
+    are mapped onto groups by bisection over those offsets (a group may span partitions, never the
+    reverse);
+  * each registered load target carries a `_Router` for one tensor kind, which resolves vLLM's
+    shard id to a group and validates shape and dtype before copying;
+  * the codebook scalar (`mul1` / `mcg`) is a hard contract: the kernels implement exactly one
+    multiplier per codebook, so a checkpoint scalar (or a `quantization_config.json`
+    `mul1_multiplier`) naming another one raises instead of decoding wrong weights.
 
 vLLM is optional: when it is importable the config registers itself as quantization "exl3";
-without it the same classes work on any torch.nn.Module (what the tests drive).
+without it the same classes work on any torch.nn.Module (what the tests and
+`exl3rocm.checkpoint` drive).
 """
 from __future__ import annotations
 
+import bisect
+import json
 import logging
 import os
-from typing import Any
+from typing import Any, Optional
 
 import torch
 from torch.nn import Parameter
@@ -56,29 +71,63 @@ except Exception:  # vLLM absent: plain stand-ins with the same roles
             return cls
         return deco
 
-# mul1 / mcg multipliers the kernels implement (codebook hash constants)
+# The hash multipliers the kernels implement, per codebook (csrc/exl3_device.h Codebook<>): a
+# checkpoint scalar selects its codebook and must name exactly this multiplier.
 CODEBOOK_MULTIPLIERS = {"mul1": 0x83DCD12D, "mcg": 0xCBAC1FED}
+SCALAR_KINDS = tuple(CODEBOOK_MULTIPLIERS)
+TENSOR_KINDS = ("trellis", "suh", "svh")
+
+
+class Exl3FormatError(ValueError):
+    """A checkpoint that the kernels cannot decode as stored (wrong codebook multiplier,
+    inconsistent bitrate)."""
 
 
 def check_codebook_scalar(kind: str, value: int) -> bool:
-    """True when a checkpoint's `mul1` / `mcg` scalar names the multiplier the kernels use (as an
-    unsigned or signed 32-bit integer).  The reference only checks presence (plugin.py:334-335);
-    a mismatch is logged, and the scalar's presence still selects the codebook."""
-    want = CODEBOOK_MULTIPLIERS[kind]
-    ok = (int(value) & 0xFFFFFFFF) == want
-    if not ok:
-        logger.warning("exl3rocm: checkpoint %s scalar %#x differs from the kernel multiplier %#x",
-                       kind, int(value) & 0xFFFFFFFF, want)
-    return ok
+    """True when `value` (as an unsigned or signed 32-bit integer) is the multiplier the kernels
+    implement for codebook `kind`."""
+    return (int(value) & 0xFFFFFFFF) == CODEBOOK_MULTIPLIERS[kind]
+
+
+def require_codebook_scalar(kind: str, value: int, where: str = "") -> int:
+    """The scalar as an unsigned 32-bit multiplier; raises Exl3FormatError when it is not the
+    kernels' (the reference only checks that the scalar is present, plugin.py:334-335)."""
+    v = int(value) & 0xFFFFFFFF
+    if v != CODEBOOK_MULTIPLIERS[kind]:
+        raise Exl3FormatError(f"exl3rocm: {where or kind} multiplier {v:#010x} is not the {kind} codebook's "
+                              f"{CODEBOOK_MULTIPLIERS[kind]:#010x}; the kernels cannot decode these weights")
+    return v
+
+
+def read_quantization_config(model_dir: str) -> dict:
+    """{normalized module: {"bits": int | None, "mul1_multiplier": int | None}} from the
+    checkpoint's quantization_config.json `tensor_storage` (the fields the reference's
+    tools/build_shape_manifest.py:69-105 reads); {} when the file is absent."""
+    path = os.path.join(model_dir, "quantization_config.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        q = json.load(f)
+    out = {}
+    for name, entry in (q.get("tensor_storage") or {}).items():
+        if entry.get("bits_per_weight") is None:
+            continue                                   # not an EXL3 module (norms, embeddings)
+        out[layout.norm_key(name)] = {"bits": int(entry["bits_per_weight"]),
+                                      "mul1_multiplier": entry.get("mul1_multiplier")}
+    return out
 
 
 @register_quantization_config("exl3")
 class Exl3Config(QuantizationConfig):
+    """Checkpoint-wide EXL3 settings: the codebook and, after maybe_update_config, every EXL3
+    module's (K, k, n) from the safetensors headers (validated against quantization_config.json
+    where the checkpoint has one)."""
 
     def __init__(self, codebook: str = "mul1"):
         super().__init__()
         self.codebook = codebook
         self.modules: dict[str, tuple[int, int, int]] = {}
+        self.multipliers: dict[str, int] = {}
 
     def __repr__(self):
         return f"Exl3Config(codebook={self.codebook}, modules={len(self.modules)})"
@@ -105,24 +154,92 @@ class Exl3Config(QuantizationConfig):
         if not os.path.isdir(model_name):
             raise NotImplementedError("exl3rocm: pass a local checkpoint directory")
         self.modules, _, _ = layout.read_checkpoint_layout(model_name)
+        for key, meta in read_quantization_config(model_name).items():
+            K = self.modules.get(key, (None,))[0]
+            if K is not None and meta["bits"] is not None and meta["bits"] != K:
+                raise Exl3FormatError(f"exl3rocm: {key}: quantization_config.json says {meta['bits']} bits, "
+                                      f"its trellis holds {K}")
+            if meta["mul1_multiplier"] is not None:
+                self.multipliers[key] = require_codebook_scalar("mul1", meta["mul1_multiplier"], key)
         logger.info("exl3rocm: %d EXL3 modules", len(self.modules))
 
     def _groups_for(self, prefix: str):
         return layout.groups_for(self.modules, prefix, os.environ.get("EXL3_VISION_QKV_BF16") == "1")
 
     def get_quant_method(self, layer: torch.nn.Module, prefix: str):
-        if isinstance(layer, (LinearBase, ParallelLMHead)):
-            groups = self._groups_for(prefix)
-            if groups is None:
-                return UnquantizedLinearMethod() if isinstance(layer, LinearBase) else None
+        if not isinstance(layer, (LinearBase, ParallelLMHead)):
+            return None
+        groups = self._groups_for(prefix)
+        if groups is not None:
             return Exl3LinearMethod(self, groups)
-        return None
+        return UnquantizedLinearMethod() if isinstance(layer, LinearBase) else None
+
+
+def _partition_groups(parts: list, widths: list) -> list:
+    """Group index of every output partition.  Group boundaries are the cumulative widths; every
+    group boundary must also end a partition, and each partition must lie inside one group."""
+    ends = [0]
+    for w in widths:
+        ends.append(ends[-1] + w)
+    starts, off = [], 0
+    for p in parts:
+        starts.append(off)
+        off += p
+    tiled = off == ends[-1] and all(e in set(starts) | {off} for e in ends)
+    assert tiled, f"exl3rocm: partitions {parts} do not tile groups {widths}"
+    return [bisect.bisect_right(ends, s) - 1 for s in starts]
+
+
+def _shard_group(layer, shard_id) -> int:
+    """The group a checkpoint tensor loads into, from vLLM's shard id: None (unfused module),
+    "q" / "k" / "v", a partition index, or a tuple of partition indices (all in one group)."""
+    groups = layer.exl3_part_to_group
+    if shard_id is None:
+        assert len(layer.exl3_n) == 1, "exl3rocm: unsharded load into fused module"
+        return 0
+    if isinstance(shard_id, str):
+        idx = [QKV_IDS[shard_id]]
+    elif isinstance(shard_id, int):
+        idx = [shard_id]
+    else:
+        idx = list(shard_id)
+    found = {groups[i] for i in idx}
+    assert len(found) == 1, f"exl3rocm: shard {shard_id} spans groups {found}"
+    return next(iter(found))
+
+
+class _Router:
+    """weight_loader of one load target: routes a checkpoint tensor of kind `kind` into its
+    group's buffer (or records the codebook scalar)."""
+
+    def __init__(self, layer, kind: str, expected_multiplier: Optional[int]):
+        self.layer = layer
+        self.kind = kind
+        self.expected = expected_multiplier
+
+    def __call__(self, param, w, shard_id=None, *args, **kwargs):
+        layer = self.layer
+        g = _shard_group(layer, getattr(w, "exl3_shard", None) if shard_id is None else shard_id)
+        if self.kind in SCALAR_KINDS:
+            v = require_codebook_scalar(self.kind, int(w.item()), f"{self.kind} of group {g}")
+            if self.expected is not None and v != self.expected:
+                raise Exl3FormatError(f"exl3rocm: {self.kind} scalar {v:#010x} differs from the checkpoint's "
+                                      f"quantization_config {self.expected:#010x}")
+            seen = getattr(layer, f"exl3_{self.kind}")
+            assert seen is None or seen == v, f"exl3rocm: {self.kind} differs across groups"
+            setattr(layer, f"exl3_{self.kind}", v)
+        else:
+            dst = getattr(layer, f"exl3_{self.kind}_{g}")
+            assert tuple(w.shape) == tuple(dst.shape), \
+                f"exl3rocm: {self.kind} shape {tuple(w.shape)} vs {tuple(dst.shape)} (group {g})"
+            dst.copy_(w)
+        layer.exl3_loaded.add((self.kind, g))
 
 
 class Exl3LinearMethod(LinearMethodBase):
-    """Per-group EXL3 storage.  The registered Parameters `trellis`, `suh`, `svh`, `mul1`|`mcg`
-    are 0-size load targets; their weight_loader routes each checkpoint tensor into that group's
-    non-persistent buffers."""
+    """EXL3 linear over per-group buffers `exl3_{trellis,suh,svh}_{i}` (non-persistent).  The
+    registered Parameters `trellis`, `suh`, `svh` and the codebook scalar are 0-size load targets
+    whose weight_loader fills those buffers."""
 
     def __init__(self, config: Exl3Config, groups):
         self.config = config
@@ -133,124 +250,74 @@ class Exl3LinearMethod(LinearMethodBase):
         k = input_size_per_partition
         if k != input_size:
             raise NotImplementedError("exl3rocm: tensor parallelism is not supported")
-        parts = list(output_partition_sizes)
-        # map output partitions onto checkpoint groups (a group may span partitions)
-        group_n = [g[3] for g in self.groups]
-        part_to_group, gi, acc = [], 0, 0
-        for p in parts:
-            assert gi < len(group_n), f"exl3rocm: partitions {parts} do not tile groups {group_n}"
-            part_to_group.append(gi)
-            acc += p
-            assert acc <= group_n[gi], f"exl3rocm: partitions {parts} do not tile groups {group_n}"
-            if acc == group_n[gi]:
-                gi, acc = gi + 1, 0
-        assert gi == len(group_n), f"exl3rocm: partitions {parts} do not tile groups {group_n}"
-        layer.exl3_part_to_group = part_to_group
-        layer.exl3_K = [g[1] for g in self.groups]
-        layer.exl3_n = [g[3] for g in self.groups]
-        for i, (_, K, gk, n) in enumerate(self.groups):
-            assert gk == k, f"exl3rocm: {self.groups[i][0]} k={gk} vs layer k={k}"
-            layer.register_buffer(f"exl3_trellis_{i}", torch.empty((k // 16, n // 16, 16 * K), dtype=torch.int16),
-                                  persistent=False)
-            layer.register_buffer(f"exl3_suh_{i}", torch.empty((k,), dtype=torch.float16), persistent=False)
-            layer.register_buffer(f"exl3_svh_{i}", torch.empty((n,), dtype=torch.float16), persistent=False)
+        keys = [g[0] for g in self.groups]
+        Ks = [g[1] for g in self.groups]
+        widths = [g[3] for g in self.groups]
+        for key, gk in zip(keys, (g[2] for g in self.groups)):
+            assert gk == k, f"exl3rocm: {key} k={gk} vs layer k={k}"
+        layer.exl3_part_to_group = _partition_groups(list(output_partition_sizes), widths)
+        layer.exl3_K, layer.exl3_n = Ks, widths
+        for i, (K, n) in enumerate(zip(Ks, widths)):
+            shapes = {"trellis": ((k // 16, n // 16, 16 * K), torch.int16), "suh": ((k,), torch.float16),
+                      "svh": ((n,), torch.float16)}
+            for kind, (shape, dt) in shapes.items():
+                layer.register_buffer(f"exl3_{kind}_{i}", torch.empty(shape, dtype=dt), persistent=False)
         layer.exl3_loaded = set()
-        layer.exl3_mul1 = None
-        layer.exl3_mcg = None
-
-        def reg(name, loader):
-            p = Parameter(torch.empty(0, dtype=torch.int8), requires_grad=False)
-            p.weight_loader = loader
-            layer.register_parameter(name, p)
-
-        reg("trellis", self._loader(layer, "trellis"))
-        reg("suh", self._loader(layer, "suh"))
-        reg("svh", self._loader(layer, "svh"))
-        if self.config.codebook in ("mul1", "mcg"):
-            reg(self.config.codebook, self._loader(layer, self.config.codebook))
+        layer.exl3_mul1 = layer.exl3_mcg = None
+        # the checkpoint's quantization_config multiplier, when every group names the same one
+        known = {self.config.multipliers.get(key) for key in keys}
+        expected = known.pop() if len(known) == 1 else None
+        # load targets: the tensor kinds, and only the codebook scalar the checkpoint stores
+        # (vLLM rejects registered parameters that are never loaded)
+        kinds = TENSOR_KINDS + ((self.config.codebook,) if self.config.codebook in SCALAR_KINDS else ())
+        for kind in kinds:
+            target = Parameter(torch.empty(0, dtype=torch.int8), requires_grad=False)
+            target.weight_loader = _Router(layer, kind, expected if kind == "mul1" else None)
+            layer.register_parameter(kind, target)
 
     @staticmethod
     def _group_of(layer, shard_id) -> int:
-        if shard_id is None:
-            assert len(layer.exl3_n) == 1, "exl3rocm: unsharded load into fused module"
-            return 0
-        if isinstance(shard_id, str):
-            parts = [QKV_IDS[shard_id]]
-        elif isinstance(shard_id, int):
-            parts = [shard_id]
-        else:
-            parts = list(shard_id)
-        gs = {layer.exl3_part_to_group[p] for p in parts}
-        assert len(gs) == 1, f"exl3rocm: shard {shard_id} spans groups {gs}"
-        return gs.pop()
-
-    def _loader(self, layer, kind):
-        def load(param, w, shard_id=None, *args, **kwargs):
-            if shard_id is None:
-                shard_id = getattr(w, "exl3_shard", None)
-            g = self._group_of(layer, shard_id)
-            if kind in ("mul1", "mcg"):
-                val = int(w.item())
-                prev = getattr(layer, f"exl3_{kind}")
-                assert prev is None or prev == val, f"exl3rocm: {kind} differs across groups"
-                setattr(layer, f"exl3_{kind}", val)
-            else:
-                buf = getattr(layer, f"exl3_{kind}_{g}")
-                assert tuple(w.shape) == tuple(buf.shape), \
-                    f"exl3rocm: {kind} shape {tuple(w.shape)} vs {tuple(buf.shape)} (group {g})"
-                buf.copy_(w)
-            layer.exl3_loaded.add((kind, g))
-        return load
+        return _shard_group(layer, shard_id)
 
     def process_weights_after_loading(self, layer):
         ng = len(layer.exl3_n)
-        missing = [(k, g) for k in ("trellis", "suh", "svh") for g in range(ng) if (k, g) not in layer.exl3_loaded]
+        missing = sorted({(kind, g) for kind in TENSOR_KINDS for g in range(ng)} - layer.exl3_loaded)
         assert not missing, f"exl3rocm: missing tensors {missing}"
         layer.exl3_is_mul1 = layer.exl3_mul1 is not None
         layer.exl3_is_mcg = layer.exl3_mcg is not None
-        for kind in ("mul1", "mcg"):
-            if getattr(layer, f"exl3_{kind}") is not None:
-                check_codebook_scalar(kind, getattr(layer, f"exl3_{kind}"))
-        k = layer.exl3_trellis_0.shape[0] * 16
         dev = layer.exl3_trellis_0.device
         if dev.type == "cuda":
-            # reserve everything the forward needs now, so graph capture never allocates
+            # every buffer the forward uses is reserved now, so graph capture never allocates
             from . import ops
+            k = layer.exl3_trellis_0.shape[0] * 16
             for K, n in zip(layer.exl3_K, layer.exl3_n):
                 ops.reserve_workspace(dev, k, n, K, groups=min(ng, 4))
             if ops.PREFILL_ROUTE == "recon":
-                ops.reserve_weight_buffer(dev, max(k * min(n, ops.RECON_SLICE_N) for n in layer.exl3_n))
-        # grouped M == 1 path over pointer tables for modules whose groups share K and width
+                ops.reserve_weight_buffer(dev, k * min(max(layer.exl3_n), ops.RECON_SLICE_N))
+        # equal-K, equal-width groups (gate/up) take the pointer-table launch at M == 1
         layer.exl3_mgemm_ptrs = None
-        if 1 < ng <= 4 and len(set(layer.exl3_K)) == 1 and len(set(layer.exl3_n)) == 1 \
-                and os.environ.get("EXL3_MGEMM", "1") != "0":
-            def ptrs(kind):
+        same_shape = len(set(layer.exl3_K)) == 1 and len(set(layer.exl3_n)) == 1
+        if 1 < ng <= 4 and same_shape and os.environ.get("EXL3_MGEMM", "1") != "0":
+            tables = []
+            for kind in TENSOR_KINDS:
                 t = torch.tensor([getattr(layer, f"exl3_{kind}_{i}").data_ptr() for i in range(ng)],
                                  dtype=torch.long, device=dev)
                 layer.register_buffer(f"exl3_ptrs_{kind}", t, persistent=False)
-                return t
-            layer.exl3_mgemm_ptrs = [ptrs("trellis"), ptrs("suh"), ptrs("svh")]
-        # drop the 0-size load targets so nothing downstream mistakes them for weights
-        for name in ("trellis", "suh", "svh", "mul1", "mcg"):
-            if name in layer._parameters:
-                del layer._parameters[name]
+                tables.append(t)
+            layer.exl3_mgemm_ptrs = tables
+        # the 0-size load targets are done: nothing downstream should take them for weights
+        for name in TENSOR_KINDS + SCALAR_KINDS:
+            layer._parameters.pop(name, None)
 
     def apply(self, layer, x, bias=None):
         from . import ops  # noqa: F401  (registers the custom ops)
         ng = len(layer.exl3_n)
-        # one opaque op per module: never concatenate per-group outputs in traced code
-        y = torch.ops.exl3rocm.linear_groups(
-            x,
-            [getattr(layer, f"exl3_trellis_{i}") for i in range(ng)],
-            [getattr(layer, f"exl3_suh_{i}") for i in range(ng)],
-            [getattr(layer, f"exl3_svh_{i}") for i in range(ng)],
-            list(layer.exl3_K), layer.exl3_is_mcg, layer.exl3_is_mul1,
-            *(layer.exl3_mgemm_ptrs or (None, None, None)))
-        if y.dtype != x.dtype:
-            y = y.to(x.dtype)
-        if bias is not None:
-            y = y + bias
-        return y
+        per = [[getattr(layer, f"exl3_{kind}_{i}") for i in range(ng)] for kind in TENSOR_KINDS]
+        # one opaque op per module: the groups' outputs are concatenated inside it
+        y = torch.ops.exl3rocm.linear_groups(x, *per, list(layer.exl3_K), layer.exl3_is_mcg, layer.exl3_is_mul1,
+                                             *(layer.exl3_mgemm_ptrs or (None, None, None)))
+        y = y if y.dtype == x.dtype else y.to(x.dtype)
+        return y if bias is None else y + bias
 
     def embedding(self, layer, input_):
         raise NotImplementedError("exl3rocm: quantized input embeddings are not supported")

@@ -119,6 +119,28 @@ def test_config4_grouped_gate_up():
         assert_close(y[rows, g * n:(g + 1) * n].cpu().numpy(), cpu.linear(x[rows], tr, bits, su, sv, 2), ("gu", g))
 
 
+@pytest.mark.parametrize("name,m,k,n", [("down", 64, 17408, 5120), ("o", 40, 5120, 5120), ("qkv-k", 200, 5120, 1024)])
+def test_small_m_prefill_splits_every_tile(name, m, k, n):
+    """M in (32, 256]: one row tile of few column tiles (down: 40) is split along K into pieces
+    (down: 6 of ~45 steps) so the launch fills the CUs.  Oracle on rows spread over the tile,
+    repeatable bitwise, and equal to the unsplit reference entry point to the parity bar."""
+    bits = 4
+    tr, su, sv = synth.layer("smallm", name, k, n, bits)
+    x = synth.activations(synth.key_of("smallm", name, "x"), m, k)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    assert plan(m, k, [n]) > 0
+    print(f"small-M split {name}: m={m} k={k} n={n}", flush=True)
+    y = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, False, True)
+    y2 = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, False, True)
+    y0 = torch.empty_like(y)
+    E.exl3_gemm_trellis(X, T, y0, SU, torch.empty_like(X), SV, bits, False, True)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+    assert_close(y.cpu().numpy(), y0.cpu().numpy(), "split vs unsplit")
+    rows = sorted({0, 1, m // 2, m - 1})
+    assert_close(y[rows].cpu().numpy(), cpu.linear(x[rows], tr, bits, su, sv, 2), f"{name} vs oracle")
+
+
 # ---------------------------------------------------------------------------------- config 3
 @pytest.mark.parametrize("k,n", [(5120, 17408), (17408, 5120)])
 def test_config3_heavy_tail_m16_m32(k, n):
@@ -198,7 +220,7 @@ def test_recon_prefill_route_through_the_op(monkeypatch):
     """EXL3_PREFILL=recon (the reference's reconstruct + hgemm_recon route, ops.py:86-97) through
     exl3rocm::linear and linear_groups: bitwise equal to the fused route (same MFMA order; the
     layer is small enough that the fused launch has no split tail), and within the bar of the oracle."""
-    k, m = 1024, 96
+    k, m = 512, 96                      # K too short for a split launch: the same summation order
     widths = (512, 384)
     mats = [synth.layer("recon-op", i, k, n, 4) for i, n in enumerate(widths)]
     x = synth.activations(synth.key_of("recon-op", "x"), m, k)
@@ -254,3 +276,22 @@ def test_serving_sequence_captures_without_manual_reserve():
         assert torch.equal(y8.view(torch.int16), eager8.view(torch.int16))
         method.apply(lay, X)                              # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_layer_loaded_from_a_checkpoint_file_vs_oracle(tmp_path):
+    """A real safetensors checkpoint (tensor data + quantization_config.json) loaded through
+    exl3rocm.checkpoint onto the GPU: the fused q/k/v module (2 / 5 / 5 bpw) at M = 1 and 40
+    against the oracle on the same file data."""
+    from exl3rocm import checkpoint
+    from test_host import QKV, _qconfig, write_exl3_checkpoint
+    data = write_exl3_checkpoint(tmp_path, QKV, qconfig=_qconfig(QKV))
+    method, lay = checkpoint.load_linear(str(tmp_path), "model.layers.0.self_attn.qkv_proj", device=DEV)
+    x = synth.activations(synth.key_of("ckpt", "x"), 40, 256)
+    X = to_dev(x)[0]
+    ref = np.concatenate([cpu.linear(x, tr.view(np.uint16), K, su, sv, 2)
+                          for (K, _, _), (tr, su, sv) in zip(QKV.values(), data.values())], axis=1)
+    y1 = method.apply(lay, X[:1])
+    y40 = method.apply(lay, X)
+    torch.cuda.synchronize()
+    assert_close(y1.cpu().numpy(), ref[:1], "file M=1", strict=True)
+    assert_close(y40.cpu().numpy(), ref, "file M=40")

@@ -113,8 +113,8 @@ def test_create_weights_and_loading():
     assert torch.equal(layer.exl3_trellis_2, tr)
     with pytest.raises(AssertionError):
         layer.trellis.weight_loader(layer.trellis, torch.zeros(1, dtype=torch.int16), "q")
-    with pytest.raises(AssertionError):
-        layer.mul1.weight_loader(layer.mul1, torch.tensor(7), "k")             # differs across groups
+    with pytest.raises(plugin.Exl3FormatError):
+        layer.mul1.weight_loader(layer.mul1, torch.tensor(7), "k")             # not the kernels' multiplier
     method.process_weights_after_loading(layer)
     assert layer.exl3_is_mul1 and not layer.exl3_is_mcg
     assert "trellis" not in layer._parameters and "mul1" not in layer._parameters
@@ -150,6 +150,96 @@ def test_codebook_scalar_check():
     assert plugin.check_codebook_scalar("mul1", 0x83DCD12D)
     assert plugin.check_codebook_scalar("mul1", 0x83DCD12D - (1 << 32))
     assert not plugin.check_codebook_scalar("mcg", 0x83DCD12D)
+    assert plugin.require_codebook_scalar("mcg", 0xCBAC1FED - (1 << 32)) == 0xCBAC1FED
+    with pytest.raises(plugin.Exl3FormatError, match="0x83dcd12d"):
+        plugin.require_codebook_scalar("mul1", 0x83DCD12C)
+
+
+def test_partition_mapping_by_offsets():
+    assert plugin._partition_groups([128, 128], [256]) == [0, 0]
+    assert plugin._partition_groups([5120, 1024, 1024], [5120, 1024, 1024]) == [0, 1, 2]
+    assert plugin._partition_groups([128, 256, 128, 128], [384, 256]) == [0, 0, 1, 1]
+    for parts, widths in (([512], [384, 128]), ([256, 256], [384, 128]), ([200], [256]), ([128], [128, 128])):
+        with pytest.raises(AssertionError):
+            plugin._partition_groups(parts, widths)
+
+
+# ---------------------------------------------------------------------------------------------
+# real checkpoint files: safetensors with tensor data, and quantization_config.json
+# ---------------------------------------------------------------------------------------------
+def write_exl3_checkpoint(path, modules: dict, mul1=0x83DCD12D, qconfig=None):
+    """modules: {checkpoint module name: (K, k, n)} -> one safetensors file with seeded trellis /
+    suh / svh data and a mul1 scalar per module; returns {module: (trellis, suh, svh)}."""
+    from safetensors.torch import save_file
+    rng = np.random.default_rng(11)
+    tensors, data = {}, {}
+    for name, (K, k, n) in modules.items():
+        tr = rng.integers(-32768, 32768, (k // 16, n // 16, 16 * K), dtype=np.int16)
+        su = rng.standard_normal(k).astype(np.float16)
+        sv = rng.standard_normal(n).astype(np.float16)
+        tensors[f"{name}.trellis"] = torch.from_numpy(tr)
+        tensors[f"{name}.suh"] = torch.from_numpy(su)
+        tensors[f"{name}.svh"] = torch.from_numpy(sv)
+        tensors[f"{name}.mul1"] = torch.tensor(mul1 - (1 << 32) if mul1 >= (1 << 31) else mul1, dtype=torch.int32)
+        data[name] = (tr, su, sv)
+    save_file(tensors, str(path / "model-00001-of-00001.safetensors"))
+    if qconfig is not None:
+        with open(path / "quantization_config.json", "w") as f:
+            json.dump(qconfig, f)
+    return data
+
+
+QKV = {"model.language_model.layers.0.self_attn.q_proj": (2, 256, 256),
+       "model.language_model.layers.0.self_attn.k_proj": (5, 256, 128),
+       "model.language_model.layers.0.self_attn.v_proj": (5, 256, 128)}
+
+
+def _qconfig(modules, mul1=0x83DCD12D, bits=None):
+    return {"codebook": "mul1", "tensor_storage": {
+        name: {"bits_per_weight": bits or K, "quant_format": "exl3", "mul1_multiplier": mul1,
+               "stored_tensors": {f"{name}.trellis": {"shape": [k // 16, n // 16, 16 * K], "dtype": "int16"}}}
+        for name, (K, k, n) in modules.items()} | {"model.norm": {"stored_tensors": {}}}}
+
+
+def test_load_linear_from_real_safetensors(tmp_path):
+    from exl3rocm import checkpoint
+    data = write_exl3_checkpoint(tmp_path, QKV, qconfig=_qconfig(QKV))
+    method, layer = checkpoint.load_linear(str(tmp_path), "model.layers.0.self_attn.qkv_proj", device="cpu")
+    assert layer.exl3_K == [2, 5, 5] and layer.exl3_n == [256, 128, 128]
+    assert layer.exl3_is_mul1 and layer.exl3_mul1 == 0x83DCD12D
+    for i, name in enumerate(QKV):
+        tr, su, sv = data[name]
+        assert np.array_equal(getattr(layer, f"exl3_trellis_{i}").numpy(), tr)
+        assert np.array_equal(getattr(layer, f"exl3_suh_{i}").numpy().view(np.uint16), su.view(np.uint16))
+        assert np.array_equal(getattr(layer, f"exl3_svh_{i}").numpy().view(np.uint16), sv.view(np.uint16))
+    assert "trellis" not in layer._parameters
+    with pytest.raises(KeyError):
+        checkpoint.load_linear(str(tmp_path), "model.layers.0.mlp.gate_up_proj", device="cpu")
+
+
+def test_wrong_multiplier_in_the_file_is_refused(tmp_path):
+    from exl3rocm import checkpoint
+    write_exl3_checkpoint(tmp_path, QKV, mul1=0x83DCD12D ^ 0x100)
+    with pytest.raises(plugin.Exl3FormatError):
+        checkpoint.load_linear(str(tmp_path), "model.layers.0.self_attn.qkv_proj", device="cpu")
+
+
+def test_quantization_config_is_a_contract(tmp_path):
+    write_exl3_checkpoint(tmp_path, QKV, qconfig=_qconfig(QKV))
+    cfg = plugin.Exl3Config()
+    cfg.maybe_update_config(str(tmp_path))
+    assert set(cfg.multipliers.values()) == {0x83DCD12D} and len(cfg.multipliers) == 3
+    for bad in (_qconfig(QKV, mul1=0x12345678), _qconfig(QKV, bits=3)):
+        with open(tmp_path / "quantization_config.json", "w") as f:
+            json.dump(bad, f)
+        with pytest.raises(plugin.Exl3FormatError):
+            plugin.Exl3Config().maybe_update_config(str(tmp_path))
+    # a scalar in the weights that disagrees with the config's multiplier is refused at load time
+    cfg.multipliers = {k: 0x83DCD12D for k in cfg.multipliers}
+    method = plugin.Exl3LinearMethod(cfg, cfg._groups_for("model.layers.0.self_attn.qkv_proj"))
+    layer = torch.nn.Module()
+    method.create_weights(layer, 256, [256, 128, 128], 256, 512, torch.float16)
+    assert layer.mul1.weight_loader.expected == 0x83DCD12D
 
 
 def test_fake_impls_shapes():
@@ -169,3 +259,17 @@ def test_cpu_tensors_fail_loudly():
     s = torch.ones(128, dtype=torch.float16)
     with pytest.raises(RuntimeError, match="GPU"):
         torch.ops.exl3rocm.linear(x, tr, s, s, 4, False, True)
+
+
+def test_vllm_entry_point_is_declared():
+    """The package declares the vLLM general-plugin entry point, and it names a callable that
+    registers the custom ops (the reference's vllm_plugin/pyproject.toml:12-13)."""
+    import importlib
+    import tomli
+    pkg = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "qwen38-27b-exl3-rdna4_amd")
+    with open(os.path.join(pkg, "pyproject.toml"), "rb") as f:
+        meta = tomli.load(f)
+    target = meta["project"]["entry-points"]["vllm.general_plugins"]["exl3rocm"]
+    mod, fn = target.split(":")
+    assert callable(getattr(importlib.import_module(mod), fn))
+    assert "libexl3_mi355x.so" in meta["tool"]["setuptools"]["package-data"]["exl3rocm"]

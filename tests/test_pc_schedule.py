@@ -114,6 +114,8 @@ def pc_steps_of_plan(M, K, widths):
     full, tail = divmod(tiles, 256)
     all_steps = K // 64
     split = min(256 // tail, all_steps // 8) if full >= 1 and tail > 0 else 1
+    if full == 0 and 2 * tail <= 256:
+        split = min(256 // tail, all_steps // 8)
     if split < 2:
         split = 1
     out = {all_steps}
@@ -170,7 +172,8 @@ def test_schedule_model_flags_a_two_stage_ring():
 
 def test_plans_produce_only_modelled_step_counts():
     shapes = [(2048, 5120, [5120]), (2048, 17408, [5120]), (2048, 5120, [17408, 17408]),
-              (2048, 5120, [5120, 1024, 1024]), (600, 256, [384]), (256, 1024, [128] * 4), (33, 128, [128])]
+              (2048, 5120, [5120, 1024, 1024]), (600, 256, [384]), (256, 1024, [128] * 4), (33, 128, [128]),
+              (64, 17408, [5120]), (40, 5120, [5120]), (96, 1024, [512, 384])]
     for M, K, widths in shapes:
         for st in pc_steps_of_plan(M, K, widths):
             assert st >= 2, (M, K, widths, st)
