@@ -65,10 +65,21 @@ int exl3_reconstruct_slice(void* W, int64_t ldw, const void* trellis, int k, int
                            int n_out, void* stream);
 
 /* Blockwise 128-point Hadamard over rows: out = fp16(H128(in [* pre]) * r * scale) [* post],
- * r = 0.088388347648; pre / post may be NULL; in == out is allowed.
+ * r = 0.088388347648; pre / post may be NULL; in == out is allowed.  float64 butterflies: exact
+ * (bit-equal to the oracle's float64 product) unless a 128-block spans more than 35 binades.
  * Replaces `had_r_128(in, out, pre, post, scale)` (reference ops.py:88,97). */
 int exl3_had_r_128(const void* in, int64_t ld_in, void* out, int64_t ld_out, int rows, int cols, const void* pre,
                    const void* post, float scale, void* stream);
+
+/* The same transform with float32 butterflies: the values the prefill GEMM uses for its input and
+ * output transforms (every lane layout of it gives these values bitwise), which can differ from
+ * exl3_had_r_128's exact float64 result in the last fp16 place.  (The fused GEMV's transforms are
+ * float64, exl3_had_r_128's values.)
+ * No counterpart of its own in the reference (whose had_r_128 serves both roles, ops.py:88,97).
+ * Callers: exl3rocm's reconstruct + hgemm_recon prefill route, so that it stays bitwise equal to
+ * the fused prefill route. */
+int exl3_had_r_128_f32(const void* in, int64_t ld_in, void* out, int64_t ld_out, int rows, int cols, const void* pre,
+                       const void* post, float scale, void* stream);
 
 /* Workgroups per group of the fused GEMV's stream-K grid for a (k, n) layer launched with
  * `groups` groups (diagnostic; a function of the shape only, never of m). */

@@ -3,7 +3,7 @@
 //  * q-block trellis decoder: one lane turns the 32 consecutive ring positions of a tile's
 //    "q-block" (positions 32q .. 32q+31 == tile columns q and q+8, all 16 rows) into 16 packed
 //    fp16 pairs, specialised per bitrate at compile time (window extraction plan, codebook).
-//  * wave64 128-point Hadamard (2 elements per lane, float64 butterflies: exact for fp16 data).
+//  * wave64 128-point Hadamard in three lane layouts, float32 or float64 butterflies.
 //  * float64 -> fp16 round-to-nearest-even.
 //
 // Format facts restated from the reference oracle (reference/exl3_oracle.py):
@@ -48,8 +48,7 @@ __device__ __forceinline__ __attribute__((address_space(1))) T* as_global(T* p)
 }
 
 // ------------------------------------------------------------------------------------------
-// float64 -> fp16 bits, round to nearest even (exact single rounding; used by the Hadamards,
-// whose float64 butterflies are exact on fp16 data, so the result equals the oracle's).
+// float64 -> fp16 bits, round to nearest even (exact single rounding).
 // ------------------------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t f64_to_f16_bits(double v)
 {
@@ -88,19 +87,34 @@ __device__ __forceinline__ f16 f64_to_f16_rto(double v)
 }
 
 // ------------------------------------------------------------------------------------------
-// 128-point Hadamard, 16 lanes per block: lane r = lane & 15 holds elements 8r .. 8r+7, so a
-// wave transforms 4 blocks at once.  Natural-order Sylvester H[i,j] = (-1)^popcount(i&j):
-// element bits 0..2 are butterflies inside the lane, bits 3..6 are lane xor 1, 2, 4, 8 within
-// a 16-lane row, done with DPP moves (quad_perm, row_half_mirror, row_ror).  float64 sums of
-// fp16 data are exact, so the result does not depend on the butterfly order.
+// 128-point Hadamard.  Natural-order Sylvester H[i,j] = (-1)^popcount(i&j), computed as seven
+// butterfly stages over the element-index bits 0, 1, ..., 6 in that order; each stage maps the
+// pair (a, b) of elements differing in that bit to (a + b, a - b).  The stages run inside a lane
+// or across lanes (DPP, ds_swizzle, v_permlane32_swap) depending on the layout, but every layout
+// performs the same additions in the same order, so all layouts give identical results for a
+// given element type T:
+//   T = double: exact whenever a block's nonzero values span at most 35 binades (53-bit sums of
+//               128 fp16 values: 35 + 11 mantissa + 7 carry bits), and then bit-exact to the
+//               oracle's float64 matrix product; fp16 spans 40 binades, so an adversarial block
+//               can still round differently.
+//               Used where exactness is the contract (the exl3_had_r_128 entry point).
+//   T = float:  24-bit sums, one rounding per stage; the fp16 result can differ from the exact one
+//               in the last place.  Half the VALU cycles and half the lane moves of double; used by
+//               the GEMV and prefill transforms, whose outputs are checked to the rel-L2 bar.
 // ------------------------------------------------------------------------------------------
 template <int CTRL>
-__device__ __forceinline__ double dpp_f64(double x)
+__device__ __forceinline__ double dpp_x(double x)
 {
     const uint64_t u = (uint64_t) __double_as_longlong(x);
     const uint32_t lo = (uint32_t) __builtin_amdgcn_mov_dpp((int) (uint32_t) u, CTRL, 0xF, 0xF, true);
     const uint32_t hi = (uint32_t) __builtin_amdgcn_mov_dpp((int) (uint32_t) (u >> 32), CTRL, 0xF, 0xF, true);
     return __longlong_as_double((long long) (((uint64_t) hi << 32) | lo));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_x(float x)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
 constexpr int DPP_QP_XOR1 = 0xB1;     // quad_perm [1,0,3,2]
@@ -109,119 +123,8 @@ constexpr int DPP_QP_REV = 0x1B;      // quad_perm [3,2,1,0]   (lane ^ 3)
 constexpr int DPP_HALF_MIRROR = 0x141; // lane ^ 7 within 8
 constexpr int DPP_ROR8 = 0x128;       // row_ror:8 == lane ^ 8 within 16
 
-// one cross-lane butterfly stage: lower lane a + b, upper lane a - b (fma with +-1 is exact
-// up to the single rounding of the sum, as the separate add / subtract would be)
-__device__ __forceinline__ void had_stage(double (&v)[8], const double (&p)[8], bool upper)
-{
-    const double s = upper ? -1.0 : 1.0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = __builtin_fma(s, v[i], p[i]);
-}
-
-__device__ __forceinline__ void wht128_x8(double (&v)[8])
-{
-#pragma unroll
-    for (int h = 1; h < 8; h <<= 1)
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if (!(i & h)) {
-                const double a = v[i], b = v[i + h];
-                v[i] = a + b;
-                v[i + h] = a - b;
-            }
-    const int r = __lane_id() & 15;
-    double p[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) p[i] = dpp_f64<DPP_QP_XOR1>(v[i]);
-    had_stage(v, p, r & 1);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) p[i] = dpp_f64<DPP_QP_XOR2>(v[i]);
-    had_stage(v, p, r & 2);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) p[i] = dpp_f64<DPP_QP_REV>(dpp_f64<DPP_HALF_MIRROR>(v[i]));
-    had_stage(v, p, r & 4);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) p[i] = dpp_f64<DPP_ROR8>(v[i]);
-    had_stage(v, p, r & 8);
-}
-
-// 8 fp16 in (16 B) -> 8 fp16 out: fp16(Had128(in [* pre]) * scale) [* post]; pre / post are the
-// matching 8 scale values (ignored when has_pre / has_post are false).  Each fp16 product is a
-// single rounding (packed fp16 multiplies), as in the reference kernels' hmul2 stages.
-__device__ __forceinline__ u32x4 had128_x8(u32x4 in, u32x4 pre, bool has_pre, u32x4 post, bool has_post, double scale)
-{
-    f16x8 x = __builtin_bit_cast(f16x8, in);
-    if (has_pre) x = x * __builtin_bit_cast(f16x8, pre);
-    double v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = (double) x[i];
-    wht128_x8(v);
-    f16x8 y;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) y[i] = f64_to_f16_rto(v[i] * scale);
-    if (has_post) y = y * __builtin_bit_cast(f16x8, post);
-    return __builtin_bit_cast(u32x4, y);
-}
-
-// One 128-block per 8 lanes, 16 elements per lane (lane r = lane & 7 holds elements 16r ..
-// 16r + 15): element bits 0..3 are butterflies inside the lane, bits 4..6 lane xor 1, 2, 4
-// (quad_perm, then row_half_mirror + quad_perm reverse).  Same exact float64 sums and roundings,
-// so the same fp16 results as had128_x8, with fewer cross-lane moves per element.
-__device__ __forceinline__ void had128_x16(const u32x4 (&in)[2], const u32x4 (&pre)[2], bool has_pre,
-                                           const u32x4 (&post)[2], bool has_post, double scale, u32x4 (&out)[2])
-{
-    double v[16];
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        f16x8 x = __builtin_bit_cast(f16x8, in[c]);
-        if (has_pre) x = x * __builtin_bit_cast(f16x8, pre[c]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[8 * c + i] = (double) x[i];
-    }
-#pragma unroll
-    for (int h = 1; h < 16; h <<= 1)
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-            if (!(i & h)) {
-                const double a = v[i], b = v[i + h];
-                v[i] = a + b;
-                v[i + h] = a - b;
-            }
-    const int r = __lane_id() & 7;
-    double p[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) p[i] = dpp_f64<DPP_QP_XOR1>(v[i]);
-    {
-        const double sg = (r & 1) ? -1.0 : 1.0;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = __builtin_fma(sg, v[i], p[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) p[i] = dpp_f64<DPP_QP_XOR2>(v[i]);
-    {
-        const double sg = (r & 2) ? -1.0 : 1.0;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = __builtin_fma(sg, v[i], p[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) p[i] = dpp_f64<DPP_QP_REV>(dpp_f64<DPP_HALF_MIRROR>(v[i]));
-    {
-        const double sg = (r & 4) ? -1.0 : 1.0;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = __builtin_fma(sg, v[i], p[i]);
-    }
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        f16x8 y;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) y[i] = f64_to_f16_rto(v[8 * c + i] * scale);
-        if (has_post) y = y * __builtin_bit_cast(f16x8, post[c]);
-        out[c] = __builtin_bit_cast(u32x4, y);
-    }
-}
-
-// 64-bit value of lane (lane ^ 16): ds_swizzle within 32-lane halves (and 0x1F, xor 0x10)
-__device__ __forceinline__ double swz16_f64(double x)
+// value of lane (lane ^ 16): ds_swizzle within 32-lane halves (and 0x1F, xor 0x10)
+__device__ __forceinline__ double swz16_x(double x)
 {
     const uint64_t u = (uint64_t) __double_as_longlong(x);
     const uint32_t lo = (uint32_t) __builtin_amdgcn_ds_swizzle((int) (uint32_t) u, 0x401F);
@@ -229,57 +132,182 @@ __device__ __forceinline__ double swz16_f64(double x)
     return __longlong_as_double((long long) (((uint64_t) hi << 32) | lo));
 }
 
+__device__ __forceinline__ float swz16_x(float x)
+{
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(x), 0x401F));
+}
+
+// (value of the lower half's lane, value of the upper half's lane) for lane & 31:
+// v_permlane32_swap(x, x) swaps the upper half of its first operand with the lower half of its
+// second, so its first result holds the lower half's values in both halves of the wave
+__device__ __forceinline__ void halves_x(double x, double& lo, double& hi)
+{
+    const uint64_t u = (uint64_t) __double_as_longlong(x);
+    const auto w0 = __builtin_amdgcn_permlane32_swap((uint32_t) u, (uint32_t) u, false, false);
+    const auto w1 = __builtin_amdgcn_permlane32_swap((uint32_t) (u >> 32), (uint32_t) (u >> 32), false, false);
+    lo = __longlong_as_double((long long) (((uint64_t) w1[0] << 32) | w0[0]));
+    hi = __longlong_as_double((long long) (((uint64_t) w1[1] << 32) | w0[1]));
+}
+
+__device__ __forceinline__ void halves_x(float x, float& lo, float& hi)
+{
+    const auto w = __builtin_amdgcn_permlane32_swap((uint32_t) __float_as_int(x), (uint32_t) __float_as_int(x), false, false);
+    lo = __int_as_float((int) w[0]);
+    hi = __int_as_float((int) w[1]);
+}
+
+// fp16 of v * scale: double -> one rounding of the exact float64 product (round to odd float32,
+// then to fp16); float -> the product rounded to float32, then to fp16
+__device__ __forceinline__ f16 scaled_f16(double v, double scale) { return f64_to_f16_rto(v * scale); }
+__device__ __forceinline__ f16 scaled_f16(float v, float scale) { return (f16) (v * scale); }
+
+// one cross-lane butterfly stage: the lane holding a (bit clear) takes a + b, the lane holding b
+// takes a - b; fma with +-1 rounds once, as the separate add / subtract would
+template <class T, int N>
+__device__ __forceinline__ void had_stage(T (&v)[N], const T (&p)[N], bool upper)
+{
+    const T s = upper ? T(-1) : T(1);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = __builtin_fma(s, v[i], p[i]);
+}
+
+// in-lane stages over element bits 0 .. log2(N) - 1
+template <class T, int N>
+__device__ __forceinline__ void had_in_lane(T (&v)[N])
+{
+#pragma unroll
+    for (int h = 1; h < N; h <<= 1)
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            if (!(i & h)) {
+                const T a = v[i], b = v[i + h];
+                v[i] = a + b;
+                v[i + h] = a - b;
+            }
+}
+
+// 16 lanes per block: lane r = lane & 15 holds elements 8r .. 8r+7 (a wave transforms 4 blocks);
+// element bits 0..2 in the lane, bits 3..6 lane xor 1, 2, 4, 8 (quad_perm, row_half_mirror, row_ror)
+template <class T>
+__device__ __forceinline__ void wht128_x8(T (&v)[8])
+{
+    had_in_lane(v);
+    const int r = __lane_id() & 15;
+    T p[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = dpp_x<DPP_QP_XOR1>(v[i]);
+    had_stage(v, p, r & 1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = dpp_x<DPP_QP_XOR2>(v[i]);
+    had_stage(v, p, r & 2);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = dpp_x<DPP_QP_REV>(dpp_x<DPP_HALF_MIRROR>(v[i]));
+    had_stage(v, p, r & 4);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) p[i] = dpp_x<DPP_ROR8>(v[i]);
+    had_stage(v, p, r & 8);
+}
+
+// 8 fp16 in (16 B) -> 8 fp16 out: fp16(Had128(in [* pre]) * scale) [* post]; pre / post are the
+// matching 8 scale values (ignored when has_pre / has_post are false).  Each fp16 product is a
+// single rounding (packed fp16 multiplies), as in the reference kernels' hmul2 stages.
+template <class T>
+__device__ __forceinline__ u32x4 had128_x8(u32x4 in, u32x4 pre, bool has_pre, u32x4 post, bool has_post, T scale)
+{
+    f16x8 x = __builtin_bit_cast(f16x8, in);
+    if (has_pre) x = x * __builtin_bit_cast(f16x8, pre);
+    T v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (T) x[i];
+    wht128_x8(v);
+    f16x8 y;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = scaled_f16(v[i], scale);
+    if (has_post) y = y * __builtin_bit_cast(f16x8, post);
+    return __builtin_bit_cast(u32x4, y);
+}
+
+// One 128-block per 8 lanes, 16 elements per lane (lane r = lane & 7 holds elements 16r ..
+// 16r + 15): element bits 0..3 in the lane, bits 4..6 lane xor 1, 2, 4 (quad_perm, then
+// row_half_mirror + quad_perm reverse).  Fewer cross-lane moves per element than had128_x8.
+template <class T>
+__device__ __forceinline__ void had128_x16(const u32x4 (&in)[2], const u32x4 (&pre)[2], bool has_pre,
+                                           const u32x4 (&post)[2], bool has_post, T scale, u32x4 (&out)[2])
+{
+    T v[16];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        f16x8 x = __builtin_bit_cast(f16x8, in[c]);
+        if (has_pre) x = x * __builtin_bit_cast(f16x8, pre[c]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[8 * c + i] = (T) x[i];
+    }
+    had_in_lane(v);
+    const int r = __lane_id() & 7;
+    T p[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = dpp_x<DPP_QP_XOR1>(v[i]);
+    had_stage(v, p, r & 1);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = dpp_x<DPP_QP_XOR2>(v[i]);
+    had_stage(v, p, r & 2);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) p[i] = dpp_x<DPP_QP_REV>(dpp_x<DPP_HALF_MIRROR>(v[i]));
+    had_stage(v, p, r & 4);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        f16x8 y;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = scaled_f16(v[8 * c + i], scale);
+        if (has_post) y = y * __builtin_bit_cast(f16x8, post[c]);
+        out[c] = __builtin_bit_cast(u32x4, y);
+    }
+}
+
 // One 128-block per wave, two elements per lane (lane l holds elements 2l and 2l + 1): element
 // bit 0 in the lane, bits 1..4 lane xor 1, 2, 4, 8 (DPP as in wht128_x8), bit 5 lane xor 16
 // (ds_swizzle), bit 6 lane xor 32 (v_permlane32_swap).  A fourth of wht128_x8's instructions per
-// lane: the latency of the GEMV's single-row input and output transforms, which are on every
-// launch's critical path.  Same exact float64 sums and roundings, so the same fp16 results as
-// had128_x8.
+// lane: the latency form for the GEMV's single-row input and output transforms, which are on every
+// launch's critical path.
+template <class T>
 __device__ __forceinline__ uint32_t had128_x2(uint32_t in, uint32_t pre, bool has_pre, uint32_t post, bool has_post,
-                                              double scale)
+                                              T scale)
 {
     f16x2 x = __builtin_bit_cast(f16x2, in);
     if (has_pre) x = x * __builtin_bit_cast(f16x2, pre);
-    const double a = (double) x[0], b = (double) x[1];
-    double v[2] = {a + b, a - b};
+    const T a = (T) x[0], b = (T) x[1];
+    T v[2] = {a + b, a - b};
     const int l = __lane_id();
-    double p[2];
-    auto stage = [&](bool upper) __attribute__((always_inline)) {
-        const double sg = upper ? -1.0 : 1.0;
-        v[0] = __builtin_fma(sg, v[0], p[0]);
-        v[1] = __builtin_fma(sg, v[1], p[1]);
-    };
+    T p[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) p[i] = dpp_f64<DPP_QP_XOR1>(v[i]);
-    stage(l & 1);
+    for (int i = 0; i < 2; ++i) p[i] = dpp_x<DPP_QP_XOR1>(v[i]);
+    had_stage(v, p, l & 1);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) p[i] = dpp_f64<DPP_QP_XOR2>(v[i]);
-    stage(l & 2);
+    for (int i = 0; i < 2; ++i) p[i] = dpp_x<DPP_QP_XOR2>(v[i]);
+    had_stage(v, p, l & 2);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) p[i] = dpp_f64<DPP_QP_REV>(dpp_f64<DPP_HALF_MIRROR>(v[i]));
-    stage(l & 4);
+    for (int i = 0; i < 2; ++i) p[i] = dpp_x<DPP_QP_REV>(dpp_x<DPP_HALF_MIRROR>(v[i]));
+    had_stage(v, p, l & 4);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) p[i] = dpp_f64<DPP_ROR8>(v[i]);
-    stage(l & 8);
+    for (int i = 0; i < 2; ++i) p[i] = dpp_x<DPP_ROR8>(v[i]);
+    had_stage(v, p, l & 8);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) p[i] = swz16_f64(v[i]);
-    stage(l & 16);
-    // v_permlane32_swap(x, x) swaps the upper half of its first operand with the lower half of
-    // its second: the first result holds the lower half's values in both halves of the wave, the
-    // second the upper half's.  Lower lanes take lo + hi, upper lanes lo - hi.
+    for (int i = 0; i < 2; ++i) p[i] = swz16_x(v[i]);
+    had_stage(v, p, l & 16);
+    // bit 6: lower lanes take lo + hi, upper lanes lo - hi
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const uint64_t u = (uint64_t) __double_as_longlong(v[i]);
-        const auto w0 = __builtin_amdgcn_permlane32_swap((uint32_t) u, (uint32_t) u, false, false);
-        const auto w1 = __builtin_amdgcn_permlane32_swap((uint32_t) (u >> 32), (uint32_t) (u >> 32), false, false);
-        const double lo = __longlong_as_double((long long) (((uint64_t) w1[0] << 32) | w0[0]));
-        const double hi = __longlong_as_double((long long) (((uint64_t) w1[1] << 32) | w0[1]));
-        v[i] = __builtin_fma(l & 32 ? -1.0 : 1.0, hi, lo);
+        T lo, hi;
+        halves_x(v[i], lo, hi);
+        v[i] = __builtin_fma(l & 32 ? T(-1) : T(1), hi, lo);
     }
-    f16x2 y = {f64_to_f16_rto(v[0] * scale), f64_to_f16_rto(v[1] * scale)};
+    f16x2 y = {scaled_f16(v[0], scale), scaled_f16(v[1], scale)};
     if (has_post) y = y * __builtin_bit_cast(f16x2, post);
     return __builtin_bit_cast(uint32_t, y);
 }
+
+// the Hadamard scale of every reference call site, per element type
+template <class T> constexpr T r_scale() { return (T) R_SCALE; }
 
 // ------------------------------------------------------------------------------------------
 // Codebook constants

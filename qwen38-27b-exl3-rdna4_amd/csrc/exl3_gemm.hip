@@ -1,12 +1,14 @@
 // exl3_gemm.hip -- prefill (large-M) EXL3 linear and dense fp16 GEMM for gfx950.
 //
 // exl3_gemm_trellis: y = had_out(fp16(had_in(x) . W), svh) in two launches:
-//   1. had_in   xh = fp16(Had128(fp16(x * suh)))                       (had_kernel)
+//   1. had_in   xh = fp16(Had128(fp16(x * suh)))            (had_kernel, float32 butterflies)
 //   2. GEMM     C = fp16(xh . W) on 128 x 128 output tiles, K step 64: each step the workgroup
 //               decodes its 4 x 8 trellis tiles (one q-block per thread) straight into LDS in
 //               MFMA B-fragment order and stages the xh rows in A-fragment order;
 //               v_mfma_f32_16x16x32_f16, fp32 accumulation; LDS double-buffered.  The epilogue
-//               applies y = fp16(fp16(Had128(C)) * svh) to the tile's whole 128-column blocks.
+//               applies y = fp16(fp16(Had128(C)) * svh) to the tile's whole 128-column blocks
+//               (float32 butterflies, the values of exl3_had_r_128_f32: +1.1 % over float64 on
+//               the configuration-4 chunk; the rows are checked to the rel-L2 bar).
 // exl3_hgemm_recon is the same GEMM with a dense fp16 W[k, n] as the B source and a plain
 // fp16 C epilogue.
 #include "exl3_device.h"
@@ -20,7 +22,7 @@ using namespace exl3;
 
 // had_r_128 of one input into several outputs in one launch (exl3_gemv.hip)
 int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, int rows, int cols, const void* const* pre,
-               int groups, const void* post, float scale, void* stream);
+               int groups, const void* post, float scale, void* stream, bool exact);
 
 namespace {
 
@@ -247,7 +249,7 @@ __global__ void __launch_bounds__(Tile<MT>::THREADS) gemm_kernel(const uint16_t*
         for (int r0 = 0; r0 < MT; r0 += TL::THREADS / 16) {
             const int r = r0 + (t >> 4);
             const u32x4 c = *reinterpret_cast<const u32x4*>(ct + r * TL::C_ROW + 8 * l16);
-            const u32x4 res = had128_x8(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, R_SCALE);
+            const u32x4 res = had128_x8<float>(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, r_scale<float>());
             if (row0 + r < M) *reinterpret_cast<u32x4*>(y + (int64_t) (row0 + r) * ldy + col0 + 8 * l16) = res;
         }
     } else {
@@ -641,7 +643,7 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
     for (int r0 = 0; r0 < PC::MT; r0 += PC::THREADS / 16) {
         const int r = r0 + (t >> 4);
         const u32x4 c = *reinterpret_cast<const u32x4*>(ct + r * PC::C_ROW + 8 * l16);
-        const u32x4 res = had128_x8(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, R_SCALE);
+        const u32x4 res = had128_x8<float>(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, r_scale<float>());
         if (row0 + r < M)
             __builtin_amdgcn_raw_buffer_store_b128(res, ysrc, (uint32_t) (((int64_t) r * a.ldy + col0 + 8 * l16) * 2), 0, SC1);
     }
@@ -765,7 +767,7 @@ int gemm_trellis_common(const void* x, int64_t ldx, const void* const* trellis, 
         svs[i] = (const uint16_t*) svh[i];
     }
     // the groups' input transforms (one x, each group's suh) in one launch
-    const int rc = launch_had(x, ldx, xo, k, m, k, suh, groups, nullptr, 1.0f, s);
+    const int rc = launch_had(x, ldx, xo, k, m, k, suh, groups, nullptr, 1.0f, s, false);
     if (rc) return rc;
     const int cb = codebook_of(mcg, mul1);
     switch (K) {

@@ -95,8 +95,12 @@ struct HadGroups {
     uint16_t* out[EXL3_MAX_GROUPS];
 };
 
+// T: the butterflies' element type (double: exl3_had_r_128 and the GEMV's pre-rotation, the same
+// values as the GEMV's in-kernel transforms; float: the prefill's input transforms and
+// exl3_had_r_128_f32, the same values as the prefill epilogue's)
+template <class T>
 __global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ in, int64_t ld_in, HadGroups hg, int64_t ld_out,
-                                                  int rows, int cols, const uint16_t* __restrict__ post, double scale)
+                                                  int rows, int cols, const uint16_t* __restrict__ post, T scale)
 {
     const int gy = blockIdx.y;
     const uint16_t* pre = gy == 0 ? hg.pre[0] : gy == 1 ? hg.pre[1] : gy == 2 ? hg.pre[2] : hg.pre[3];
@@ -120,7 +124,7 @@ __global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ i
     }
     // every lane takes part in the DPP exchanges; only live lanes store
     u32x4 res[2];
-    had128_x16(v, pv, pre != nullptr, qv, post != nullptr, R_SCALE * scale, res);
+    had128_x16<T>(v, pv, pre != nullptr, qv, post != nullptr, scale, res);
     if (live) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) *reinterpret_cast<u32x4*>(out + row * ld_out + col + 8 * c) = res[c];
@@ -128,9 +132,9 @@ __global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ i
 }
 
 // had_r_128 of one input into `groups` outputs, group i scaled by pre[i] (may be null): one launch
-// (the prefill's input transforms of a fused module)
+// (the prefill's input transforms of a fused module); exact: float64 butterflies, else float32
 int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, int rows, int cols, const void* const* pre,
-               int groups, const void* post, float scale, void* stream)
+               int groups, const void* post, float scale, void* stream, bool exact)
 {
     if (!in || !out || rows < 0 || cols % 128 || cols < 128 || ld_in < cols || ld_out < cols || ld_in % 8 || ld_out % 8 ||
         groups < 1 || groups > EXL3_MAX_GROUPS || (((uintptr_t) in) & 15) || (((uintptr_t) post) & 15))
@@ -144,8 +148,13 @@ int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, 
     }
     if (rows == 0) return EXL3_OK;
     const int64_t jobs = (int64_t) rows * (cols / 128);           // 8 lanes each
-    hipLaunchKernelGGL(had_kernel, dim3((unsigned) ((jobs + 31) / 32), (unsigned) groups), dim3(256), 0, (hipStream_t) stream,
-                       (const uint16_t*) in, ld_in, hg, ld_out, rows, cols, (const uint16_t*) post, (double) scale);
+    const dim3 grid((unsigned) ((jobs + 31) / 32), (unsigned) groups);
+    if (exact)
+        hipLaunchKernelGGL(had_kernel<double>, grid, dim3(256), 0, (hipStream_t) stream, (const uint16_t*) in, ld_in, hg, ld_out,
+                           rows, cols, (const uint16_t*) post, R_SCALE * (double) scale);
+    else
+        hipLaunchKernelGGL(had_kernel<float>, grid, dim3(256), 0, (hipStream_t) stream, (const uint16_t*) in, ld_in, hg, ld_out,
+                           rows, cols, (const uint16_t*) post, (float) (R_SCALE * (double) scale));
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 
@@ -353,7 +362,7 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
             outs[i] = (uint16_t*) xr + (int64_t) i * m * k;
             pres[i] = gs[i].suh;
         }
-        const int rc = launch_had(x, ldx, outs, k, m, k, pres, groups, nullptr, 1.0f, stream);
+        const int rc = launch_had(x, ldx, outs, k, m, k, pres, groups, nullptr, 1.0f, stream, true);
         if (rc != EXL3_OK) return rc;
         a.xr = (const uint16_t*) xr;
     }
@@ -611,7 +620,15 @@ int exl3_had_r_128(const void* in, int64_t ld_in, void* out, int64_t ld_out, int
 {
     void* const outs[1] = {out};
     const void* const pres[1] = {pre};
-    return launch_had(in, ld_in, outs, ld_out, rows, cols, pres, 1, post, scale, stream);
+    return launch_had(in, ld_in, outs, ld_out, rows, cols, pres, 1, post, scale, stream, true);
+}
+
+int exl3_had_r_128_f32(const void* in, int64_t ld_in, void* out, int64_t ld_out, int rows, int cols, const void* pre,
+                       const void* post, float scale, void* stream)
+{
+    void* const outs[1] = {out};
+    const void* const pres[1] = {pre};
+    return launch_had(in, ld_in, outs, ld_out, rows, cols, pres, 1, post, scale, stream, false);
 }
 
 }  // extern "C"

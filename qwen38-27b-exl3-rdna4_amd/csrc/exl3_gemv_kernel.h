@@ -284,6 +284,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
         col = (u - (u / UPB) * UPB) * 128 + 8 * (threadIdx.x & 15);
     };
 
+    // Transforms run float64 butterflies (the pre-rotation pass too, so every layout gives the same
+    // values): the rotated input and y are then the correctly rounded fp16 of the exact transforms,
+    // which the reference's strict M = 1 gates assume (a last-place flip of one large output alone
+    // is ~3e-3 of the output RMS).  Float32 butterflies measured no faster here: the prologue waits
+    // on memory, not on the rotation's VALU work.
     // The prologue and the completion phase sit on every workgroup's critical path while other
     // workgroups on the same SIMDs run VALU-heavy decode loops: give them issue priority.
     __builtin_amdgcn_s_setprio(2);
@@ -356,7 +361,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 x0 = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * ldx + col);
                 if (!pre) s0 = *reinterpret_cast<gc_u32x4*>(gsuh + col);
             }
-            const u32x4 r = pre ? x0 : had128_x8(x0, s0, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
+            const u32x4 r = pre ? x0 : had128_x8<double>(x0, s0, true, u32x4{0u, 0u, 0u, 0u}, false, r_scale<double>());
             if (i < njobs) {
                 int m, col;
                 job_src(c0, i, m, col);
@@ -375,7 +380,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                         if (!pre) sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
                     }
                 }
-                const u32x4 r2 = pre ? xv : had128_x8(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, R_SCALE);
+                const u32x4 r2 = pre ? xv : had128_x8<double>(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, r_scale<double>());
                 if (i2 < njobs)
                     *reinterpret_cast<u32x4*>(lds_a + ((i2 / M) * UROWS + m) * A_ROW + 8 * (threadIdx.x & 15)) = r2;
             }
@@ -385,7 +390,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     if (wide) {
         if (wave < nfirst)
             *reinterpret_cast<uint32_t*>(lds_a + (wave * UROWS) * A_ROW + 2 * lane) =
-                had128_x2(px.x, ps.x, true, 0u, false, R_SCALE);
+                had128_x2<double>(px.x, ps.x, true, 0u, false, r_scale<double>());
     } else {
         rotate_chunk(c0, c1, px, ps, px2, ps2, true);
     }
@@ -751,8 +756,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                     const int cb = seg0_cb + b0 + s_list[r0 + wave];
                     const uint32_t cg = *reinterpret_cast<const uint32_t*>(lds_c + (wave * RM) * A_ROW + 2 * lane);
                     const uint32_t cu = *reinterpret_cast<const uint32_t*>(lds_c + (wave * RM + 1) * A_ROW + 2 * lane);
-                    const uint32_t rg = had128_x2(cg, 0u, false, sv_first.x, true, R_SCALE);
-                    const uint32_t ru = had128_x2(cu, 0u, false, sv_first_u.x, true, R_SCALE);
+                    const uint32_t rg = had128_x2<double>(cg, 0u, false, sv_first.x, true, r_scale<double>());
+                    const uint32_t ru = had128_x2<double>(cu, 0u, false, sv_first_u.x, true, r_scale<double>());
                     __builtin_amdgcn_raw_buffer_store_b32(silu_mul_x2(rg, ru), y0src, (uint32_t) ((cb * 128 + 2 * lane) * 2), 0,
                                                           SC1);
                 }
@@ -774,8 +779,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                         svg = rr0 == 0 ? sv_first : *reinterpret_cast<gc_u32x4*>(as_global(a.g[0].svh) + cb * 128 + 8 * l16);
                         svu = rr0 == 0 ? sv_first_u : *reinterpret_cast<gc_u32x4*>(as_global(a.g[1].svh) + cb * 128 + 8 * l16);
                     }
-                    const u32x4 rg = had128_x8(cg, u32x4{0u, 0u, 0u, 0u}, false, svg, true, R_SCALE);
-                    const u32x4 ru = had128_x8(cu, u32x4{0u, 0u, 0u, 0u}, false, svu, true, R_SCALE);
+                    const u32x4 rg = had128_x8<double>(cg, u32x4{0u, 0u, 0u, 0u}, false, svg, true, r_scale<double>());
+                    const u32x4 ru = had128_x8<double>(cu, u32x4{0u, 0u, 0u, 0u}, false, svu, true, r_scale<double>());
                     if (live)
                         __builtin_amdgcn_raw_buffer_store_b128(silu_mul_x8(rg, ru), y0src,
                                                                (uint32_t) (((int64_t) m * a.ldy + cb * 128 + 8 * l16) * 2), 0, SC1);
@@ -788,7 +793,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 if (wave < rb) {
                     const int cb = seg0_cb + b0 + s_list[r0 + wave];
                     const uint32_t c = *reinterpret_cast<const uint32_t*>(lds_c + wave * A_ROW + 2 * lane);
-                    __builtin_amdgcn_raw_buffer_store_b32(had128_x2(c, 0u, false, sv_first.x, true, R_SCALE), ysrc,
+                    __builtin_amdgcn_raw_buffer_store_b32(had128_x2<double>(c, 0u, false, sv_first.x, true, r_scale<double>()), ysrc,
                                                           (uint32_t) ((cb * 128 + 2 * lane) * 2), 0, SC1);
                 }
                 __syncthreads();                               // lds_c free for the next blocks
@@ -805,7 +810,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                     c = *reinterpret_cast<const u32x4*>(lds_c + rr * A_ROW + 8 * l16);
                     sv = rr0 == 0 ? sv_first : *reinterpret_cast<gc_u32x4*>(gsvh + cb * 128 + 8 * l16);
                 }
-                const u32x4 res = had128_x8(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, R_SCALE);
+                const u32x4 res = had128_x8<double>(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, r_scale<double>());
                 if (live)
                     __builtin_amdgcn_raw_buffer_store_b128(res, ysrc, (uint32_t) (((int64_t) m * a.ldy + cb * 128 + 8 * l16) * 2), 0, SC1);
             }

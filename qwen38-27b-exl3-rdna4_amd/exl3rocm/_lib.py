@@ -28,6 +28,7 @@ SIGNATURES = {
     "exl3_reconstruct": (_i, [_p, _p, _i, _i, _i, _i, _i, _p]),
     "exl3_reconstruct_slice": (_i, [_p, _i64, _p, _i, _i, _i, _i, _i, _i, _i, _p]),
     "exl3_had_r_128": (_i, [_p, _i64, _p, _i64, _i, _i, _p, _p, _f, _p]),
+    "exl3_had_r_128_f32": (_i, [_p, _i64, _p, _i64, _i, _i, _p, _p, _f, _p]),
     "exl3_gemv_grid": (_i, [_i, _i, _i]),
     "exl3_gemv_workspace_size": (_sz, [_i, _i, _i, _i, _i]),
     "exl3_gemv_mr_supported": (_i, [_i, _i, _i, _i, _i, _i]),

@@ -123,8 +123,10 @@ def reconstruct_slice(W: torch.Tensor, trellis: torch.Tensor, K: int, mcg: bool,
 
 
 def had_r_128(inp: torch.Tensor, out: torch.Tensor, pre: Optional[torch.Tensor], post: Optional[torch.Tensor],
-              scale: float) -> None:
-    """Blockwise Hadamard over the last dim (multiple of 128); 2-D operands may have any row stride."""
+              scale: float, exact: bool = True) -> None:
+    """Blockwise Hadamard over the last dim (multiple of 128); 2-D operands may have any row stride.
+    exact: float64 butterflies (exl3_had_r_128, also the fused GEMV's values); otherwise the
+    float32 values the prefill GEMM uses (exl3_had_r_128_f32)."""
     _cuda(inp, out, pre, post)
     _need(inp.dtype == torch.float16 and out.dtype == torch.float16 and inp.shape == out.shape,
           "had_r_128: fp16 tensors of equal shape")
@@ -139,7 +141,8 @@ def had_r_128(inp: torch.Tensor, out: torch.Tensor, pre: Optional[torch.Tensor],
 
     i2, o2 = as2d(inp), as2d(out)
     rows = i2.shape[0]
-    L.check(L.lib().exl3_had_r_128(i2.data_ptr(), i2.stride(0) if rows > 1 else cols, o2.data_ptr(),
+    fn = L.lib().exl3_had_r_128 if exact else L.lib().exl3_had_r_128_f32
+    L.check(fn(i2.data_ptr(), i2.stride(0) if rows > 1 else cols, o2.data_ptr(),
                                    o2.stride(0) if rows > 1 else cols, rows, cols,
                                    pre.data_ptr() if pre is not None else None,
                                    post.data_ptr() if post is not None else None, float(scale), _stream(inp)),

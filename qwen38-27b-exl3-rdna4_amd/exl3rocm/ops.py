@@ -82,8 +82,9 @@ def _linear_into(x2, trellis, suh, svh, K, mcg, mul1, y):
         if rc != 0:
             raise RuntimeError(f"exl3rocm: GEMV declined shape m={M} k={k} n={n} K={K}")
     elif PREFILL_ROUTE == "recon":
+        # the fused prefill's float32 transforms (exact=False): this route stays bitwise equal to it
         xh = torch.empty_like(x2)
-        E.had_r_128(x2, xh, suh, None, 1.0)
+        E.had_r_128(x2, xh, suh, None, 1.0, exact=False)
         for n0 in range(0, n, RECON_SLICE_N):
             n1 = min(n0 + RECON_SLICE_N, n)
             w = _weight_buffer(x2.device, k * (n1 - n0)).view(k, n1 - n0)
@@ -92,7 +93,7 @@ def _linear_into(x2, trellis, suh, svh, K, mcg, mul1, y):
             else:
                 E.reconstruct_slice(w, trellis, K, mcg, mul1, n0)
             E.hgemm_recon(xh, w, y[:, n0:n1])
-        E.had_r_128(y, y, None, svh, 1.0)
+        E.had_r_128(y, y, None, svh, 1.0, exact=False)
     else:
         # the grouped entry point with one group: its launch balances the last wave of tiles
         xh = torch.empty_like(x2)
