@@ -98,7 +98,12 @@ constexpr int RED_BATCH = 16;                   // partial loads in flight per t
 constexpr int CNT_STRIDE = 32;
 constexpr int A_ROW = 136;                      // LDS row of one rotated 128-block (padded, halves)
 constexpr int LDS_BUDGET = 64 * 1024;           // per workgroup: 2 workgroups per CU
-constexpr int RING = 8;                         // 64-row k steps in flight per wave (even)
+// 64-row k steps in flight per wave (even).  4 measured faster than 8 (+2 % config 1; gate, down
+// and o -1.7, -1.2 and -0.3 us alone): at launch every wave of every CU requests its first ring
+// half at once, and the CUs' load queues stall each wave's issue until early data returns, so a
+// shallower ring starts the first decode sooner (the first step of gate/up completed ~5 us after
+// launch with 8 in flight).
+constexpr int RING = 4;
 constexpr int WAVES_PER_SIMD = 2;
 
 // s_waitcnt vmcnt(0) (gfx9 encoding: expcnt / lgkmcnt left at their maxima), fenced against
