@@ -154,9 +154,10 @@ __device__ __forceinline__ int64_t uniform_i64(int64_t v)
 
 // Unit split of a group's U units over its G workgroups: workgroup w owns [lo(w), lo(w + 1)),
 // lo(w) = floor(U * S(w) / S(G)) with S(w) = wa * min(w, h) + wb * max(w - h, 0).  The first h
-// workgroups of the group are dispatched first on their CU; the SIMD arbiter favours their (older)
-// waves, so they get the larger weight wa and both waves of a CU finish their units together.  A
-// function of the shape only (never of m): rows stay bitwise equal to the m == 1 call.
+// workgroups of the group are dispatched first on their CU (weight wa = 2); the others are the
+// second workgroup on their CU, run their loop at the higher wave priority (the SIMD arbiter
+// otherwise favours the older waves) and take the larger weight wb = 3.  A function of the shape
+// only (never of m): rows stay bitwise equal to the m == 1 call.
 struct Split {
     int U, G, h, wa, wb;
     UDiv d_sg, d_u, d_wa, d_wb;          // divisions by S(G), U, wa and wb
