@@ -181,6 +181,49 @@ def per_shape_gemv(torch, sets, x5120, x17408, reps=64):
     return out
 
 
+def approx_m1(torch, sets, x5120, x17408, reps=64):
+    """The opt-in approximate mul1 GEMV (exl3_gemv_mr_approx) at M = 1 on the configuration-1
+    shapes: mean launch duration per mode, as per_shape_gemv times the faithful one, and each
+    mode's rel-L2 deviation from the faithful output of the same launch."""
+    from exl3rocm import kernels as E
+    out = {}
+    s = torch.cuda.Stream()
+    for mode in ("affine", "int8"):
+        row = {}
+        for name, k, n in LAYER:
+            x = x17408 if k == INTER else x5120
+            y = torch.empty(1, n, dtype=torch.float16, device="cuda")
+            yf = torch.empty_like(y)
+            with torch.cuda.stream(s):
+                for ls in sets:
+                    T, SU, SV = ls.w[name]
+                    E.exl3_gemv_mr_approx(x, T, y, SU, None, SV, ls.bits, mode)
+                T, SU, SV = sets[0].w[name]
+                E.exl3_gemv_mr_approx(x, T, y, SU, None, SV, sets[0].bits, mode)
+                E.exl3_gemv(x, T, yf, SU, None, SV, False, True)
+            s.synchronize()
+            dev = ((y.float() - yf.float()).norm() / yf.float().norm()).item()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                for r in range(reps):
+                    T, SU, SV = sets[r % len(sets)].w[name]
+                    E.exl3_gemv_mr_approx(x, T, y, SU, None, SV, sets[0].bits, mode)
+            with torch.cuda.stream(s):
+                g.replay()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(s)
+                for _ in range(3):
+                    g.replay()
+                e1.record(s)
+            s.synchronize()
+            us = e0.elapsed_time(e1) * 1e3 / (3 * reps)
+            b = algo_bytes(1, k, n, sets[0].bits)
+            row[name] = {"us": round(us, 3), "gbs": round(b / us / 1e3, 1), "rel_l2_vs_faithful": round(dev, 6)}
+            del g
+        out[mode] = row
+    return out
+
+
 def gated_mlp(torch, sets, x5120, ms=(1, 8), reps=32):
     """The MLP input of config 1: gate/up + SiLU-and-mul fused into one GEMV launch
     (exl3_gemv_silu_mul) against the unfused pair (linear_groups, then the elementwise kernel,
@@ -496,6 +539,8 @@ def main() -> int:
     extra = {"launches_per_step": lps, "step_bytes": step_bytes, "wall_s": round(wall, 3)}
     log("per-shape GEMV timing")
     extra["per_shape_m1"] = per_shape_gemv(torch, sets, x5120, x17408)
+    log("approximate mul1 GEMV (opt-in affine / int8 routes)")
+    extra["approx_m1"] = approx_m1(torch, sets, x5120, x17408)
     log("gated MLP input (gate/up + SiLU-and-mul)")
     extra["gated_mlp"] = gated_mlp(torch, sets, x5120)
     if not args.no_sweep:

@@ -116,6 +116,24 @@ int exl3_gemv_mr(const void* x, int64_t ldx, const void* trellis, void* y, int64
                  const void* svh, int m, int k, int n, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
                  void* stream);
 
+/* Approximate mul1 EXL3 linear for 1 <= m <= 32 (opt-in; outputs are not the faithful staging's):
+ *   mode 1 (affine): C = k_inv * sum_k a_k (1024 + s_k) + k_bias * sum_k a_k, i.e. the mul1 weights
+ *     before their fp16 rounding (rel-L2 ~5e-4 from the faithful output);
+ *   mode 2 (int8 activations): the rotated input quantized per (row, 128-input slice) as
+ *     v = clamp(rint(a / q), -127, 127), q = max(|a|, 1e-8) / 127, and C = sum over slices of
+ *     q (k_inv sum v (1024 + s) + k_bias sum v) -- the reference's int8 path (integer products,
+ *     affine epilogue), with one scale per slice.
+ * C is rounded to fp16 and transformed as in exl3_gemv_mr.  Arguments, workspace and A_had as
+ * exl3_gemv_mr (mul1 codebook implied).  Returns EXL3_EINVAL for another mode.
+ * Replaces the reference's opt-in int8 GEMV behind exl3_gemm (EXL3_ROCM_GFX1201_INT8,
+ * vllm_plugin/patches/exl3-fork/0001-int8-port-gfx1201-compat.patch:153-523; oracle
+ * reference/exl3_oracle.py:357-412); mode 1 has no counterpart (the same epilogue on fp16
+ * activations).  On gfx950 the dot products run on fp16 MFMA in both modes (the quantized values
+ * and 1024 + s are exact fp16 integers): the saving is the per-weight fp16 scale of the decode. */
+int exl3_gemv_mr_approx(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh,
+                        void* A_had, const void* svh, int m, int k, int n, int K, int mode, void* workspace,
+                        size_t ws_bytes, void* stream);
+
 /* Up to 4 groups sharing x (equal k, n, K): group i writes columns [i*n, (i+1)*n) of y.
  * trellis / suh / svh are host arrays of device pointers.
  * Replaces `exl3_gemv_mr_grouped(A, [B], C, [suh], A_had, [svh], K, mcg, mul1, bszm)`

@@ -259,6 +259,86 @@ def linear(x, trellis: np.ndarray, bits: int, suh, svh, cb: int = 2, faithful: b
 
 
 # ---------------------------------------------------------------------------
+# Approximate mul1 forms: unrounded weights (affine) and int8 activations
+# (reference exl3_oracle.py:357-412)
+# ---------------------------------------------------------------------------
+def mul1_affine_weights(states: np.ndarray) -> np.ndarray:
+    """mul1 weights before their fp16 rounding: (1024 + bytesum(w * 0x83DCD12D)) * K_INV + K_BIAS,
+    exact in float64 (codebook_f16 is this value rounded once to fp16)."""
+    s = byte_sum(codebook_hash(states, 2)).astype(np.float64)
+    return (1024.0 + s) * K_INV + K_BIAS
+
+
+def quantize_splats(a_had, q: float, residual: bool = False):
+    """Symmetric int8 quantization with clamp [-127, 127] (reference exl3_oracle.py:357-371):
+    v = clip(rint(a / q)); with residual a second int8 v2 of the remainder at scale q / 254.
+    Returns (v, v2 or None, sum(v), sum(v2))."""
+    a = np.asarray(a_had, dtype=np.float64)
+    v = np.clip(np.rint(a / q).astype(np.int64), -127, 127)
+    v2, s2 = None, 0
+    if residual:
+        r = a - q * v.astype(np.float64)
+        v2 = np.clip(np.rint(r / (q / 254.0)).astype(np.int64), -127, 127)
+        s2 = int(v2.sum())
+    return v, v2, int(v.sum()), s2
+
+
+def gemv_int8_reference(a_had, states: np.ndarray, q: float, svh, residual: bool = False) -> np.ndarray:
+    """The reference's int8-activation GEMV with one global scale q (exl3_oracle.py:374-412):
+    exact integer accumulation of v . bytesum, then the affine epilogue
+    y_rot = K_INV * (q acc1 + q2 acc2) + (1024 K_INV + K_BIAS) (q s1 + q2 s2), and the exact
+    output transform (float64, no fp16 rounding).  states: (k, n) 16-bit state matrix."""
+    a = np.asarray(a_had, dtype=np.float64)
+    v, v2, s1, s2 = quantize_splats(a, q, residual)
+    s = byte_sum(codebook_hash(states, 2)).astype(np.int64)
+    acc = q * (v @ s).astype(np.float64)
+    suma = q * s1
+    if residual:
+        q2 = q / 254.0
+        acc = acc + q2 * (v2 @ s).astype(np.float64)
+        suma += q2 * s2
+    y_rot = K_INV * acc + (1024.0 * K_INV + K_BIAS) * suma
+    return had_out(y_rot, svh, faithful=False)
+
+
+def slice_scales(a_had, slice_len: int = 128) -> np.ndarray:
+    """One int8 scale per (row, slice of slice_len inputs): max(|a| over the slice, 1e-8) / 127
+    (the per-slice form of the reference's quantization, exl3_oracle.py:378-384)."""
+    a = np.atleast_2d(np.asarray(a_had, dtype=np.float64))
+    m, k = a.shape
+    amax = np.abs(a.reshape(m, k // slice_len, slice_len)).max(axis=2)
+    return np.maximum(amax, 1e-8) / 127.0
+
+
+def linear_approx(x, trellis: np.ndarray, bits: int, suh, svh, mode: str) -> np.ndarray:
+    """The GEMV's approximate mul1 routes, staged as the kernels stage them: faithful fp16 A_had,
+    then linear_approx_rotated."""
+    x = to_f16(np.atleast_2d(np.asarray(x, dtype=np.float64)))
+    return linear_approx_rotated(had_in(x, to_f16(suh), True), trellis, bits, svh, mode)
+
+
+def linear_approx_rotated(a, trellis: np.ndarray, bits: int, svh, mode: str) -> np.ndarray:
+    """From the rotated input a [m, k]: C = sum over k of a_k w_k with the unrounded weights
+    w_k = K_INV (1024 + s_k) + K_BIAS (mode "affine"), or with a_k replaced by q v_k, v_k the int8
+    quantization of a at one scale q per 128-input slice (mode "int8"); C rounded to fp16;
+    faithful output transform."""
+    a = np.atleast_2d(np.asarray(a, dtype=np.float64))
+    svh = to_f16(svh)
+    S = states_matrix(trellis, bits)
+    W = mul1_affine_weights(S)
+    if mode == "int8":
+        q = slice_scales(a)
+        m, k = a.shape
+        qk = np.repeat(q, 128, axis=1)
+        v = np.clip(np.rint(a / qk), -127, 127)
+        a = v * qk
+    elif mode != "affine":
+        raise ValueError(mode)
+    c = to_f16(a @ W)
+    return had_out(c, svh, True)
+
+
+# ---------------------------------------------------------------------------
 # Error metrics used by the tests
 # ---------------------------------------------------------------------------
 def rel_l2(got, ref) -> float:

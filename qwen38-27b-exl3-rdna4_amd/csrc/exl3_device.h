@@ -312,8 +312,13 @@ template <class T> constexpr T r_scale() { return (T) R_SCALE; }
 // ------------------------------------------------------------------------------------------
 // Codebook constants
 // ------------------------------------------------------------------------------------------
+// CB 3 and 4 are the mul1 hash without the per-weight fp16 scale: the decoder emits the exact fp16
+// integers 1024 + s, and the GEMV applies k_inv and k_bias per output instead (the affine and
+// int8-activation routes of the fused GEMV; never used for decoded weight tiles)
 template <int CB> struct Codebook;
 template <> struct Codebook<2> { static constexpr uint32_t lo = 0xD12Du, hi = 0x83DCu, add = 0; };       // mul1
+template <> struct Codebook<3> : Codebook<2> {};                                                          // mul1, unscaled
+template <> struct Codebook<4> : Codebook<2> {};                                                          // mul1, unscaled
 template <> struct Codebook<1> { static constexpr uint32_t lo = 0x1FEDu, hi = 0xCBACu, add = 0; };       // mcg
 template <> struct Codebook<0> { static constexpr uint32_t lo = 0x7C72u, hi = 0x0551u, add = 64248484u; }; // 3inst
 
@@ -380,15 +385,17 @@ __device__ __forceinline__ uint32_t decode_pair(const uint32_t* W, uint32_t k_hi
 {
     const uint32_t x0 = state_x<BITS, CB, 2 * I>(W, k_hi, k_add, k_lo);
     const uint32_t x1 = state_x<BITS, CB, 2 * I + 1>(W, k_hi, k_add, k_lo);
-    if constexpr (CB == 2) {
+    if constexpr (CB >= 2) {
         // 0x6400 + bytesum is the fp16 bit pattern of 1024 + s (exact for s <= 1020).  Byte sums
         // of differences against zero: v_sad_u8 adds s0 to 0x64006400, v_sad_hi_u8 adds s1 << 16,
         // which packs the pair (1024 + s1, 1024 + s0) in two ops with no carry between halves.
         const uint32_t lo = __builtin_amdgcn_sad_u8(x0, 0u, c6400);
         f16x2 h = __builtin_bit_cast(f16x2, __builtin_amdgcn_sad_hi_u8(x1, 0u, lo));
-        const f16x2 k_inv = {bits_f16(0x1EEEu), bits_f16(0x1EEEu)};
-        const f16x2 k_bias = {bits_f16(0xC931u), bits_f16(0xC931u)};
-        h = __builtin_elementwise_fma(h, k_inv, k_bias);           // v_pk_fma_f16: one rounding
+        if constexpr (CB == 2) {
+            const f16x2 k_inv = {bits_f16(0x1EEEu), bits_f16(0x1EEEu)};
+            const f16x2 k_bias = {bits_f16(0xC931u), bits_f16(0xC931u)};
+            h = __builtin_elementwise_fma(h, k_inv, k_bias);       // v_pk_fma_f16: one rounding
+        }
         return __builtin_bit_cast(uint32_t, h);
     } else {
         // gather lo halves and hi halves of the two hashes, then the mask/xor (half-symmetric
@@ -420,7 +427,7 @@ __device__ __forceinline__ void decode_qblock(const uint32_t* W, uint32_t* P)
 {
     // constants live in SGPRs / one VGPR; the asm constraints keep them out of literals
     const uint32_t k_hi = Codebook<CB>::hi << 16;
-    const uint32_t k_add = CB == 0 ? Codebook<0>::add : 0u;
+    const uint32_t k_add = CB == 0 ? Codebook<0>::add : 0u;   // (CB 3 / 4: the mul1 hash, unscaled)
     const uint32_t k_lo = Codebook<CB>::lo;
     const uint32_t c6400 = 0x64006400u;
     decode_pairs_rec<BITS, CB, 0>(W, P, k_hi, k_add, k_lo, c6400);

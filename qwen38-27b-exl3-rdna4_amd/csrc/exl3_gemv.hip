@@ -325,8 +325,9 @@ int prerot_rows()
 // xr: the caller's scratch of groups * m * k fp16 for pre-rotated input (may be null)
 int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widths, int groups,
                 const int64_t* const* tabs, int64_t ldy, int m, int k, int K, int mcg, int mul1, void* ws,
-                size_t ws_bytes, void* stream, bool gated = false, void* xr = nullptr)
+                size_t ws_bytes, void* stream, bool gated = false, void* xr = nullptr, int approx = 0)
 {
+    if (approx && (gated || approx > 2)) return EXL3_EINVAL;
     if (gated && (groups != 2 || tabs || widths[0] != widths[1] || ldy < widths[0])) return EXL3_EINVAL;
     if (!x || groups < 1 || groups > EXL3_MAX_GROUPS || ldx < k) return EXL3_EINVAL;
     // the kernel moves fp16 in 16-byte groups of 8: x rows, y rows, suh and svh 16-byte aligned
@@ -400,6 +401,7 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
     a.ldy = ldy;
     a.counters = (uint32_t*) ws;
     a.part = (float*) ((char*) ws + COUNTER_BYTES);
+    if (approx) return launch_gemv_approx(a, K, 2 + approx, p.total_wgs, (hipStream_t) stream);
     return gated ? launch_gemv_gated(a, K, codebook_of(mcg, mul1), p.total_wgs, (hipStream_t) stream)
                  : launch_gemv_impl<false>(a, K, codebook_of(mcg, mul1), p.total_wgs, (hipStream_t) stream);
 }
@@ -490,6 +492,15 @@ int exl3_gemv_mr(const void* x, int64_t ldx, const void* trellis, void* y, int64
     if (!trellis || !y || !suh || !svh) return EXL3_EINVAL;
     GemvGroup g{(const uint32_t*) trellis, (const uint16_t*) suh, (const uint16_t*) svh, (uint16_t*) y};
     return gemv_common(x, ldx, &g, &n, 1, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream, false, A_had);
+}
+
+int exl3_gemv_mr_approx(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh,
+                        void* A_had, const void* svh, int m, int k, int n, int K, int mode, void* workspace,
+                        size_t ws_bytes, void* stream)
+{
+    if (!trellis || !y || !suh || !svh || mode < 1 || mode > 2) return EXL3_EINVAL;
+    GemvGroup g{(const uint32_t*) trellis, (const uint16_t*) suh, (const uint16_t*) svh, (uint16_t*) y};
+    return gemv_common(x, ldx, &g, &n, 1, nullptr, ldy, m, k, K, 0, 1, workspace, ws_bytes, stream, false, A_had, mode);
 }
 
 int exl3_gemv_mr_grouped(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,

@@ -229,6 +229,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     const GemvGroup gg = grp == 0 ? a.g[0] : grp == 1 ? a.g[1] : grp == 2 ? a.g[2] : a.g[3];
     const int w = older ? b - gg.o0 : gg.nold + (b - gg.y0);
     constexpr int MT = MT_ == 0 ? 1 : MT_;
+    // approximate mul1 routes (CB 3: affine, CB 4: int8 activations): the decoder emits 1024 + s
+    // unscaled; per (unit, row) the input rotation leaves in the LDS row's padding the row's input
+    // sum (affine) or its int8 scale q and integer sum (int8)
+    constexpr bool AFF = CB == 3, I8 = CB == 4;
+    constexpr float MUL1_K_INV = 0.00676727294921875f, MUL1_K_BIAS = -10.3828125f;   // fp16 0x1EEE, 0xC931
     const int G = gg.G, UPB = a.UPB, M = MT_ == 0 ? 1 : a.M;
     const int NB = gg.n / 128, NT = gg.n / 16, U = NB * UPB;
     const Split sp{U, G, gg.h, a.wa, a.wb, gg.d_sg, gg.d_u, a.d_wa, a.d_wb};
@@ -295,6 +300,56 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // which the reference's strict M = 1 gates assume (a last-place flip of one large output alone
     // is ~3e-3 of the output RMS).  Float32 butterflies measured no faster here: the prologue waits
     // on memory, not on the rotation's VALU work.
+    // Approximate routes: the row's input values (8 a lane, `width` lanes a row) -> the values the
+    // MFMA consumes, with the row's scalars written to the padding of its LDS row (lds_row: the
+    // row's first half, live: this lane group stores).  Every lane of the group takes part in the
+    // reductions.
+    auto approx_row = [&](u32x4 r, int width, uint16_t* lds_row, bool live) __attribute__((always_inline)) {
+        if constexpr (AFF || I8) {
+            const f16x8 h = __builtin_bit_cast(f16x8, r);
+            auto red = [&](float v, bool mx) __attribute__((always_inline)) {
+                for (int o = 1; o < width; o <<= 1) {
+                    const float w = __shfl_xor(v, o, width);
+                    v = mx ? fmaxf(v, w) : v + w;
+                }
+                return v;
+            };
+            float* pad = reinterpret_cast<float*>(lds_row + 128);
+            const bool leader = live && ((int) threadIdx.x & (width - 1)) == 0;
+            if constexpr (AFF) {
+                float sum = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) sum += (float) h[i];
+                sum = red(sum, false);
+                if (leader) pad[0] = sum;
+                return r;
+            } else {
+                // symmetric int8 of the slice: q = max(|a|, 1e-8) / 127, v = clamp(rint(a / q))
+                float mx = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) mx = fmaxf(mx, __builtin_fabsf((float) h[i]));
+                const float q = fmaxf(red(mx, true), 1e-8f) / 127.f;
+                f16x8 v;
+                float sum = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float t = fminf(fmaxf(__builtin_rintf((float) h[i] / q), -127.f), 127.f);
+                    v[i] = (f16) t;
+                    sum += t;
+                }
+                sum = red(sum, false);
+                if (leader) {
+                    pad[0] = q;
+                    pad[1] = sum;
+                }
+                return __builtin_bit_cast(u32x4, v);
+            }
+        } else {
+            (void) width; (void) lds_row; (void) live;
+            return r;
+        }
+    };
+
     // The prologue and the completion phase sit on every workgroup's critical path while other
     // workgroups on the same SIMDs run VALU-heavy decode loops: give them issue priority.
     __builtin_amdgcn_s_setprio(2);
@@ -367,11 +422,13 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 x0 = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * ldx + col);
                 if (!pre) s0 = *reinterpret_cast<gc_u32x4*>(gsuh + col);
             }
-            const u32x4 r = pre ? x0 : had128_x8<double>(x0, s0, true, u32x4{0u, 0u, 0u, 0u}, false, r_scale<double>());
-            if (i < njobs) {
-                int m, col;
-                job_src(c0, i, m, col);
-                *reinterpret_cast<u32x4*>(lds_a + ((i / M) * UROWS + m) * A_ROW + 8 * (threadIdx.x & 15)) = r;
+            u32x4 r = pre ? x0 : had128_x8<double>(x0, s0, true, u32x4{0u, 0u, 0u, 0u}, false, r_scale<double>());
+            {
+                int m = 0, col;
+                if (i < njobs) job_src(c0, i, m, col);
+                uint16_t* row = lds_a + ((i < njobs ? i / M : 0) * UROWS + m) * A_ROW;
+                r = approx_row(r, 16, row, i < njobs);
+                if (i < njobs) *reinterpret_cast<u32x4*>(row + 8 * (threadIdx.x & 15)) = r;
             }
             for (int i2 = i + 16; i2 - (threadIdx.x & 63) / 16 < njobs; i2 += 16) {
                 u32x4 xv = {0u, 0u, 0u, 0u}, sv = xv;
@@ -386,17 +443,24 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                         if (!pre) sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
                     }
                 }
-                const u32x4 r2 = pre ? xv : had128_x8<double>(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, r_scale<double>());
-                if (i2 < njobs)
-                    *reinterpret_cast<u32x4*>(lds_a + ((i2 / M) * UROWS + m) * A_ROW + 8 * (threadIdx.x & 15)) = r2;
+                u32x4 r2 = pre ? xv : had128_x8<double>(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, r_scale<double>());
+                uint16_t* row2 = lds_a + ((i2 < njobs ? i2 / M : 0) * UROWS + m) * A_ROW;
+                r2 = approx_row(r2, 16, row2, i2 < njobs);
+                if (i2 < njobs) *reinterpret_cast<u32x4*>(row2 + 8 * (threadIdx.x & 15)) = r2;
             }
         }
     };
     int c0 = ulo, c1 = min(ulo + a.chunk_units, uhi);
     if (wide) {
-        if (wave < nfirst)
-            *reinterpret_cast<uint32_t*>(lds_a + (wave * UROWS) * A_ROW + 2 * lane) =
-                had128_x2<double>(px.x, ps.x, true, 0u, false, r_scale<double>());
+        if (wave < nfirst) {
+            uint32_t r = had128_x2<double>(px.x, ps.x, true, 0u, false, r_scale<double>());
+            if constexpr (AFF || I8) {
+                // one row of 128 per wave, 2 values a lane: the same helper on a 64-lane group
+                const u32x4 r8 = approx_row(u32x4{r, 0u, 0u, 0u}, 64, lds_a + (wave * UROWS) * A_ROW, true);
+                r = r8.x;
+            }
+            *reinterpret_cast<uint32_t*>(lds_a + (wave * UROWS) * A_ROW + 2 * lane) = r;
+        }
     } else {
         rotate_chunk(c0, c1, px, ps, px2, ps2, true);
     }
@@ -419,6 +483,23 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // approximate routes: the block segment's input sums per accumulator row (affine), or the
+    // segment's folded sum of finished units (int8: acc holds one unit at a time)
+    float asum_seg[MT][4];
+    f32x4 acc_seg[2][MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) asum_seg[mt][v] = 0.f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc_seg[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // the padding scalars of unit row mt * 16 + 4 g + v of this lane (rows >= M: the zero row)
+    auto pad_of = [&](const uint16_t* unit_a, int mt, int v) __attribute__((always_inline)) {
+        const int row = mt * 16 + 4 * g + v;
+        return reinterpret_cast<const float*>(unit_a + (row < M ? row : M) * A_ROW + 128);
+    };
 
     const int colb = wave * 32 + (j >> 3) * 16 + (j & 7);    // + 8h: column of this lane in the block
     auto write_partial = [&](int cb) __attribute__((always_inline)) {
@@ -430,8 +511,11 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
                     const int m = mt * 16 + 4 * g + v;
+                    float val = acc[h][mt][v];
+                    if constexpr (AFF) val = MUL1_K_INV * acc[h][mt][v] + MUL1_K_BIAS * asum_seg[mt][v];
+                    if constexpr (I8) val = acc_seg[h][mt][v];
                     if (m < M)
-                        __hip_atomic_store(&slab[m * 128 + colb + 8 * h], acc[h][mt][v], __ATOMIC_RELAXED,
+                        __hip_atomic_store(&slab[m * 128 + colb + 8 * h], val, __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
                 }
     };
@@ -466,19 +550,49 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // sub-step i of the ring turn starting at unit u0 (slot i, d = i & 1)
     auto sub_step = [&](auto I, int u0, bool refill) __attribute__((always_inline)) {
         constexpr int i = decltype(I)::value;
+        const uint16_t* unit_a = lds_a + (u0 + i / 2 - c0) * UROWS * A_ROW;
         if (!(i & 1)) {
             if (left == 0) {                                  // a new 128-column block starts
                 write_partial(cb_cur);
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
 #pragma unroll
-                    for (int mt = 0; mt < MT; ++mt) acc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int mt = 0; mt < MT; ++mt) {
+                        acc[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                        acc_seg[h][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) asum_seg[mt][v] = 0.f;
                 ++cb_cur;
                 left = UPB;
             }
             --left;
+            if constexpr (AFF) {                              // the unit's input sums join the segment
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) asum_seg[mt][v] += pad_of(unit_a, mt, v)[0];
+            }
         }
-        step(Wr[i], lds_a + (u0 + i / 2 - c0) * UROWS * A_ROW, i & 1, refill);
+        step(Wr[i], unit_a, i & 1, refill);
+        if constexpr (I8) {
+            if (i & 1) {                                      // unit done: fold q (k_inv acc + k_bias sum v)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) {
+                        const float* pd = pad_of(unit_a, mt, v);
+                        const float q = pd[0], sv = pd[1];
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            acc_seg[h][mt][v] += q * (MUL1_K_INV * acc[h][mt][v] + MUL1_K_BIAS * sv);
+                            acc[h][mt][v] = 0.f;
+                        }
+                    }
+            }
+        }
         if ((i & 1) && refill) advance_load();
     };
     auto next_chunk = [&](int u0) __attribute__((always_inline)) {      // chunks hold whole ring turns
@@ -874,3 +988,5 @@ int launch_gemv_impl(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s
 
 // gated instantiations live in exl3_gemv_gated.hip
 int launch_gemv_gated(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s);
+// approximate mul1 instantiations (codebook ids 3 and 4) live in exl3_gemv_approx.hip
+int launch_gemv_approx(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s);

@@ -50,6 +50,7 @@ SIGNATURES = {
                                        _p]),
     "exl3_gemm_trellis_workspace_size": (_sz, [_i, _i, _ip, _i]),
     "exl3_gemm": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
+    "exl3_gemv_mr_approx": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "exl3_gemv_mr_noalloc": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _i, _i, _i, _i, _i, _i, _p]),
 }
 

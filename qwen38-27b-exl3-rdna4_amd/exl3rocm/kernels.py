@@ -209,6 +209,25 @@ def exl3_gemv_mr(A, B, C, suh, A_had, svh, K: int, mcg: bool, mul1: bool) -> int
                    "exl3_gemv_mr")
 
 
+APPROX_MODES = {"affine": 1, "int8": 2}
+
+
+def exl3_gemv_mr_approx(A, B, C, suh, A_had, svh, K: int, mode: str) -> int:
+    """The opt-in approximate mul1 GEMV: mode "affine" (unrounded weights) or "int8" (int8
+    activations, one scale per 128-input slice); see include/exl3_mi355x.h."""
+    _cuda(A, B, C, suh, svh)
+    _need(mode in APPROX_MODES, f"exl3_gemv_mr_approx: mode must be one of {sorted(APPROX_MODES)}")
+    x2, m, k = _rows(A)
+    n = svh.shape[0]
+    _need(B.shape[-1] == 16 * K, "exl3_gemv_mr_approx: trellis last dim must be 16*K")
+    ws = workspace(A.device, gemv_workspace_bytes(m, k, n, K))
+    xr = _rot_scratch(A_had, A.device, 1, m, k)
+    return L.check(L.lib().exl3_gemv_mr_approx(x2.data_ptr(), x2.stride(0) if m > 1 else k, B.data_ptr(), C.data_ptr(),
+                                               _ldy(C, n), suh.data_ptr(), xr.data_ptr() if xr is not None else None,
+                                               svh.data_ptr(), m, k, n, K, APPROX_MODES[mode], ws.data_ptr(),
+                                               ws.numel(), _stream(A)), "exl3_gemv_mr_approx")
+
+
 def exl3_gemv_mr_noalloc(A, B, C, suh, svh, K: int, mcg: bool, mul1: bool) -> int:
     """exl3_gemv_mr with its workspace in the library's per-GPU device array: no allocation here
     or in the library.  Calls that overlap on one GPU race (one stream at a time)."""

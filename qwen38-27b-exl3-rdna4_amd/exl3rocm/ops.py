@@ -7,7 +7,9 @@ One call computes one checkpoint tensor ("group"): y = had(had(x * suh) @ W_inne
 Routing by rows M:
   M <= EXL3_MR_MAX (32)  -> fused GEMV (input Hadamard, trellis decode + MFMA dot, split-K
                             reduction and output Hadamard in one launch); every row is bitwise
-                            equal to the M == 1 call of that row
+                            equal to the M == 1 call of that row; EXL3_GEMV_APPROX=affine|int8
+                            selects the opt-in approximate mul1 forms (unrounded weights, or
+                            int8 activations as the reference's EXL3_ROCM_GFX1201_INT8 path)
   M  > EXL3_MR_MAX       -> input Hadamard pass, then the prefill GEMM (trellis decoded into LDS,
                             fp16 MFMA, fp32 accumulate, output Hadamard and svh in its epilogue);
                             a fused module's groups share one GEMM launch; EXL3_PREFILL=recon takes
@@ -30,6 +32,9 @@ PREFILL_ROUTE = os.environ.get("EXL3_PREFILL", "fused")
 # linear_silu_mul at M <= MR_MAX: "unfused" (grouped GEMV + elementwise kernel) or "fused" (one
 # gated GEMV launch)
 GATED_ROUTE = os.environ.get("EXL3_GATED", "unfused")
+# opt-in approximate mul1 GEMV for M <= MR_MAX: "" (faithful, the default), "affine" (unrounded
+# weights) or "int8" (int8 activations, the reference's EXL3_ROCM_GFX1201_INT8 path)
+GEMV_APPROX = os.environ.get("EXL3_GEMV_APPROX", "")
 
 _wbuf: dict = {}
 
@@ -77,7 +82,11 @@ def _linear_into(x2, trellis, suh, svh, K, mcg, mul1, y):
     """One group into y ([M, n] view, unit column stride, any row stride)."""
     M, k = x2.shape
     n = svh.shape[0]
-    if M <= MR_MAX:
+    if M <= MR_MAX and GEMV_APPROX and mul1:
+        rc = E.exl3_gemv_mr_approx(x2, trellis, y, suh, None, svh, K, GEMV_APPROX)
+        if rc != 0:
+            raise RuntimeError(f"exl3rocm: approximate GEMV declined shape m={M} k={k} n={n} K={K}")
+    elif M <= MR_MAX:
         rc = E.exl3_gemv_mr(x2, trellis, y, suh, None, svh, K, mcg, mul1)
         if rc != 0:
             raise RuntimeError(f"exl3rocm: GEMV declined shape m={M} k={k} n={n} K={K}")
@@ -134,6 +143,14 @@ def exl3_linear_groups(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[t
     x2, k = _prep(x)
     M = x2.shape[0]
     ng = len(trellis)
+    if M <= MR_MAX and GEMV_APPROX and mul1:
+        # the approximate route runs each group as its own launch
+        y = torch.empty((M, sum(widths)), dtype=torch.float16, device=x.device)
+        n0 = 0
+        for g in range(ng):
+            _linear_into(x2, trellis[g], suh[g], svh[g], K[g], mcg, mul1, y[:, n0:n0 + widths[g]])
+            n0 += widths[g]
+        return y.view(*x.shape[:-1], n0)
     if M == 1 and ptrs_trellis is not None and ng <= _lib.MAX_GROUPS:
         y = torch.empty((ng, 1, widths[0]), dtype=torch.float16, device=x.device)
         E.exl3_mgemm(x2.view(1, 1, k), ptrs_trellis, y, ptrs_suh, None, ptrs_svh, K[0], mcg, mul1)

@@ -18,6 +18,8 @@ What is pinned (reference function, file:line):
 * ``gemv_mul1`` (:307, faithful=True) on several (k, n, bits, cb), plus the
   K=N=4096 4-bpw mcg layer of the headline CPU configuration, whose inputs are
   regenerated from the counter RNG (``exl3rocm.synth``) rather than stored.
+* ``quantize_splats`` (:357) on ties, clamps and random data, plain and residual
+* ``gemv_int8_reference`` (:374) on two layers, plain and residual, global q
 
 Usage: python tests/golden/make_golden.py [--reference /root/reference]
 """
@@ -130,6 +132,32 @@ def main() -> int:
     out["config0_W_sha"] = np.frombuffer(
         hashlib.sha256(f16_bits(O.decode_trellis(tr, bits, cb)).tobytes()).digest(), dtype=np.uint8)
     meta["config0"] = {"k": k, "n": n, "bits": bits, "cb": cb, "keys": ["config0", 0, "trellis|suh|svh|x"]}
+
+    # --- int8 activation path (quantize_splats, gemv_int8_reference) ---------------
+    qa = np.concatenate([np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, 127.5, 200.0, -200.0, 0.0, 1e-9]),
+                         rng.standard_normal(116) * 40.0])
+    for res in (False, True):
+        v, v2, s1, s2 = O.quantize_splats(qa, 1.0, residual=res)
+        out[f"qs_v_r{int(res)}"] = np.asarray(v, dtype=np.int64)
+        if res:
+            out["qs_v2_r1"] = np.asarray(v2, dtype=np.int64)
+        out[f"qs_sums_r{int(res)}"] = np.array([s1, s2], dtype=np.int64)
+    out["qs_a"] = qa
+    for idx, (k, n, bits) in enumerate([(256, 128, 3), (512, 256, 4), (384, 256, 4)]):
+        tr = rng.integers(0, 65536, size=(k // 16, n // 16, 16 * bits), dtype=np.uint16)
+        ah = rng.standard_normal(k) * 0.7
+        if idx == 2:
+            # every 128-input slice holds the global maximum magnitude: a per-slice scale equals q
+            ah = np.clip(ah, -2.5, 2.5)
+            ah[::128] = 3.0 * np.sign(rng.standard_normal(k // 128))
+        sv = (np.sign(rng.standard_normal(n)) * np.exp(0.25 * rng.standard_normal(n))).astype(np.float16)
+        S = O.trellis_states(tr, bits)
+        q = max(np.abs(ah).max(), 1e-8) / 127.0
+        pre = f"int8_{idx}_"
+        out[pre + "trellis"], out[pre + "a_had"], out[pre + "svh"] = tr, ah, sv
+        for res in (False, True):
+            out[pre + f"y_r{int(res)}"] = O.gemv_int8_reference(ah, S, q, sv.astype(np.float64), residual=res)
+        meta.setdefault("int8_cases", []).append({"name": pre, "k": k, "n": n, "bits": bits, "q": q})
 
     np.savez_compressed(args.out, **out)
     with open(os.path.splitext(args.out)[0] + ".json", "w") as f:

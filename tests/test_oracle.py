@@ -227,3 +227,80 @@ def test_synth_is_deterministic_and_distributed():
     assert 0.45 < np.mean(s > 0) < 0.55
     h = synth.activations(7, 1, 10000, heavy_tail=True).astype(np.float64)
     assert 0.3 < np.mean(np.abs(h) > 6) * 100 < 3.0      # ~1% of channels scaled x20
+
+
+# ---------------------------------------------------------------------------------------------
+# approximate mul1 forms: unrounded weights, int8 activations (reference exl3_oracle.py:357-412)
+# ---------------------------------------------------------------------------------------------
+def test_affine_weights_round_to_the_mul1_table(golden):
+    """The unrounded mul1 weights, rounded once to fp16, are the reference's whole mul1 table."""
+    import hashlib
+    g, meta = golden
+    w = O.mul1_affine_weights(np.arange(65536)).astype(np.float16).view(np.uint16)
+    assert hashlib.sha256(w.tobytes()).hexdigest() == meta["cb2_sha256"]
+    assert np.array_equal(w, O.codebook_f16(np.arange(65536), 2).view(np.uint16))
+
+
+def test_quantize_splats_matches_reference_vectors(golden):
+    g, _ = golden
+    a = g["qs_a"]
+    for res in (0, 1):
+        v, v2, s1, s2 = O.quantize_splats(a, 1.0, residual=bool(res))
+        assert np.array_equal(v, g[f"qs_v_r{res}"])
+        assert [s1, s2] == list(g[f"qs_sums_r{res}"])
+        if res:
+            assert np.array_equal(v2, g["qs_v2_r1"])
+    v, _, _, _ = O.quantize_splats(np.array([0.5, 1.5, 2.5, -2.5, 300.0, -300.0]), 1.0)
+    assert list(v) == [0, 2, 2, -2, 127, -127]                 # round half to even, clamp at 127
+
+
+def test_gemv_int8_reference_matches_reference_vectors(golden):
+    g, meta = golden
+    for case in meta["int8_cases"]:
+        pre, bits = case["name"], case["bits"]
+        S = O.states_matrix(g[pre + "trellis"], bits)
+        for res in (0, 1):
+            y = O.gemv_int8_reference(g[pre + "a_had"], S, case["q"], g[pre + "svh"].astype(np.float64), bool(res))
+            np.testing.assert_allclose(y, g[pre + f"y_r{res}"], rtol=1e-12, atol=1e-12)
+
+
+def test_sliced_int8_equals_global_when_every_slice_holds_the_max(golden):
+    """The kernels' per-slice scale form against the reference's global-scale vectors, on the case
+    whose every 128-input slice holds the global maximum (so both scales agree): equal up to the
+    kernels' fp16 staging of C and y."""
+    g, meta = golden
+    case = [c for c in meta["int8_cases"] if c["name"] == "int8_2_"][0]
+    a = g["int8_2_a_had"]
+    assert np.allclose(O.slice_scales(a), case["q"])
+    y = O.linear_approx_rotated(a, g["int8_2_trellis"], case["bits"], g["int8_2_svh"], "int8")[0]
+    ref = g["int8_2_y_r0"]
+    assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 1e-3
+
+
+def test_int8_is_lossless_on_exactly_quantized_input():
+    """Rotated inputs that are q * integers with |v| <= 127 and 127 q in every slice quantize
+    without loss: the int8 form equals the affine form exactly."""
+    rng = np.random.default_rng(8)
+    k, n, bits = 256, 128, 4
+    q = 2.0 ** -5
+    v = rng.integers(-120, 121, size=(3, k)).astype(np.float64)
+    v[:, ::128] = 127.0
+    a = v * q
+    tr = rng.integers(0, 65536, size=(k // 16, n // 16, 16 * bits), dtype=np.uint16)
+    sv = np.ones(n, dtype=np.float16)
+    ya = O.linear_approx_rotated(a, tr, bits, sv, "affine")
+    yi = O.linear_approx_rotated(a, tr, bits, sv, "int8")
+    assert np.array_equal(ya, yi)
+
+
+def test_affine_form_is_near_the_faithful_linear():
+    rng = np.random.default_rng(9)
+    k, n, bits = 512, 256, 4
+    tr = rng.integers(0, 65536, size=(k // 16, n // 16, 16 * bits), dtype=np.uint16)
+    x = rng.standard_normal((2, k)).astype(np.float16)
+    su = np.ones(k, dtype=np.float16)
+    sv = np.ones(n, dtype=np.float16)
+    yf = O.linear(x, tr, bits, su, sv, 2)
+    ya = O.linear_approx(x, tr, bits, su, sv, "affine")
+    yi = O.linear_approx(x, tr, bits, su, sv, "int8")
+    assert O.rel_l2(ya, yf) < 1e-3 and 0 < O.rel_l2(yi, yf) < 2e-2
