@@ -225,10 +225,12 @@ def approx_m1(torch, sets, x5120, x17408, reps=64):
 
 
 def gated_mlp(torch, sets, x5120, ms=(1, 8), reps=32):
-    """The MLP input of config 1: gate/up + SiLU-and-mul fused into one GEMV launch
-    (exl3_gemv_silu_mul) against the unfused pair (linear_groups, then the elementwise kernel,
-    linear_silu_mul's default route); mean duration per call from a graph of `reps` calls over
-    the weight copies."""
+    """The MLP of config 1 (gate/up, SiLU-and-mul, down) three ways, duration per MLP from a graph
+    of `reps` MLPs over the weight copies (median of 7 interleaved rounds of 3 replays):
+      unfused_us: linear_groups(gate, up), the elementwise SiLU-and-mul kernel, linear(down);
+      silu_in_us: linear_groups(gate, up), then silu_mul_linear (the down GEMV forms the
+                  activation as its input loads: exl3_gemv_silu_in), two launches;
+      gated_us:   exl3_gemv_silu_mul (gate/up and the activation in one launch), linear(down)."""
     from exl3rocm import kernels as E
     ops = torch.ops.exl3rocm
     n = INTER
@@ -238,20 +240,29 @@ def gated_mlp(torch, sets, x5120, ms=(1, 8), reps=32):
         x = x5120.expand(m, HIDDEN).contiguous()
         act = torch.empty(m, n, dtype=torch.float16, device="cuda")
 
-        def fused(ls):
+        def gate_up(ls):
+            w = ls.w
+            ptrs = ls.gu_ptrs if m == 1 else [None] * 3
+            return ops.linear_groups(x, [w["gate"][0], w["up"][0]], [w["gate"][1], w["up"][1]],
+                                     [w["gate"][2], w["up"][2]], [ls.bits, ls.bits], ls.mcg, ls.mul1, *ptrs)
+
+        def unfused(ls):
+            gu = gate_up(ls)
+            E.silu_mul(gu[:, :n], gu[:, n:], act)
+            ops.linear(act, *ls.w["down"], ls.bits, ls.mcg, ls.mul1)
+
+        def silu_in(ls):
+            ops.silu_mul_linear(gate_up(ls), *ls.w["down"], ls.bits, ls.mcg, ls.mul1)
+
+        def gated(ls):
             w = ls.w
             E.exl3_gemv_silu_mul(x, [w["gate"][0], w["up"][0]], act, [w["gate"][1], w["up"][1]],
                                  [w["gate"][2], w["up"][2]], ls.bits, ls.mcg, ls.mul1)
+            ops.linear(act, *w["down"], ls.bits, ls.mcg, ls.mul1)
 
-        def unfused(ls):
-            w = ls.w
-            ptrs = ls.gu_ptrs if m == 1 else [None] * 3
-            gu = ops.linear_groups(x, [w["gate"][0], w["up"][0]], [w["gate"][1], w["up"][1]],
-                                   [w["gate"][2], w["up"][2]], [ls.bits, ls.bits], ls.mcg, ls.mul1, *ptrs)
-            E.silu_mul(gu[:, :n], gu[:, n:], act)
-
-        row = {}
-        for tag, fn in (("fused_us", fused), ("unfused_us", unfused)):
+        forms = (("unfused_us", unfused), ("silu_in_us", silu_in), ("gated_us", gated))
+        graphs = {}
+        for tag, fn in forms:
             with torch.cuda.stream(s):
                 for ls in sets:
                     fn(ls)
@@ -260,16 +271,25 @@ def gated_mlp(torch, sets, x5120, ms=(1, 8), reps=32):
             with torch.cuda.graph(g, stream=s):
                 for r in range(reps):
                     fn(sets[r % len(sets)])
-            with torch.cuda.stream(s):
-                g.replay()
-                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                e0.record(s)
-                for _ in range(3):
-                    g.replay()
-                e1.record(s)
-            s.synchronize()
-            row[tag] = round(e0.elapsed_time(e1) * 1e3 / (3 * reps), 2)
-            del g
+            graphs[tag] = g
+        # the forms' graphs replayed in turn, 7 rounds: the median per form (boxes drift by a few
+        # percent over seconds, more than the forms differ)
+        times = {tag: [] for tag, _ in forms}
+        with torch.cuda.stream(s):
+            for tag, _ in forms:
+                graphs[tag].replay()
+            for _ in range(7):
+                for tag, _ in forms:
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record(s)
+                    for _ in range(3):
+                        graphs[tag].replay()
+                    e1.record(s)
+                    times[tag].append((e0, e1))
+        s.synchronize()
+        row = {tag: round(float(np.median([a.elapsed_time(b) for a, b in ev])) * 1e3 / (3 * reps), 2)
+               for tag, ev in times.items()}
+        del graphs
         out[f"m{m}"] = row
     return out
 
@@ -541,8 +561,8 @@ def main() -> int:
     extra["per_shape_m1"] = per_shape_gemv(torch, sets, x5120, x17408)
     log("approximate mul1 GEMV (opt-in affine / int8 routes)")
     extra["approx_m1"] = approx_m1(torch, sets, x5120, x17408)
-    log("gated MLP input (gate/up + SiLU-and-mul)")
-    extra["gated_mlp"] = gated_mlp(torch, sets, x5120)
+    log("gated MLP (gate/up, SiLU-and-mul, down) three ways")
+    extra["gated_mlp"] = gated_mlp(torch, sets, x5120, ms=(1, 2, 4, 8, 16))
     if not args.no_sweep:
         log("small-batch crossover")
         extra["config3_small_batch"] = small_batch(torch, sets)

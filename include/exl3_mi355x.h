@@ -191,6 +191,18 @@ int exl3_gemv_silu_mul(const void* x, int64_t ldx, const void* const* trellis, v
 int exl3_silu_mul(const void* gate, const void* up, int64_t ld_in, void* out, int64_t ld_out, int rows, int n,
                   void* stream);
 
+/* Gated MLP output, 1 <= m <= 32: exl3_gemv_mr over the input x = fp16(fp16(silu(gate)) * up)
+ * (the exl3_silu_mul roundings), formed as the rows load; gate and up rows ld_in apart (a gated
+ * module's grouped [m, 2n] output: gate = y, up = y + n, ld_in = 2n).  Bitwise equal to
+ * exl3_silu_mul followed by exl3_gemv_mr.  A_had (m * k, optional) as exl3_gemv_mr, but from
+ * m >= 4 (EXL3_GEMV_SILU_PREROT_M): it receives the rotated activation.  No counterpart in the reference: its down
+ * projection reads the SiluAndMul output (reference docs/EFFICIENCY_INVESTIGATION.md:36-66
+ * proposes fusing the activation).  Callers: exl3rocm's silu_mul_linear op (the down projection
+ * of a decode step).  Removes the activation launch and its [m, n] round trip. */
+int exl3_gemv_silu_in(const void* gate, const void* up, int64_t ld_in, const void* trellis, void* y, int64_t ldy,
+                      const void* suh, void* A_had, const void* svh, int m, int k, int n, int K, int mcg, int mul1,
+                      void* workspace, size_t ws_bytes, void* stream);
+
 /* Grouped M == 1 linear over device int64 pointer tables (one entry per group), output
  * (groups, 1, n) == the concatenated row.
  * Replaces `exl3_mgemm(x, ptrs_trellis, y, ptrs_suh, xh, ptrs_svh, ...)` (reference ops.py:137-138). */

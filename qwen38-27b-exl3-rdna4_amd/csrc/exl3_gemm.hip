@@ -22,7 +22,7 @@ using namespace exl3;
 
 // had_r_128 of one input into several outputs in one launch (exl3_gemv.hip)
 int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, int rows, int cols, const void* const* pre,
-               int groups, const void* post, float scale, void* stream, bool exact);
+               int groups, const void* post, float scale, void* stream, bool exact, const void* in_up);
 
 namespace {
 
@@ -767,7 +767,7 @@ int gemm_trellis_common(const void* x, int64_t ldx, const void* const* trellis, 
         svs[i] = (const uint16_t*) svh[i];
     }
     // the groups' input transforms (one x, each group's suh) in one launch
-    const int rc = launch_had(x, ldx, xo, k, m, k, suh, groups, nullptr, 1.0f, s, false);
+    const int rc = launch_had(x, ldx, xo, k, m, k, suh, groups, nullptr, 1.0f, s, false, nullptr);
     if (rc) return rc;
     const int cb = codebook_of(mcg, mul1);
     switch (K) {

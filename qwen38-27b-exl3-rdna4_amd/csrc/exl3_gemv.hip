@@ -98,9 +98,11 @@ struct HadGroups {
 // T: the butterflies' element type (double: exl3_had_r_128 and the GEMV's pre-rotation, the same
 // values as the GEMV's in-kernel transforms; float: the prefill's input transforms and
 // exl3_had_r_128_f32, the same values as the prefill epilogue's)
+// in_up (may be null): the input rows are fp16(fp16(silu(in)) * in_up) (a gated MLP's activation)
 template <class T>
-__global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ in, int64_t ld_in, HadGroups hg, int64_t ld_out,
-                                                  int rows, int cols, const uint16_t* __restrict__ post, T scale)
+__global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ in, const uint16_t* __restrict__ in_up,
+                                                  int64_t ld_in, HadGroups hg, int64_t ld_out, int rows, int cols,
+                                                  const uint16_t* __restrict__ post, T scale)
 {
     const int gy = blockIdx.y;
     const uint16_t* pre = gy == 0 ? hg.pre[0] : gy == 1 ? hg.pre[1] : gy == 2 ? hg.pre[2] : hg.pre[3];
@@ -118,6 +120,7 @@ __global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ i
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             v[c] = *reinterpret_cast<const u32x4*>(in + row * ld_in + col + 8 * c);
+            if (in_up) v[c] = silu_mul_x8(v[c], *reinterpret_cast<const u32x4*>(in_up + row * ld_in + col + 8 * c));
             if (pre) pv[c] = *reinterpret_cast<const u32x4*>(pre + col + 8 * c);
             if (post) qv[c] = *reinterpret_cast<const u32x4*>(post + col + 8 * c);
         }
@@ -134,8 +137,9 @@ __global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ i
 // had_r_128 of one input into `groups` outputs, group i scaled by pre[i] (may be null): one launch
 // (the prefill's input transforms of a fused module); exact: float64 butterflies, else float32
 int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, int rows, int cols, const void* const* pre,
-               int groups, const void* post, float scale, void* stream, bool exact)
+               int groups, const void* post, float scale, void* stream, bool exact, const void* in_up)
 {
+    if (((uintptr_t) in_up) & 15) return EXL3_EINVAL;
     if (!in || !out || rows < 0 || cols % 128 || cols < 128 || ld_in < cols || ld_out < cols || ld_in % 8 || ld_out % 8 ||
         groups < 1 || groups > EXL3_MAX_GROUPS || (((uintptr_t) in) & 15) || (((uintptr_t) post) & 15))
         return EXL3_EINVAL;
@@ -150,11 +154,13 @@ int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, 
     const int64_t jobs = (int64_t) rows * (cols / 128);           // 8 lanes each
     const dim3 grid((unsigned) ((jobs + 31) / 32), (unsigned) groups);
     if (exact)
-        hipLaunchKernelGGL(had_kernel<double>, grid, dim3(256), 0, (hipStream_t) stream, (const uint16_t*) in, ld_in, hg, ld_out,
-                           rows, cols, (const uint16_t*) post, R_SCALE * (double) scale);
+        hipLaunchKernelGGL(had_kernel<double>, grid, dim3(256), 0, (hipStream_t) stream, (const uint16_t*) in,
+                           (const uint16_t*) in_up, ld_in, hg, ld_out, rows, cols, (const uint16_t*) post,
+                           R_SCALE * (double) scale);
     else
-        hipLaunchKernelGGL(had_kernel<float>, grid, dim3(256), 0, (hipStream_t) stream, (const uint16_t*) in, ld_in, hg, ld_out,
-                           rows, cols, (const uint16_t*) post, (float) (R_SCALE * (double) scale));
+        hipLaunchKernelGGL(had_kernel<float>, grid, dim3(256), 0, (hipStream_t) stream, (const uint16_t*) in,
+                           (const uint16_t*) in_up, ld_in, hg, ld_out, rows, cols, (const uint16_t*) post,
+                           (float) (R_SCALE * (double) scale));
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 
@@ -322,11 +328,23 @@ int prerot_rows()
     return v;
 }
 
+// The same for a SiLU input (EXL3_GEMV_SILU_PREROT_M overrides): there the pass takes the place
+// of the activation kernel the caller would otherwise run, while rotating in LDS repeats the SiLU
+// in every workgroup sharing a k-range (config-1 down projection, MLP time against the
+// two-launch form: in LDS -2.4% at 2 rows, +0.8% at 4, +2.5% at 8; the pass +0.8% at 4, -2.2% at 8).
+int silu_prerot_rows()
+{
+    static const int v = env_int("EXL3_GEMV_SILU_PREROT_M", 4);
+    return v;
+}
+
 // xr: the caller's scratch of groups * m * k fp16 for pre-rotated input (may be null)
 int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widths, int groups,
                 const int64_t* const* tabs, int64_t ldy, int m, int k, int K, int mcg, int mul1, void* ws,
-                size_t ws_bytes, void* stream, bool gated = false, void* xr = nullptr, int approx = 0)
+                size_t ws_bytes, void* stream, bool gated = false, void* xr = nullptr, int approx = 0,
+                const void* x_up = nullptr)
 {
+    if (x_up && (gated || tabs || approx || (((uintptr_t) x_up) & 15))) return EXL3_EINVAL;
     if (approx && (gated || approx > 2)) return EXL3_EINVAL;
     if (gated && (groups != 2 || tabs || widths[0] != widths[1] || ldy < widths[0])) return EXL3_EINVAL;
     if (!x || groups < 1 || groups > EXL3_MAX_GROUPS || ldx < k) return EXL3_EINVAL;
@@ -354,7 +372,8 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
     GemvArgs a{};
     a.x = (const uint16_t*) x;
     a.ldx = ldx;
-    if (xr && !tabs && m > 1 && m >= prerot_rows()) {
+    a.x_up = (const uint16_t*) x_up;
+    if (xr && !tabs && m > 1 && m >= (x_up ? silu_prerot_rows() : prerot_rows())) {
         if (((uintptr_t) xr) & 15) return EXL3_EINVAL;
         // every group's rotated rows in one launch
         void* outs[EXL3_MAX_GROUPS];
@@ -363,9 +382,10 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
             outs[i] = (uint16_t*) xr + (int64_t) i * m * k;
             pres[i] = gs[i].suh;
         }
-        const int rc = launch_had(x, ldx, outs, k, m, k, pres, groups, nullptr, 1.0f, stream, true);
+        const int rc = launch_had(x, ldx, outs, k, m, k, pres, groups, nullptr, 1.0f, stream, true, x_up);
         if (rc != EXL3_OK) return rc;
         a.xr = (const uint16_t*) xr;
+        a.x_up = nullptr;                       // the activation is in the pre-rotated rows
     }
     for (int i = 0; i < groups; ++i) {
         a.g[i] = gs[i];
@@ -402,8 +422,9 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
     a.counters = (uint32_t*) ws;
     a.part = (float*) ((char*) ws + COUNTER_BYTES);
     if (approx) return launch_gemv_approx(a, K, 2 + approx, p.total_wgs, (hipStream_t) stream);
+    if (a.x_up) return launch_gemv_silu_in(a, K, codebook_of(mcg, mul1), p.total_wgs, (hipStream_t) stream);
     return gated ? launch_gemv_gated(a, K, codebook_of(mcg, mul1), p.total_wgs, (hipStream_t) stream)
-                 : launch_gemv_impl<false>(a, K, codebook_of(mcg, mul1), p.total_wgs, (hipStream_t) stream);
+                 : launch_gemv_impl<FORM_PLAIN>(a, K, codebook_of(mcg, mul1), p.total_wgs, (hipStream_t) stream);
 }
 
 }  // namespace
@@ -501,6 +522,16 @@ int exl3_gemv_mr_approx(const void* x, int64_t ldx, const void* trellis, void* y
     if (!trellis || !y || !suh || !svh || mode < 1 || mode > 2) return EXL3_EINVAL;
     GemvGroup g{(const uint32_t*) trellis, (const uint16_t*) suh, (const uint16_t*) svh, (uint16_t*) y};
     return gemv_common(x, ldx, &g, &n, 1, nullptr, ldy, m, k, K, 0, 1, workspace, ws_bytes, stream, false, A_had, mode);
+}
+
+int exl3_gemv_silu_in(const void* gate, const void* up, int64_t ld_in, const void* trellis, void* y, int64_t ldy,
+                      const void* suh, void* A_had, const void* svh, int m, int k, int n, int K, int mcg, int mul1,
+                      void* workspace, size_t ws_bytes, void* stream)
+{
+    if (!gate || !up || !trellis || !y || !suh || !svh) return EXL3_EINVAL;
+    GemvGroup g{(const uint32_t*) trellis, (const uint16_t*) suh, (const uint16_t*) svh, (uint16_t*) y};
+    return gemv_common(gate, ld_in, &g, &n, 1, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream, false, A_had,
+                       0, up);
 }
 
 int exl3_gemv_mr_grouped(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,
@@ -631,7 +662,7 @@ int exl3_had_r_128(const void* in, int64_t ld_in, void* out, int64_t ld_out, int
 {
     void* const outs[1] = {out};
     const void* const pres[1] = {pre};
-    return launch_had(in, ld_in, outs, ld_out, rows, cols, pres, 1, post, scale, stream, true);
+    return launch_had(in, ld_in, outs, ld_out, rows, cols, pres, 1, post, scale, stream, true, nullptr);
 }
 
 int exl3_had_r_128_f32(const void* in, int64_t ld_in, void* out, int64_t ld_out, int rows, int cols, const void* pre,
@@ -639,7 +670,7 @@ int exl3_had_r_128_f32(const void* in, int64_t ld_in, void* out, int64_t ld_out,
 {
     void* const outs[1] = {out};
     const void* const pres[1] = {pre};
-    return launch_had(in, ld_in, outs, ld_out, rows, cols, pres, 1, post, scale, stream, false);
+    return launch_had(in, ld_in, outs, ld_out, rows, cols, pres, 1, post, scale, stream, false, nullptr);
 }
 
 }  // extern "C"

@@ -6,7 +6,7 @@
 template <int BITS>
 static int launch_approx_bits(const GemvArgs& a, int cb, int wgs, hipStream_t s)
 {
-    return cb == 3 ? launch_gemv_m<BITS, 3, false>(a, wgs, s) : launch_gemv_m<BITS, 4, false>(a, wgs, s);
+    return cb == 3 ? launch_gemv_m<BITS, 3, FORM_PLAIN>(a, wgs, s) : launch_gemv_m<BITS, 4, FORM_PLAIN>(a, wgs, s);
 }
 
 int launch_gemv_approx(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s)

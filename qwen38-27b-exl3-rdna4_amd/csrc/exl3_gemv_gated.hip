@@ -4,5 +4,5 @@
 
 int launch_gemv_gated(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s)
 {
-    return launch_gemv_impl<true>(a, bits, cb, wgs, s);
+    return launch_gemv_impl<FORM_GATED>(a, bits, cb, wgs, s);
 }

@@ -76,6 +76,8 @@ struct GemvArgs {
     const uint16_t* xr;        // or, when set, every group's rotated input fp16(Had128(fp16(x * suh))):
                                // group i's rows at xr + i * M * k, k apart (computed by one pass per
                                // group before the launch)
+    const uint16_t* x_up;      // FORM_SILU_IN: the input rows are fp16(fp16(silu(x)) * x_up), x_up rows
+                               // ldx apart as x's (a gated MLP's activation, computed here)
     int64_t ldx;
     GemvGroup g[EXL3_MAX_GROUPS];
     const int64_t* tab_trellis; // optional device pointer tables (grouped M=1 `mgemm` form): they
@@ -196,12 +198,17 @@ struct Split {
 
 // Two workgroups (8 waves) per CU are resident at once: up to 256 registers per lane, enough for
 // a ring deep enough that one wave alone keeps its SIMD busy.
-// MT: 16-row MFMA tiles of the input rows (0: exactly one row, a compile-time M).  GATED: groups
-// 0 (gate) and 1 (up) of equal width; the workgroup completing a block of both writes
-// fp16(fp16(silu(gate)) * up) to g[0].y instead of the two outputs.
-template <int BITS, int CB, int MT_, bool GATED>
+// MT: 16-row MFMA tiles of the input rows (0: exactly one row, a compile-time M).  FORM:
+//   FORM_PLAIN   the EXL3 linear of each group;
+//   FORM_GATED   groups 0 (gate) and 1 (up) of equal width; the workgroup completing a block of
+//                both writes fp16(fp16(silu(gate)) * up) to g[0].y instead of the two outputs;
+//   FORM_SILU_IN the input rows are fp16(fp16(silu(x)) * x_up), formed as they load.
+enum { FORM_PLAIN = 0, FORM_GATED = 1, FORM_SILU_IN = 2 };
+
+template <int BITS, int CB, int MT_, int FORM>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_SIMD, WAVES_PER_SIMD))) gemv_kernel(GemvArgs a)
 {
+    constexpr bool GATED = FORM == FORM_GATED;
     extern __shared__ __align__(16) uint16_t smem[];
     __shared__ int s_last[256];
     __shared__ int s_list[256];
@@ -260,6 +267,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // the input rows: x (rotated here, per workgroup) or the group's pre-rotated rows
     const bool pre = MT_ != 0 && a.xr != nullptr;
     gc_u16* const gx = as_global(pre ? a.xr + (int64_t) grp * M * a.k : a.x);
+    // gated-MLP input: the activation silu(gate) * up is formed from the two rows as they load
+    constexpr bool silu_in = FORM == FORM_SILU_IN;
+    gc_u16* const gxu = as_global(a.x_up);
     const int64_t ldx = pre ? (int64_t) a.k : a.ldx;
     // outputs go out as write-through (device-scope) stores: no dirty output lines are left in L2
     // for the end-of-kernel writeback (~0.2 us off the small launches)
@@ -357,7 +367,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // ---- first input chunk: the x / suh loads of its first two 16-lane job passes go out before
     // the trellis ring (a pass requested after the ring waits behind every workgroup's ring)
     const int nfirst = min(a.chunk_units, uhi - ulo) * M;
-    u32x4 px = {0u, 0u, 0u, 0u}, ps = px, px2 = px, ps2 = px;
+    u32x4 px = {0u, 0u, 0u, 0u}, ps = px, px2 = px, ps2 = px, pu = px, pu2 = px;
     // a single row of at most 4 jobs: one job per wave, two columns a lane (had128_x2, a fourth
     // of the 16-lane transform's latency)
     const bool wide = MT_ == 0 && nfirst <= 4;
@@ -366,6 +376,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             const int u = ulo + wave;
             const int col = (u - (u / UPB) * UPB) * 128 + 2 * lane;
             px.x = *reinterpret_cast<gc_u32*>(gx + col);
+            if (silu_in) pu.x = *reinterpret_cast<gc_u32*>(gxu + col);
             ps.x = *reinterpret_cast<gc_u32*>(gsuh + col);
         }
     } else {
@@ -374,12 +385,14 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             int m, col;
             job_src(ulo, i, m, col);
             px = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * ldx + col);
+            if (silu_in) pu = *reinterpret_cast<gc_u32x4*>(gxu + (int64_t) m * ldx + col);
             if (!pre) ps = *reinterpret_cast<gc_u32x4*>(gsuh + col);
         }
         if (i + 16 < nfirst) {
             int m, col;
             job_src(ulo, i + 16, m, col);
             px2 = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * ldx + col);
+            if (silu_in) pu2 = *reinterpret_cast<gc_u32x4*>(gxu + (int64_t) m * ldx + col);
             if (!pre) ps2 = *reinterpret_cast<gc_u32x4*>(gsuh + col);
         }
     }
@@ -410,9 +423,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     };
     static_for(std::make_integer_sequence<int, RING / 2>{}, fill);
     // rotated input of units [c0, c1) -> LDS; with have_first the lane's first two 16-lane jobs use
-    // (x0, s0) and (x1, s1)
-    auto rotate_chunk = [&](int c0, int c1, u32x4 x0, u32x4 s0, u32x4 x1, u32x4 s1, bool have_first)
-        __attribute__((always_inline)) {
+    // (x0, s0, u0) and (x1, s1, u1) (u: the up rows of a gated-MLP input)
+    auto rotate_chunk = [&](int c0, int c1, u32x4 x0, u32x4 s0, u32x4 x1, u32x4 s1, u32x4 u0, u32x4 u1,
+                            bool have_first) __attribute__((always_inline)) {
         const int njobs = (c1 - c0) * M;
         const int i = threadIdx.x >> 4;
         if (i - (threadIdx.x & 63) / 16 < njobs) {            // waves with a job (whole 16-lane groups)
@@ -420,8 +433,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 int m, col;
                 job_src(c0, i, m, col);
                 x0 = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * ldx + col);
+                if (silu_in) u0 = *reinterpret_cast<gc_u32x4*>(gxu + (int64_t) m * ldx + col);
                 if (!pre) s0 = *reinterpret_cast<gc_u32x4*>(gsuh + col);
             }
+            if (silu_in) x0 = silu_mul_x8(x0, u0);
             u32x4 r = pre ? x0 : had128_x8<double>(x0, s0, true, u32x4{0u, 0u, 0u, 0u}, false, r_scale<double>());
             {
                 int m = 0, col;
@@ -431,18 +446,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 if (i < njobs) *reinterpret_cast<u32x4*>(row + 8 * (threadIdx.x & 15)) = r;
             }
             for (int i2 = i + 16; i2 - (threadIdx.x & 63) / 16 < njobs; i2 += 16) {
-                u32x4 xv = {0u, 0u, 0u, 0u}, sv = xv;
+                u32x4 xv = {0u, 0u, 0u, 0u}, sv = xv, uv = xv;
                 int m = 0, col = 0;
                 if (i2 < njobs) {
                     job_src(c0, i2, m, col);
                     if (have_first && i2 == i + 16) {
                         xv = x1;
                         sv = s1;
+                        uv = u1;
                     } else {
                         xv = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * ldx + col);
+                        if (silu_in) uv = *reinterpret_cast<gc_u32x4*>(gxu + (int64_t) m * ldx + col);
                         if (!pre) sv = *reinterpret_cast<gc_u32x4*>(gsuh + col);
                     }
                 }
+                if (silu_in) xv = silu_mul_x8(xv, uv);
                 u32x4 r2 = pre ? xv : had128_x8<double>(xv, sv, true, u32x4{0u, 0u, 0u, 0u}, false, r_scale<double>());
                 uint16_t* row2 = lds_a + ((i2 < njobs ? i2 / M : 0) * UROWS + m) * A_ROW;
                 r2 = approx_row(r2, 16, row2, i2 < njobs);
@@ -453,7 +471,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     int c0 = ulo, c1 = min(ulo + a.chunk_units, uhi);
     if (wide) {
         if (wave < nfirst) {
-            uint32_t r = had128_x2<double>(px.x, ps.x, true, 0u, false, r_scale<double>());
+            const uint32_t xin = silu_in ? silu_mul_x2(px.x, pu.x) : px.x;
+            uint32_t r = had128_x2<double>(xin, ps.x, true, 0u, false, r_scale<double>());
             if constexpr (AFF || I8) {
                 // one row of 128 per wave, 2 values a lane: the same helper on a 64-lane group
                 const u32x4 r8 = approx_row(u32x4{r, 0u, 0u, 0u}, 64, lds_a + (wave * UROWS) * A_ROW, true);
@@ -462,7 +481,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             *reinterpret_cast<uint32_t*>(lds_a + (wave * UROWS) * A_ROW + 2 * lane) = r;
         }
     } else {
-        rotate_chunk(c0, c1, px, ps, px2, ps2, true);
+        rotate_chunk(c0, c1, px, ps, px2, ps2, pu, pu2, true);
     }
     static_for(std::make_integer_sequence<int, RING / 2>{}, [&](auto I) __attribute__((always_inline)) {
         fill(std::integral_constant<int, RING / 2 + decltype(I)::value>{});
@@ -600,7 +619,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             c0 = c1;
             c1 = min(c0 + a.chunk_units, uhi);
             __syncthreads();
-            rotate_chunk(c0, c1, px, ps, px2, ps2, false);
+            rotate_chunk(c0, c1, px, ps, px2, ps2, pu, pu2, false);
             __syncthreads();
         }
     };
@@ -946,47 +965,49 @@ inline size_t lds_bytes(int M, int cu, bool gated)
     return ((size_t) cu * (M + 1) + c_rows) * A_ROW * 2;
 }
 
-template <int BITS, int CB, int MT_, bool GATED>
+template <int BITS, int CB, int MT_, int FORM>
 int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t stream)
 {
-    hipLaunchKernelGGL((gemv_kernel<BITS, CB, MT_, GATED>), dim3(wgs), dim3(256), lds_bytes(a.M, a.chunk_units, GATED), stream, a);
+    hipLaunchKernelGGL((gemv_kernel<BITS, CB, MT_, FORM>), dim3(wgs), dim3(256),
+                       lds_bytes(a.M, a.chunk_units, FORM == FORM_GATED), stream, a);
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 
-template <int BITS, int CB, bool GATED>
+template <int BITS, int CB, int FORM>
 int launch_gemv_m(const GemvArgs& a, int wgs, hipStream_t s)
 {
-    return a.M == 1 ? launch_gemv_t<BITS, CB, 0, GATED>(a, wgs, s)
-         : a.M <= 16 ? launch_gemv_t<BITS, CB, 1, GATED>(a, wgs, s) : launch_gemv_t<BITS, CB, 2, GATED>(a, wgs, s);
+    return a.M == 1 ? launch_gemv_t<BITS, CB, 0, FORM>(a, wgs, s)
+         : a.M <= 16 ? launch_gemv_t<BITS, CB, 1, FORM>(a, wgs, s) : launch_gemv_t<BITS, CB, 2, FORM>(a, wgs, s);
 }
 
-template <int BITS, bool GATED>
+template <int BITS, int FORM>
 int launch_gemv_cb(const GemvArgs& a, int cb, int wgs, hipStream_t s)
 {
     switch (cb) {
-        case 0: return launch_gemv_m<BITS, 0, GATED>(a, wgs, s);
-        case 1: return launch_gemv_m<BITS, 1, GATED>(a, wgs, s);
-        default: return launch_gemv_m<BITS, 2, GATED>(a, wgs, s);
+        case 0: return launch_gemv_m<BITS, 0, FORM>(a, wgs, s);
+        case 1: return launch_gemv_m<BITS, 1, FORM>(a, wgs, s);
+        default: return launch_gemv_m<BITS, 2, FORM>(a, wgs, s);
     }
 }
 
-// the kernel instantiation for (bits, codebook, rows); GATED: the gate / up form
-template <bool GATED>
+// the kernel instantiation for (bits, codebook, rows) of one form
+template <int FORM>
 int launch_gemv_impl(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s)
 {
     switch (bits) {
-        case 1: return launch_gemv_cb<1, GATED>(a, cb, wgs, s);
-        case 2: return launch_gemv_cb<2, GATED>(a, cb, wgs, s);
-        case 3: return launch_gemv_cb<3, GATED>(a, cb, wgs, s);
-        case 4: return launch_gemv_cb<4, GATED>(a, cb, wgs, s);
-        case 5: return launch_gemv_cb<5, GATED>(a, cb, wgs, s);
-        case 6: return launch_gemv_cb<6, GATED>(a, cb, wgs, s);
-        case 7: return launch_gemv_cb<7, GATED>(a, cb, wgs, s);
-        default: return launch_gemv_cb<8, GATED>(a, cb, wgs, s);
+        case 1: return launch_gemv_cb<1, FORM>(a, cb, wgs, s);
+        case 2: return launch_gemv_cb<2, FORM>(a, cb, wgs, s);
+        case 3: return launch_gemv_cb<3, FORM>(a, cb, wgs, s);
+        case 4: return launch_gemv_cb<4, FORM>(a, cb, wgs, s);
+        case 5: return launch_gemv_cb<5, FORM>(a, cb, wgs, s);
+        case 6: return launch_gemv_cb<6, FORM>(a, cb, wgs, s);
+        case 7: return launch_gemv_cb<7, FORM>(a, cb, wgs, s);
+        default: return launch_gemv_cb<8, FORM>(a, cb, wgs, s);
     }
 }
 
-// gated instantiations live in exl3_gemv_gated.hip
+// gated instantiations live in exl3_gemv_gated.hip, SiLU-input ones in exl3_gemv_silu.hip
 int launch_gemv_gated(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s);
+int launch_gemv_silu_in(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s);
 // approximate mul1 instantiations (codebook ids 3 and 4) live in exl3_gemv_approx.hip
 int launch_gemv_approx(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s);

@@ -181,14 +181,14 @@ def exl3_gemv(A, B, C, suh, A_had, svh, mcg: bool, mul1: bool) -> int:
 _prerot = None
 
 
-def _rot_scratch(A_had, device, groups: int, m: int, k: int):
+def _rot_scratch(A_had, device, groups: int, m: int, k: int, any_rows: bool = False):
     """The A_had scratch for the multi-row GEMV (groups * m * k fp16): the caller's when it is large
     enough, else a fresh one; none below the library's pre-rotation row count (the kernel rotates
-    in LDS there)."""
+    in LDS there) unless any_rows (the SiLU-input form, whose own row count the library applies)."""
     global _prerot
     if _prerot is None:
         _prerot = int(L.lib().exl3_gemv_prerot_rows())
-    if m <= 1 or m < _prerot:
+    if m <= 1 or (m < _prerot and not any_rows):
         return None
     if A_had is not None and A_had.dtype == torch.float16 and A_had.is_contiguous() and A_had.numel() >= groups * m * k:
         return A_had
@@ -307,6 +307,29 @@ def exl3_gemv_silu_mul(A, B: Sequence[torch.Tensor], C, suh: Sequence[torch.Tens
                                               _ldy(C, n), ps, xr.data_ptr() if xr is not None else None, pv, m, k, n,
                                               K, *_cb_flags(mcg, mul1), ws.data_ptr(),
                                               ws.numel(), _stream(A)), "exl3_gemv_silu_mul")
+
+
+def exl3_gemv_silu_in(gate, up, B, C, suh, A_had, svh, K: int, mcg: bool, mul1: bool) -> int:
+    """exl3_gemv_mr over the input fp16(fp16(silu(gate)) * up) (m <= 32), formed as the rows load:
+    gate and up are [m, k] views with equal row spacing (typically the two halves of a gated
+    module's grouped output).  Bitwise equal to silu_mul followed by exl3_gemv_mr.  No counterpart
+    in the reference extension."""
+    _cuda(gate, up, B, C, suh, svh)
+    k = gate.shape[-1]
+    g2, u2 = gate.reshape(-1, k), up.reshape(-1, k)
+    m = g2.shape[0]
+    n = svh.shape[0]
+    _need(u2.shape == g2.shape, "silu_in: gate and up of one shape")
+    _need(all(t.dtype == torch.float16 and t.stride(-1) == 1 for t in (g2, u2)), "silu_in: fp16, unit stride")
+    _need(m <= 1 or g2.stride(0) == u2.stride(0), "silu_in: gate and up rows equally spaced")
+    _need(B.shape[-1] == 16 * K, "exl3_gemv_silu_in: trellis last dim must be 16*K")
+    ld_in = g2.stride(0) if m > 1 else k
+    ws = workspace(gate.device, gemv_workspace_bytes(m, k, n, K))
+    xr = _rot_scratch(A_had, gate.device, 1, m, k, any_rows=True)
+    return L.check(L.lib().exl3_gemv_silu_in(g2.data_ptr(), u2.data_ptr(), ld_in, B.data_ptr(), C.data_ptr(),
+                                             _ldy(C, n), suh.data_ptr(), xr.data_ptr() if xr is not None else None,
+                                             svh.data_ptr(), m, k, n, K, *_cb_flags(mcg, mul1), ws.data_ptr(),
+                                             ws.numel(), _stream(gate)), "exl3_gemv_silu_in")
 
 
 def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor) -> None:

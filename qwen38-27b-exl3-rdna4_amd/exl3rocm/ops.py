@@ -236,3 +236,40 @@ def exl3_linear_silu_mul(x: torch.Tensor, trellis: list[torch.Tensor], suh: list
 @exl3_linear_silu_mul.register_fake
 def _(x, trellis, suh, svh, K, mcg, mul1):
     return x.new_empty((*x.shape[:-1], svh[0].shape[0]), dtype=torch.float16)
+
+
+@torch.library.custom_op("exl3rocm::silu_mul_linear", mutates_args=())
+def exl3_silu_mul_linear(gu: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+                         K: int, mcg: bool, mul1: bool) -> torch.Tensor:
+    """A gated MLP's output: SiLU-and-mul of gu = [gate | up] (the [.., 2k] output of the gate/up
+    linear_groups), act = fp16(fp16(silu(gate)) * up), then the down linear of act.  No
+    counterpart in the reference plugin, whose MLP runs a separate SiluAndMul before the down
+    linear (the fusion is proposed in reference docs/EFFICIENCY_INVESTIGATION.md:36-66).
+
+    At M <= EXL3_MR_MAX one GEMV launch forms act from gate and up as its input rows load; above
+    it (and on the approximate GEMV routes) the elementwise kernel writes act and linear runs on
+    it.  Every route equals silu_mul followed by linear, bitwise."""
+    k2 = gu.shape[-1]
+    k = suh.shape[0]
+    if k2 != 2 * k:
+        raise RuntimeError(f"exl3rocm: silu_mul_linear takes [gate | up] of 2 * {k} columns, got {k2}")
+    g2, _ = _prep(gu)
+    M = g2.shape[0]
+    n = svh.shape[0]
+    y = torch.empty((M, n), dtype=torch.float16, device=gu.device)
+    if M == 0:
+        return y.view(*gu.shape[:-1], n)
+    if M <= MR_MAX and not (GEMV_APPROX and mul1):
+        rc = E.exl3_gemv_silu_in(g2[:, :k], g2[:, k:], trellis, y, suh, None, svh, K, mcg, mul1)
+        if rc != 0:
+            raise RuntimeError(f"exl3rocm: GEMV declined shape m={M} k={k} n={n} K={K}")
+    else:
+        act = torch.empty((M, k), dtype=torch.float16, device=gu.device)
+        E.silu_mul(g2[:, :k], g2[:, k:], act)
+        _linear_into(act, trellis, suh, svh, K, mcg, mul1, y)
+    return y.view(*gu.shape[:-1], n)
+
+
+@exl3_silu_mul_linear.register_fake
+def _(gu, trellis, suh, svh, K, mcg, mul1):
+    return gu.new_empty((*gu.shape[:-1], svh.shape[0]), dtype=torch.float16)

@@ -1,0 +1,150 @@
+"""GPU parity of the down-projection GEMV with the SiLU-and-mul input formed as it loads
+(exl3_gemv_silu_in, op exl3rocm::silu_mul_linear) -- run with -m gpu on an MI355X.
+
+The fused form must equal the two-launch form (exl3_silu_mul, then exl3_gemv_mr) bitwise at every
+row count (in-LDS rotation below the pre-rotation row count, the pre-rotation pass from it), every
+row must equal its m == 1 call, and the result must meet the north-star bar against the oracle
+(act = fp16(fp16(silu(g)) * u) in float64, then the faithful linear).
+"""
+import numpy as np
+import pytest
+import torch
+
+import cpu
+import exl3_oracle as O
+from exl3rocm import _lib, kernels as E, ops, synth
+from test_gpu_parity import DEV, assert_close, to_dev
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU")]
+
+
+def down(k, n, bits, m, tag="silu-in", spread=1.0):
+    tr, su, sv = synth.layer(tag, f"{k}x{n}x{bits}", k, n, bits)
+    gu = synth.activations(synth.key_of(tag, f"{k}x{n}x{bits}", "gu", m), m, 2 * k)
+    gu = (gu.astype(np.float32) * spread).astype(np.float16)
+    return gu, tr, su, sv
+
+
+def two_launch(GU, T, SU, SV, k, bits, mcg, mul1):
+    act = torch.empty(GU.shape[0], k, dtype=torch.float16, device=DEV)
+    E.silu_mul(GU[:, :k], GU[:, k:], act)
+    y = torch.empty(GU.shape[0], SV.shape[0], dtype=torch.float16, device=DEV)
+    assert E.exl3_gemv_mr(act, T, y, SU, None, SV, bits, mcg, mul1) == 0
+    return act, y
+
+
+def fused(GU, T, SU, SV, k, bits, mcg, mul1, A_had=None):
+    y = torch.empty(GU.shape[0], SV.shape[0], dtype=torch.float16, device=DEV)
+    assert E.exl3_gemv_silu_in(GU[:, :k], GU[:, k:], T, y, SU, A_had, SV, bits, mcg, mul1) == 0
+    return y
+
+
+def same(a, b):
+    return torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def raw_silu_in(GU, T, SU, SV, k, bits, mcg, mul1):
+    """The C-ABI call without A_had: the kernel rotates (and applies the SiLU) in LDS at any m."""
+    m, n = GU.shape[0], SV.shape[0]
+    y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    ws = E.workspace(GU.device, E.gemv_workspace_bytes(m, k, n, bits))
+    rc = _lib.lib().exl3_gemv_silu_in(GU.data_ptr(), GU.data_ptr() + 2 * k, GU.stride(0), T.data_ptr(), y.data_ptr(),
+                                      n, SU.data_ptr(), None, SV.data_ptr(), m, k, n, bits, int(mcg), int(mul1),
+                                      ws.data_ptr(), ws.numel(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    return y
+
+
+@pytest.mark.parametrize("m,k,n,bits,cb", [(1, 17408, 5120, 4, 2), (2, 17408, 5120, 4, 2), (4, 17408, 5120, 4, 2),
+                                           (12, 17408, 5120, 4, 2),
+                                           (32, 17408, 5120, 4, 2), (1, 512, 256, 3, 0), (3, 1024, 768, 2, 1),
+                                           (16, 2048, 1024, 6, 2), (11, 256, 128, 8, 1)])
+def test_silu_in_matches_two_launches(m, k, n, bits, cb):
+    gu, tr, su, sv = down(k, n, bits, m)
+    print(f"silu_in m={m} k={k} n={n} bits={bits} cb={cb}", flush=True)
+    GU, T, SU, SV = to_dev(gu, tr.view(np.int16), su, sv)
+    mcg, mul1 = cb == 1, cb == 2
+    act, want = two_launch(GU, T, SU, SV, k, bits, mcg, mul1)
+    got = fused(GU, T, SU, SV, k, bits, mcg, mul1)
+    assert same(got, want), "fused input == silu_mul then exl3_gemv_mr"
+    if m > 1:
+        # the pre-rotation pass (m >= 4) leaves the rotated activation in A_had; without A_had the
+        # kernel forms and rotates it in LDS
+        xr = torch.empty(m * k, dtype=torch.float16, device=DEV)
+        assert same(fused(GU, T, SU, SV, k, bits, mcg, mul1, A_had=xr), want)
+        assert same(raw_silu_in(GU, T, SU, SV, k, bits, mcg, mul1), want), "in-LDS form"
+        if m >= 4:
+            xw = torch.empty(m, k, dtype=torch.float16, device=DEV)
+            E.had_r_128(act, xw, SU, None, 1.0)
+            assert same(xr.view(m, k), xw), "A_had == the exact rotation of the activation"
+        y1 = torch.empty(1, n, dtype=torch.float16, device=DEV)
+        for r in (0, m - 1):
+            assert E.exl3_gemv_silu_in(GU[r:r + 1, :k], GU[r:r + 1, k:], T, y1, SU, None, SV, bits, mcg, mul1) == 0
+            assert same(y1, want[r:r + 1]), ("row == its m == 1 call", r)
+    torch.cuda.synchronize()
+
+
+def test_silu_in_vs_oracle():
+    m, k, n, bits = 3, 2048, 1024, 4
+    gu, tr, su, sv = down(k, n, bits, m, tag="silu-in-oracle", spread=4.0)
+    GU, T, SU, SV = to_dev(gu, tr.view(np.int16), su, sv)
+    got = fused(GU, T, SU, SV, k, bits, False, True)
+    g, u = gu[:, :k].astype(np.float64), gu[:, k:].astype(np.float64)
+    with np.errstate(over="ignore"):                  # exp(-g) = inf for very negative g: silu -> -0
+        act = O.to_f16(O.to_f16(g / (1.0 + np.exp(-g))) * u)
+    ref = cpu.linear(act.astype(np.float16), tr, bits, su, sv, 2)
+    torch.cuda.synchronize()
+    assert_close(got.cpu().numpy(), ref, "silu_in vs oracle")
+
+
+def test_silu_in_saturating_gate():
+    """Gate values out to about +-40 (silu underflows to -0 and saturates to g) and large up values."""
+    m, k, n, bits = 2, 1024, 512, 4
+    gu, tr, su, sv = down(k, n, bits, m, tag="silu-in-sat", spread=8.0)
+    GU, T, SU, SV = to_dev(gu, tr.view(np.int16), su, sv)
+    _, want = two_launch(GU, T, SU, SV, k, bits, False, True)
+    assert same(fused(GU, T, SU, SV, k, bits, False, True), want)
+    assert torch.isfinite(want).all()
+
+
+@pytest.mark.parametrize("m", [1, 5, 40])
+def test_silu_mul_linear_op(m):
+    """The op: M <= 32 on the fused GEMV, M > 32 on silu_mul then the prefill; == the two-launch
+    form bitwise; rows of a [b, s, 2k] input keep their leading shape."""
+    k, n, bits = 1024, 768, 4
+    gu, tr, su, sv = down(k, n, bits, m, tag="silu-in-op")
+    GU, T, SU, SV = to_dev(gu, tr.view(np.int16), su, sv)
+    y = torch.ops.exl3rocm.silu_mul_linear(GU.view(1, m, 2 * k), T, SU, SV, bits, False, True)
+    assert y.shape == (1, m, n)
+    act = torch.empty(m, k, dtype=torch.float16, device=DEV)
+    E.silu_mul(GU[:, :k], GU[:, k:], act)
+    want = torch.ops.exl3rocm.linear(act, T, SU, SV, bits, False, True)
+    assert same(y.view(m, n), want)
+    with pytest.raises(RuntimeError):
+        torch.ops.exl3rocm.silu_mul_linear(GU[:, :k], T, SU, SV, bits, False, True)
+
+
+def test_silu_in_graph_replays():
+    m, k, n, bits = 4, 17408, 5120, 4
+    gu, tr, su, sv = down(k, n, bits, m, tag="silu-in-graph")
+    GU, T, SU, SV = to_dev(gu, tr.view(np.int16), su, sv)
+    eager = fused(GU, T, SU, SV, k, bits, False, True)
+    y = torch.empty_like(eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.reserve_workspace(DEV, k, n, bits)
+        E.exl3_gemv_silu_in(GU[:, :k], GU[:, k:], T, y, SU, None, SV, bits, False, True)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        E.exl3_gemv_silu_in(GU[:, :k], GU[:, k:], T, y, SU, None, SV, bits, False, True)
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert same(y, eager)
+        eager = fused(GU, T, SU, SV, k, bits, False, True)
+        torch.cuda.synchronize()
