@@ -327,9 +327,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             float* pad = reinterpret_cast<float*>(lds_row + 128);
             const bool leader = live && ((int) threadIdx.x & (width - 1)) == 0;
             if constexpr (AFF) {
-                float sum = 0.f;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) sum += (float) h[i];
+                // pairwise in the lane, then across lanes: the 64-lane form (2 values a lane, the
+                // rest zero) adds in exactly the 16-lane form's order, so a row's sum, and with it
+                // every output, is the same bitwise in both
+                const float p0 = (float) h[0] + (float) h[1], p1 = (float) h[2] + (float) h[3];
+                const float p2 = (float) h[4] + (float) h[5], p3 = (float) h[6] + (float) h[7];
+                float sum = (p0 + p1) + (p2 + p3);
                 sum = red(sum, false);
                 if (leader) pad[0] = sum;
                 return r;

@@ -54,11 +54,14 @@ def test_approx_vs_oracle(mode, k, n, bits):
         assert dev["rel_l2"] <= 2e-2 and dev["cosine_similarity"] > 0.999, dev   # the int8 error family
 
 
+@pytest.mark.parametrize("k,n", [(5120, 2048), (5120, 1024), (2048, 5120), (17408, 1024)])
 @pytest.mark.parametrize("mode", ["affine", "int8"])
-def test_approx_rows_equal_m1(mode):
-    k, n, bits = 5120, 2048, 4
-    tr, su, sv = synth.layer("approx-rows", mode, k, n, bits)
-    x = synth.activations(synth.key_of("approx-rows", mode, "x"), 32, k)
+def test_approx_rows_equal_m1(mode, k, n):
+    """Row sums (affine) and scales (int8) of the single-row layout (2 values a lane) equal the
+    multi-row layout's (8 a lane) bitwise, whichever layout a workgroup's unit count selects."""
+    bits = 4
+    tr, su, sv = synth.layer("approx-rows", f"{mode}{k}x{n}", k, n, bits)
+    x = synth.activations(synth.key_of("approx-rows", mode, k, n, "x"), 32, k)
     X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
     rows1 = []
     for r in range(32):
