@@ -547,7 +547,7 @@ def main() -> int:
                 "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": round(traffic) if traffic is not None else None,
                 "traffic_source": "profiles/gemv_traffic_config1.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
-                "kernel": "gemv_kernel<4,2,0,false> (every M=1 launch of the step)",
+                "kernel": "gemv_kernel<4,2,0,0> (every M=1 launch of the step)",
                 "bytes_per_launch": step_bytes / lps, "mean_launch_us": round(avg_launch_us, 3)}
     weights = sum(k * n for _, k, n in LAYER)
     valu_floor_us = weights * VALU_OPS_PER_WEIGHT_4BPW / VALU_LANE_OPS_PER_S * 1e6
