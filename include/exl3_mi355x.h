@@ -121,8 +121,9 @@ int exl3_gemv_mr(const void* x, int64_t ldx, const void* trellis, void* y, int64
  *     before their fp16 rounding (rel-L2 ~5e-4 from the faithful output);
  *   mode 2 (int8 activations): the rotated input quantized per (row, 128-input slice) as
  *     v = clamp(rint(a / q), -127, 127), q = max(|a|, 1e-8) / 127, and C = sum over slices of
- *     q (k_inv sum v (1024 + s) + k_bias sum v) -- the reference's int8 path (integer products,
- *     affine epilogue), with one scale per slice.
+ *     q (k_inv sum v s + (1024 k_inv + k_bias) sum v) -- the reference's int8 path (integer
+ *     products, affine epilogue), with one scale per slice.  A slice's sum v s is exact
+ *     (|v s| <= 127 * 1020, 128 terms: below 2^24, so its fp32 MFMA accumulation never rounds).
  * C is rounded to fp16 and transformed as in exl3_gemv_mr.  Arguments, workspace and A_had as
  * exl3_gemv_mr (mul1 codebook implied).  Returns EXL3_EINVAL for another mode.
  * Replaces the reference's opt-in int8 GEMV behind exl3_gemm (EXL3_ROCM_GFX1201_INT8,

@@ -313,8 +313,8 @@ template <class T> constexpr T r_scale() { return (T) R_SCALE; }
 // Codebook constants
 // ------------------------------------------------------------------------------------------
 // CB 3 and 4 are the mul1 hash without the per-weight fp16 scale: the decoder emits the exact fp16
-// integers 1024 + s, and the GEMV applies k_inv and k_bias per output instead (the affine and
-// int8-activation routes of the fused GEMV; never used for decoded weight tiles)
+// integers 1024 + s (CB 3) or s (CB 4), and the GEMV applies k_inv and k_bias per output instead
+// (the affine and int8-activation routes of the fused GEMV; never used for decoded weight tiles)
 template <int CB> struct Codebook;
 template <> struct Codebook<2> { static constexpr uint32_t lo = 0xD12Du, hi = 0x83DCu, add = 0; };       // mul1
 template <> struct Codebook<3> : Codebook<2> {};                                                          // mul1, unscaled
@@ -395,6 +395,10 @@ __device__ __forceinline__ uint32_t decode_pair(const uint32_t* W, uint32_t k_hi
             const f16x2 k_inv = {bits_f16(0x1EEEu), bits_f16(0x1EEEu)};
             const f16x2 k_bias = {bits_f16(0xC931u), bits_f16(0xC931u)};
             h = __builtin_elementwise_fma(h, k_inv, k_bias);       // v_pk_fma_f16: one rounding
+        } else if constexpr (CB == 4) {
+            // the byte sums themselves (exact: s <= 1020): int8 products v * s stay below 2^17
+            // and a 128-input slice's sum below 2^24, so fp32 accumulation keeps it exact
+            h = h - f16x2{(f16) 1024.0f, (f16) 1024.0f};
         }
         return __builtin_bit_cast(uint32_t, h);
     } else {

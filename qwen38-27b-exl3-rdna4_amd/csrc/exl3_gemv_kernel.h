@@ -241,6 +241,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // sum (affine) or its int8 scale q and integer sum (int8)
     constexpr bool AFF = CB == 3, I8 = CB == 4;
     constexpr float MUL1_K_INV = 0.00676727294921875f, MUL1_K_BIAS = -10.3828125f;   // fp16 0x1EEE, 0xC931
+    constexpr float MUL1_K_SUM = 1024.0f * MUL1_K_INV + MUL1_K_BIAS;                    // -3.453125, exact
     const int G = gg.G, UPB = a.UPB, M = MT_ == 0 ? 1 : a.M;
     const int NB = gg.n / 128, NT = gg.n / 16, U = NB * UPB;
     const Split sp{U, G, gg.h, a.wa, a.wb, gg.d_sg, gg.d_u, a.d_wa, a.d_wb};
@@ -600,7 +601,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
         }
         step(Wr[i], unit_a, i & 1, refill);
         if constexpr (I8) {
-            if (i & 1) {                                      // unit done: fold q (k_inv acc + k_bias sum v)
+            if (i & 1) {                                      // unit done: fold q (k_inv acc + (1024 k_inv + k_bias) sum v)
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -609,7 +610,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                         const float q = pd[0], sv = pd[1];
 #pragma unroll
                         for (int h = 0; h < 2; ++h) {
-                            acc_seg[h][mt][v] += q * (MUL1_K_INV * acc[h][mt][v] + MUL1_K_BIAS * sv);
+                            acc_seg[h][mt][v] += q * (MUL1_K_INV * acc[h][mt][v] + MUL1_K_SUM * sv);
                             acc[h][mt][v] = 0.f;
                         }
                     }

@@ -32,9 +32,22 @@ PREFILL_ROUTE = os.environ.get("EXL3_PREFILL", "fused")
 # linear_silu_mul at M <= MR_MAX: "unfused" (grouped GEMV + elementwise kernel) or "fused" (one
 # gated GEMV launch)
 GATED_ROUTE = os.environ.get("EXL3_GATED", "unfused")
-# opt-in approximate mul1 GEMV for M <= MR_MAX: "" (faithful, the default), "affine" (unrounded
-# weights) or "int8" (int8 activations, the reference's EXL3_ROCM_GFX1201_INT8 path)
-GEMV_APPROX = os.environ.get("EXL3_GEMV_APPROX", "")
+def approx_mode(value: Optional[str]) -> str:
+    """EXL3_GEMV_APPROX -> the GEMV's approximate mul1 route: "" (faithful, the default; also for
+    "0", "off", "none", "faithful"), "affine" (unrounded weights) or "int8" (int8 activations, the
+    reference's EXL3_ROCM_GFX1201_INT8 path).  Any other value raises: a misspelt opt-in must not
+    silently run (or silently skip) a route with a different numerical budget."""
+    v = (value or "").strip().lower()
+    if v in ("", "0", "off", "none", "faithful"):
+        return ""
+    if v not in E.APPROX_MODES:
+        raise ValueError(f"exl3rocm: EXL3_GEMV_APPROX={value!r}: expected one of "
+                         f"{sorted(E.APPROX_MODES)} or off")
+    return v
+
+
+# opt-in approximate mul1 GEMV for M <= MR_MAX
+GEMV_APPROX = approx_mode(os.environ.get("EXL3_GEMV_APPROX"))
 
 _wbuf: dict = {}
 

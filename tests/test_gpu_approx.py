@@ -94,3 +94,43 @@ def test_approx_op_route(monkeypatch):
     monkeypatch.setattr(ops, "GEMV_APPROX", "")
     faithful = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, False, True)
     assert not torch.equal(faithful.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("mode", ["affine", "int8"])
+def test_approx_streams_and_graph_replays_are_deterministic(mode):
+    """Four layers on four streams (each its own workspace), 20 rounds, equal their serial
+    results bitwise; a captured graph of one call replays to the eager result (the reference's
+    int8 contract, tests/test_int8_contract.py: concurrent-stream determinism; here the route is
+    also graph-capturable rather than falling back under capture)."""
+    k, n, bits = 1024, 512, 4
+    layers = []
+    for i in range(4):
+        tr, su, sv = synth.layer("approx-streams", i, k, n, bits)
+        x = synth.activations(synth.key_of("approx-streams", i, "x"), 2, k)
+        layers.append(to_dev(x, tr.view(np.int16), su, sv))
+    outs = [torch.empty(2, n, dtype=torch.float16, device=DEV) for _ in layers]
+    want = []
+    for (X, T, SU, SV), y in zip(layers, outs):
+        E.exl3_gemv_mr_approx(X, T, y, SU, None, SV, bits, mode)
+        want.append(y.clone())
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in layers]
+    for _ in range(20):
+        for s, (X, T, SU, SV), y in zip(streams, layers, outs):
+            with torch.cuda.stream(s):
+                E.exl3_gemv_mr_approx(X, T, y, SU, None, SV, bits, mode)
+    torch.cuda.synchronize()
+    for y, w in zip(outs, want):
+        assert torch.equal(y.view(torch.int16), w.view(torch.int16))
+    X, T, SU, SV = layers[0]
+    y = torch.empty(2, n, dtype=torch.float16, device=DEV)
+    s = streams[0]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        E.exl3_gemv_mr_approx(X, T, y, SU, None, SV, bits, mode)
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), want[0].view(torch.int16))

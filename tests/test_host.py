@@ -273,3 +273,15 @@ def test_vllm_entry_point_is_declared():
     mod, fn = target.split(":")
     assert callable(getattr(importlib.import_module(mod), fn))
     assert "libexl3_mi355x.so" in meta["tool"]["setuptools"]["package-data"]["exl3rocm"]
+
+
+def test_approx_route_setting():
+    """EXL3_GEMV_APPROX: off values select the faithful GEMV, the two routes by name (any case),
+    anything else is refused rather than silently ignored."""
+    for off in (None, "", "0", "off", "OFF", " none ", "faithful"):
+        assert ops.approx_mode(off) == ""
+    assert ops.approx_mode("affine") == "affine"
+    assert ops.approx_mode(" INT8") == "int8"
+    for bad in ("1", "7", "int4", "affin"):
+        with pytest.raises(ValueError):
+            ops.approx_mode(bad)

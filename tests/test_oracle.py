@@ -304,3 +304,23 @@ def test_affine_form_is_near_the_faithful_linear():
     ya = O.linear_approx(x, tr, bits, su, sv, "affine")
     yi = O.linear_approx(x, tr, bits, su, sv, "int8")
     assert O.rel_l2(ya, yf) < 1e-3 and 0 < O.rel_l2(yi, yf) < 2e-2
+
+
+def test_int8_slice_sums_are_exact_in_fp32():
+    """Arithmetic bound of the GEMV's int8 route (the counterpart of the reference's integer
+    overflow proof, tests/test_arithmetic_bounds.py): the decoder hands the MFMA the byte sums s
+    (<= 4 * 255 = 1020) and the quantized v (|v| <= 127), so one 128-input slice's sum of v * s is
+    an integer below 2^24 and its fp32 accumulation, in any order, is exact.  With 1024 + s it
+    would not be; 1024 sum v joins in the fold instead, through 1024 k_inv + k_bias, which is
+    itself exact in fp32."""
+    worst = 128 * 127 * 1020
+    assert worst < 2 ** 24
+    assert 128 * 127 * (1024 + 1020) > 2 ** 24
+    s = O.byte_sum(O.codebook_hash(np.arange(65536, dtype=np.uint32), 2))
+    assert int(s.max()) <= 1020 and int(s.min()) >= 0
+    acc = np.float32(0.0)
+    for _ in range(128):                                   # the worst case, summed in fp32
+        acc = np.float32(acc + np.float32(127 * 1020))
+    assert int(acc) == worst
+    k_sum = np.float32(1024.0) * np.float32(O.K_INV) + np.float32(O.K_BIAS)
+    assert float(k_sum) == 1024.0 * O.K_INV + O.K_BIAS == -3.453125
