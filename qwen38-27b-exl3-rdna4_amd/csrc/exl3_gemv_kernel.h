@@ -280,7 +280,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // operand of MFMA rows >= M), then the fp16 C of one block for the output transform
     const int UROWS = M + 1;
     uint16_t* lds_a = smem;                                   // [chunk_units][M + 1][A_ROW]
-    uint16_t* lds_c = smem + a.chunk_units * UROWS * A_ROW;   // [M][A_ROW]
+    uint16_t* lds_c = smem + a.chunk_units * UROWS * A_ROW;   // [2 M][A_ROW]: two blocks side by side
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int g = lane >> 4, j = lane & 15, q = j & 7;
     const int ulo = sp.lo(w), uhi = sp.lo(w + 1);
@@ -660,7 +660,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     __syncthreads();
     const int nblk = cb_cur - seg0_cb + 1;
     // completed blocks (gated: block pairs, 2M rows each: gate, then up) reduced side by side
-    const int RB = M == 1 ? 2 : 1;
+    // blocks reduced side by side: two up to 8 rows (one round trip of partial loads for both;
+    // measured slower from 16 rows, where one block already fills the passes)
+    const int RB = gated && M > 1 ? 1 : (M <= 8 ? 2 : 1);
     const int RM = gated ? 2 * M : M;
     const Split sp0{U, a.g[0].G, a.g[0].h, a.wa, a.wb, a.g[0].d_sg, a.g[0].d_u, a.d_wa, a.d_wb};
     const Split sp1{U, a.g[1].G, a.g[1].h, a.wa, a.wb, a.g[1].d_sg, a.g[1].d_u, a.d_wa, a.d_wb};
@@ -805,37 +807,86 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                     }
                 }
             } else if (!GATED && MT_ != 0 && M > 1) {
-                // one block per pass (rb == 1): every element shares the block's contributors, so a
-                // thread keeps 4 elements x 8 contributors of loads in flight (sums in contributor order)
-                const int bi = s_list[r0];
-                const int wf = s_own[0][bi], nc = s_own[1][bi];
-                const int64_t cs = (int64_t) gg.max_seg * M * 128;
-                const float* p0 = part_grp + ((int64_t) wf * gg.max_seg + s_own[2][bi]) * M * 128;
-                const float* p1 = part_grp + (int64_t) (wf + 1) * cs;
-                for (int e0 = threadIdx.x; e0 < total; e0 += 1024) {
-                    float sum[4] = {0.f, 0.f, 0.f, 0.f};
-                    for (int c0 = 0; c0 < nc; c0 += 8) {
-                        float v[4][8];
-#pragma unroll
-                        for (int j = 0; j < 4; ++j)
-#pragma unroll
-                            for (int cc = 0; cc < 8; ++cc) {
-                                const int c = c0 + cc, e = e0 + 256 * j;
-                                const float* src = (c == 0 ? p0 : p1 + (int64_t) (c - 1) * cs) + e;
-                                v[j][cc] = c < nc && e < total
-                                               ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                               : 0.f;
+                if (rb == 2) {
+                    // two blocks side by side (M <= 8): a thread keeps 4 elements x 8 contributors of
+                    // loads in flight, each element summing its block's contributors in order (one
+                    // round trip for both blocks: -1.5 to -2 us at M = 2 / 4 on gate; the one-block
+                    // pass below stays from 16 rows, where its hoisted pointers measured faster)
+                    const int half = M * 128;
+                    const int bi0 = s_list[r0], bi1 = s_list[r0 + 1];
+                    const int64_t cs = (int64_t) gg.max_seg * M * 128;
+                    const int nc0 = s_own[1][bi0], nc1 = s_own[1][bi1];
+                    const float* const q0 = part_grp + ((int64_t) s_own[0][bi0] * gg.max_seg + s_own[2][bi0]) * M * 128;
+                    const float* const q1 = part_grp + (int64_t) (s_own[0][bi0] + 1) * cs;
+                    const float* const r0p = part_grp + ((int64_t) s_own[0][bi1] * gg.max_seg + s_own[2][bi1]) * M * 128;
+                    const float* const r1p = part_grp + (int64_t) (s_own[0][bi1] + 1) * cs;
+                    const int ncmax = nc0 > nc1 ? nc0 : nc1;
+                    for (int e0 = threadIdx.x; e0 < total; e0 += 1024) {
+                        float sum[4] = {0.f, 0.f, 0.f, 0.f};
+                        for (int c0 = 0; c0 < ncmax; c0 += 8) {
+                            float v[4][8];
+    #pragma unroll
+                            for (int j = 0; j < 4; ++j) {
+                                const int e = e0 + 256 * j;
+                                const bool second = e >= half;
+                                const int el = second ? e - half : e;
+                                const int nc = e < total ? (second ? nc1 : nc0) : 0;
+    #pragma unroll
+                                for (int cc = 0; cc < 8; ++cc) {
+                                    const int c = c0 + cc;
+                                    const float* src = (c == 0 ? (second ? r0p : q0)
+                                                               : (second ? r1p : q1) + (int64_t) (c - 1) * cs) + el;
+                                    v[j][cc] = c < nc ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+                                }
                             }
-#pragma unroll
-                        for (int j = 0; j < 4; ++j)
-#pragma unroll
-                            for (int cc = 0; cc < 8; ++cc)
-                                if (c0 + cc < nc) sum[j] += v[j][cc];
+    #pragma unroll
+                            for (int j = 0; j < 4; ++j) {
+                                const int e = e0 + 256 * j;
+                                const int nc = e < total ? (e >= half ? nc1 : nc0) : 0;
+    #pragma unroll
+                                for (int cc = 0; cc < 8; ++cc)
+                                    if (c0 + cc < nc) sum[j] += v[j][cc];
+                            }
+                        }
+    #pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const int e = e0 + 256 * j;
+                            if (e < total) lds_c[(e >> 7) * A_ROW + (e & 127)] = f16_bits((f16) sum[j]);
+                        }
                     }
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int e = e0 + 256 * j;
-                        if (e < total) lds_c[(e >> 7) * A_ROW + (e & 127)] = f16_bits((f16) sum[j]);
+                } else {
+                    // one block per pass (rb == 1): every element shares the block's contributors, so a
+                    // thread keeps 4 elements x 8 contributors of loads in flight (sums in contributor order)
+                    const int bi = s_list[r0];
+                    const int wf = s_own[0][bi], nc = s_own[1][bi];
+                    const int64_t cs = (int64_t) gg.max_seg * M * 128;
+                    const float* p0 = part_grp + ((int64_t) wf * gg.max_seg + s_own[2][bi]) * M * 128;
+                    const float* p1 = part_grp + (int64_t) (wf + 1) * cs;
+                    for (int e0 = threadIdx.x; e0 < total; e0 += 1024) {
+                        float sum[4] = {0.f, 0.f, 0.f, 0.f};
+                        for (int c0 = 0; c0 < nc; c0 += 8) {
+                            float v[4][8];
+    #pragma unroll
+                            for (int j = 0; j < 4; ++j)
+    #pragma unroll
+                                for (int cc = 0; cc < 8; ++cc) {
+                                    const int c = c0 + cc, e = e0 + 256 * j;
+                                    const float* src = (c == 0 ? p0 : p1 + (int64_t) (c - 1) * cs) + e;
+                                    v[j][cc] = c < nc && e < total
+                                                   ? __hip_atomic_load(src, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                                   : 0.f;
+                                }
+    #pragma unroll
+                            for (int j = 0; j < 4; ++j)
+    #pragma unroll
+                                for (int cc = 0; cc < 8; ++cc)
+                                    if (c0 + cc < nc) sum[j] += v[j][cc];
+                        }
+    #pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const int e = e0 + 256 * j;
+                            if (e < total) lds_c[(e >> 7) * A_ROW + (e & 127)] = f16_bits((f16) sum[j]);
+                        }
                     }
                 }
             } else if constexpr (!GATED) {
@@ -965,7 +1016,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
 // LDS: chunk_units x (m + 1) input rows, then the C rows of the blocks reduced side by side
 inline size_t lds_bytes(int M, int cu, bool gated)
 {
-    const int c_rows = (M == 1 ? 2 : 1) * (gated ? 2 * M : M);    // side-by-side blocks (pairs) x rows
+    // blocks (gated: pairs) reduced side by side x rows: as RB in the kernel
+    const int c_rows = gated ? (M == 1 ? 4 : 2 * M) : (M <= 8 ? 2 * M : M);
     return ((size_t) cu * (M + 1) + c_rows) * A_ROW * 2;
 }
 
