@@ -88,8 +88,7 @@ __global__ void __launch_bounds__(256) reconstruct_kernel(const uint32_t* __rest
 // had_r_128: out = fp16(Had128(in [* pre]) * r * scale) [* post]; one 8-lane group per 128-block,
 // 8 blocks per wave (reference binding `had_r_128`, vllm_plugin/exl3rocm/ops.py:88,97)
 // ============================================================================================
-// the (pre, out) pair of each group of one launch (a fused module's input transforms read one x);
-// blockIdx.y selects the group, with constant indices only
+// the (pre, out) pair of each group of one launch (a fused module's input transforms read one x)
 struct HadGroups {
     const uint16_t* pre[EXL3_MAX_GROUPS];
     uint16_t* out[EXL3_MAX_GROUPS];
@@ -99,38 +98,46 @@ struct HadGroups {
 // values as the GEMV's in-kernel transforms; float: the prefill's input transforms and
 // exl3_had_r_128_f32, the same values as the prefill epilogue's)
 // in_up (may be null): the input rows are fp16(fp16(silu(in)) * in_up) (a gated MLP's activation)
+// Every group's output of a block comes from one read of the input block (a fused module's groups
+// differ only in their pre-scale).
 template <class T>
 __global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ in, const uint16_t* __restrict__ in_up,
-                                                  int64_t ld_in, HadGroups hg, int64_t ld_out, int rows, int cols,
-                                                  const uint16_t* __restrict__ post, T scale)
+                                                  int64_t ld_in, HadGroups hg, int groups, int64_t ld_out, int rows,
+                                                  int cols, const uint16_t* __restrict__ post, T scale)
 {
-    const int gy = blockIdx.y;
-    const uint16_t* pre = gy == 0 ? hg.pre[0] : gy == 1 ? hg.pre[1] : gy == 2 ? hg.pre[2] : hg.pre[3];
-    uint16_t* out = gy == 0 ? hg.out[0] : gy == 1 ? hg.out[1] : gy == 2 ? hg.out[2] : hg.out[3];
     const int blocks_per_row = cols / 128;
     const int64_t job = ((int64_t) blockIdx.x * 256 + threadIdx.x) >> 3;     // one 128-block per 8 lanes
     const bool live = job < (int64_t) rows * blocks_per_row;
     const int r = threadIdx.x & 7;
     const int64_t row = live ? job / blocks_per_row : 0;
     const int col = live ? (int) (job % blocks_per_row) * 128 + 16 * r : 0;
-    u32x4 v[2], pv[2], qv[2];
+    u32x4 v[2], qv[2];
 #pragma unroll
-    for (int c = 0; c < 2; ++c) v[c] = pv[c] = qv[c] = u32x4{0u, 0u, 0u, 0u};
+    for (int c = 0; c < 2; ++c) v[c] = qv[c] = u32x4{0u, 0u, 0u, 0u};
     if (live) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             v[c] = *reinterpret_cast<const u32x4*>(in + row * ld_in + col + 8 * c);
             if (in_up) v[c] = silu_mul_x8(v[c], *reinterpret_cast<const u32x4*>(in_up + row * ld_in + col + 8 * c));
-            if (pre) pv[c] = *reinterpret_cast<const u32x4*>(pre + col + 8 * c);
             if (post) qv[c] = *reinterpret_cast<const u32x4*>(post + col + 8 * c);
         }
     }
-    // every lane takes part in the DPP exchanges; only live lanes store
-    u32x4 res[2];
-    had128_x16<T>(v, pv, pre != nullptr, qv, post != nullptr, scale, res);
-    if (live) {
+    for (int g = 0; g < groups; ++g) {
+        // constant indices into the argument struct (a runtime index would copy it to scratch)
+        const uint16_t* pre = g == 0 ? hg.pre[0] : g == 1 ? hg.pre[1] : g == 2 ? hg.pre[2] : hg.pre[3];
+        uint16_t* out = g == 0 ? hg.out[0] : g == 1 ? hg.out[1] : g == 2 ? hg.out[2] : hg.out[3];
+        u32x4 pv[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+        if (live && pre) {
 #pragma unroll
-        for (int c = 0; c < 2; ++c) *reinterpret_cast<u32x4*>(out + row * ld_out + col + 8 * c) = res[c];
+            for (int c = 0; c < 2; ++c) pv[c] = *reinterpret_cast<const u32x4*>(pre + col + 8 * c);
+        }
+        // every lane takes part in the DPP exchanges; only live lanes store
+        u32x4 res[2];
+        had128_x16<T>(v, pv, pre != nullptr, qv, post != nullptr, scale, res);
+        if (live) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c) *reinterpret_cast<u32x4*>(out + row * ld_out + col + 8 * c) = res[c];
+        }
     }
 }
 
@@ -152,14 +159,14 @@ int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, 
     }
     if (rows == 0) return EXL3_OK;
     const int64_t jobs = (int64_t) rows * (cols / 128);           // 8 lanes each
-    const dim3 grid((unsigned) ((jobs + 31) / 32), (unsigned) groups);
+    const dim3 grid((unsigned) ((jobs + 31) / 32));
     if (exact)
         hipLaunchKernelGGL(had_kernel<double>, grid, dim3(256), 0, (hipStream_t) stream, (const uint16_t*) in,
-                           (const uint16_t*) in_up, ld_in, hg, ld_out, rows, cols, (const uint16_t*) post,
+                           (const uint16_t*) in_up, ld_in, hg, groups, ld_out, rows, cols, (const uint16_t*) post,
                            R_SCALE * (double) scale);
     else
         hipLaunchKernelGGL(had_kernel<float>, grid, dim3(256), 0, (hipStream_t) stream, (const uint16_t*) in,
-                           (const uint16_t*) in_up, ld_in, hg, ld_out, rows, cols, (const uint16_t*) post,
+                           (const uint16_t*) in_up, ld_in, hg, groups, ld_out, rows, cols, (const uint16_t*) post,
                            (float) (R_SCALE * (double) scale));
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
