@@ -97,10 +97,13 @@ __device__ __forceinline__ f16 f64_to_f16_rto(double v)
 //               128 fp16 values: 35 + 11 mantissa + 7 carry bits), and then bit-exact to the
 //               oracle's float64 matrix product; fp16 spans 40 binades, so an adversarial block
 //               can still round differently.
-//               Used where exactness is the contract (the exl3_had_r_128 entry point).
+//               Used where exactness is the contract: the exl3_had_r_128 entry point and the fused
+//               GEMV's input and output transforms (the reference's strict M = 1 gates assume
+//               correctly rounded fp16 values).
 //   T = float:  24-bit sums, one rounding per stage; the fp16 result can differ from the exact one
 //               in the last place.  Half the VALU cycles and half the lane moves of double; used by
-//               the GEMV and prefill transforms, whose outputs are checked to the rel-L2 bar.
+//               the prefill's transforms (and exl3_had_r_128_f32), whose outputs are checked to the
+//               rel-L2 bar.
 // ------------------------------------------------------------------------------------------
 template <int CTRL>
 __device__ __forceinline__ double dpp_x(double x)
