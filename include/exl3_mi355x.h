@@ -107,7 +107,7 @@ int exl3_gemv(const void* x, int64_t ldx, const void* trellis, void* y, int64_t 
 
 /* 1 <= m <= 32 EXL3 linear, output rows with stride ldy.
  * A_had: optional fp16 scratch of m * k elements (groups * m * k for the grouped forms).  When
- * given and m >= 12 (EXL3_GEMV_PREROT_M), the input is rotated once per group into it,
+ * given and m >= 8 (EXL3_GEMV_PREROT_M), the input is rotated once per group into it,
  * A_had = fp16(Had128(fp16(x * suh))) as in the reference, and the GEMV reads those rows; otherwise
  * every workgroup rotates its own k-range in LDS.  Either way the output is the same, bitwise.
  * Replaces `exl3_gemv_mr(A, B, C, suh, A_had, svh, K, mcg, mul1)` (reference ops.py:85;
@@ -159,7 +159,7 @@ int exl3_gemv_mr_grouped_widths(const void* x, int64_t ldx, const void* const* t
 size_t exl3_gemv_workspace_size_widths(int m, int k, const int* widths, int groups);
 
 /* Rows from which the multi-row GEMV entry points rotate the input once per group into A_had
- * (EXL3_GEMV_PREROT_M, default 12); callers need not provide A_had below it.  No reference
+ * (EXL3_GEMV_PREROT_M, default 8); callers need not provide A_had below it.  No reference
  * counterpart.  Callers: exl3rocm's kernel wrappers. */
 int exl3_gemv_prerot_rows(void);
 

@@ -327,11 +327,12 @@ bool shape_ok(int m, int k, int n, int K)
 // read from gs, the table entries are the caller's contract
 // rows from which the input is rotated once per group by a separate pass into the caller's A_had
 // scratch, instead of by every workgroup for its own k-range (EXL3_GEMV_PREROT_M overrides): at
-// M = 32 the per-workgroup rotation is more VALU work than the decode; at M = 8 the extra pass
-// costs more than it saves (measured on config-1 gate and down)
+// M = 32 the per-workgroup rotation is more VALU work than the decode; with the rows copied into
+// LDS in batches the pass pays from 8 rows (config-1 down at M = 8: 32.9 -> 30.8 us, gate even;
+// at M = 4 it costs 2 us)
 int prerot_rows()
 {
-    static const int v = env_int("EXL3_GEMV_PREROT_M", 12);
+    static const int v = env_int("EXL3_GEMV_PREROT_M", 8);
     return v;
 }
 

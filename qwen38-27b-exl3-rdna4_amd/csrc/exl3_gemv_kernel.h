@@ -432,6 +432,35 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                             bool have_first) __attribute__((always_inline)) {
         const int njobs = (c1 - c0) * M;
         const int i = threadIdx.x >> 4;
+        if (MT_ != 0 && pre) {
+            // pre-rotated rows: a plain copy into LDS, PRE_BATCH passes of loads in flight before
+            // their stores (one round trip per batch instead of one per 16-job pass)
+            constexpr int PRE_BATCH = 8;
+            for (int b0 = i; b0 - (threadIdx.x & 63) / 16 < njobs; b0 += 16 * PRE_BATCH) {
+                u32x4 buf[PRE_BATCH];
+#pragma unroll
+                for (int p = 0; p < PRE_BATCH; ++p) {
+                    const int i3 = b0 + 16 * p;
+                    buf[p] = u32x4{0u, 0u, 0u, 0u};
+                    if (i3 < njobs) {
+                        int m3, col3;
+                        job_src(c0, i3, m3, col3);
+                        buf[p] = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m3 * ldx + col3);
+                    }
+                }
+#pragma unroll
+                for (int p = 0; p < PRE_BATCH; ++p) {
+                    const int i3 = b0 + 16 * p;
+                    if (i3 - (threadIdx.x & 63) / 16 >= njobs) break;   // whole 16-lane groups of the wave
+                    int m3 = 0, col3;
+                    if (i3 < njobs) job_src(c0, i3, m3, col3);
+                    uint16_t* row3 = lds_a + ((i3 < njobs ? i3 / M : 0) * UROWS + m3) * A_ROW;
+                    const u32x4 r3 = approx_row(buf[p], 16, row3, i3 < njobs);
+                    if (i3 < njobs) *reinterpret_cast<u32x4*>(row3 + 8 * (threadIdx.x & 15)) = r3;
+                }
+            }
+            return;
+        }
         if (i - (threadIdx.x & 63) / 16 < njobs) {            // waves with a job (whole 16-lane groups)
             if (!have_first && i < njobs) {
                 int m, col;

@@ -126,7 +126,7 @@ def test_reconstruct_full_size_bitexact(k, n, bits, cb):
 def test_had_r_128_f32_vs_exact():
     """The float32 transform (the prefill's values) against the exact float64 one: equal in all
     but a few elements, and those within one fp16 unit in the last place.  The GEMV's pre-rotated
-    input rows (A_had at m >= 12) are the exact transform's, bitwise."""
+    input rows (A_had from m >= 8) are the exact transform's, bitwise."""
     rng = np.random.default_rng(5)
     x = (rng.standard_normal((64, 5120)) * 2).astype(np.float16)
     su = synth.scales(2, 5120)
