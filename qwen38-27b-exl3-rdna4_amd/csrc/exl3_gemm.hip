@@ -428,42 +428,51 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
                 B[jj] = *reinterpret_cast<const f16x8*>(bf + ((ks * 8 + j) * 64 + (lane ^ bswz(j))) * 16);
             }
         };
-        auto mm = [&](const f16x8* A, int jh, const f16x8* B) __attribute__((always_inline)) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj)
-                    acc[i][4 * jh + jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B[jj], acc[i][4 * jh + jj], 0, 0, 0);
-        };
+        // row tiles of this wave holding live rows: a wave of a small-M tile skips the MFMAs of
+        // its dead row tiles (a loop of its own: a guard inside the full tiles' loop cost 1 %)
+        const int live_rt = min(4, max(0, (M - row0 - 64 * wave + 15) / 16));
         f16x8 A0[4], A1[4], B0[4], B1[4];
         barrier_lds();                                     // B_-1: stage 0 staged
         rd_a(stage(0), 0, A0);
         rd_b(stage(0), 0, 0, B0);
         // sched_barrier pins the issue order: the reads of the next sub-block go out before the
         // MFMAs that hide them, and nothing crosses the workgroup barrier
-        for (int s = 0; s < steps; ++s) {
-            const char* stg = stage(s);
-            rd_b(stg, 0, 1, B1);
-            rd_a(stg, 1, A1);
-            __builtin_amdgcn_sched_barrier(0);
-            mm(A0, 0, B0);
-            __builtin_amdgcn_sched_barrier(0);
-            rd_b(stg, 1, 0, B0);
-            __builtin_amdgcn_sched_barrier(0);
-            mm(A0, 1, B1);
-            __builtin_amdgcn_sched_barrier(0);
-            rd_b(stg, 1, 1, B1);
-            __builtin_amdgcn_sched_barrier(0);
-            mm(A1, 0, B0);
-            barrier_lds();                                 // B_s: stage s read, stage s + 1 staged
-            if (s + 1 < steps) {
-                rd_a(stage(s + 1), 0, A0);
-                rd_b(stage(s + 1), 0, 0, B0);
+        auto main_loop = [&](auto FULL) __attribute__((always_inline)) {
+            auto mm = [&](const f16x8* A, int jh, const f16x8* B) __attribute__((always_inline)) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (decltype(FULL)::value || i < live_rt) {
+#pragma unroll
+                        for (int jj = 0; jj < 4; ++jj)
+                            acc[i][4 * jh + jj] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B[jj], acc[i][4 * jh + jj], 0, 0, 0);
+                    }
+            };
+            for (int s = 0; s < steps; ++s) {
+                const char* stg = stage(s);
+                rd_b(stg, 0, 1, B1);
+                rd_a(stg, 1, A1);
+                __builtin_amdgcn_sched_barrier(0);
+                mm(A0, 0, B0);
+                __builtin_amdgcn_sched_barrier(0);
+                rd_b(stg, 1, 0, B0);
+                __builtin_amdgcn_sched_barrier(0);
+                mm(A0, 1, B1);
+                __builtin_amdgcn_sched_barrier(0);
+                rd_b(stg, 1, 1, B1);
+                __builtin_amdgcn_sched_barrier(0);
+                mm(A1, 0, B0);
+                barrier_lds();                                 // B_s: stage s read, stage s + 1 staged
+                if (s + 1 < steps) {
+                    rd_a(stage(s + 1), 0, A0);
+                    rd_b(stage(s + 1), 0, 0, B0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                mm(A1, 1, B1);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_barrier(0);
-            mm(A1, 1, B1);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        };
+        if (live_rt == 4) main_loop(std::true_type{});
+        else main_loop(std::false_type{});
         if (piece) {
             // this piece's partial out; then count the pieces in, and the last one sums them all
 #pragma unroll
@@ -527,8 +536,10 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
         // xh rows go straight to LDS (buffer loads with the lds bit, 16 bytes a lane): wave pw's
         // load j fills the 1 KB block L = 8 pw + j of the stage's A tiles, row tile L >> 1, slots
         // 64 (L & 1) + lane.  Inverting slot = a_slot(r, c) gives lane's row r and chunk c: each
-        // group of 8 lanes reads one row's 8 chunks, a whole 128-byte line.  Rows past M read row
-        // M - 1 (their outputs are never stored, and rows do not interact)
+        // group of 8 lanes reads one row's 8 chunks, a whole 128-byte line.  Rows past M take an
+        // offset past the buffer's range: the load still issues (the waits below count every
+        // load), but it touches no memory (out-of-range buffer reads return 0), and those rows'
+        // outputs are never stored (rows do not interact)
         const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint16_t*>(gg.xh), 0, (int) ((uint32_t) M * (uint32_t) a.ldx * 2u), RAW_BUFFER_FLAGS);
         uint32_t aoff[8];
@@ -538,8 +549,8 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
             const int qq = 4 * (L & 1) + (lane >> 4), rem = lane & 15;
             const int r = (L >> 1) * 16 + 2 * qq + (rem >> 3);             // row in the tile
             const int c = (rem & 7) ^ qq;                                 // 16-byte chunk
-            const int gr = min(row0 + r, M - 1);
-            aoff[j] = ((uint32_t) gr * (uint32_t) a.ldx + c * 8) * 2u;
+            const int gr = row0 + r;
+            aoff[j] = gr < M ? ((uint32_t) gr * (uint32_t) a.ldx + c * 8) * 2u : 0xFFFFFFF0u;
         }
         auto dma_a = [&](int st, char* stg) __attribute__((always_inline)) {
 #pragma unroll
@@ -640,7 +651,7 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
     // stores write through L2 (device scope), so the end-of-kernel writeback finds no dirty output
     const __amdgpu_buffer_rsrc_t ysrc = __builtin_amdgcn_make_buffer_rsrc(gg.y + (int64_t) row0 * a.ldy, 0, 0x7FFFFFFF,
                                                                           RAW_BUFFER_FLAGS);
-    for (int r0 = 0; r0 < PC::MT; r0 += PC::THREADS / 16) {
+    for (int r0 = 0; r0 < PC::MT && row0 + r0 < M; r0 += PC::THREADS / 16) {
         const int r = r0 + (t >> 4);
         const u32x4 c = *reinterpret_cast<const u32x4*>(ct + r * PC::C_ROW + 8 * l16);
         const u32x4 res = had128_x8<float>(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, r_scale<float>());
