@@ -474,13 +474,25 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
         if (live_rt == 4) main_loop(std::true_type{});
         else main_loop(std::false_type{});
         if (piece) {
-            // this piece's partial out; then count the pieces in, and the last one sums them all
+            // this piece's partial out (its live row tiles); then count the pieces in, and the last
+            // one sums them all
+            if (live_rt == 4) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), prs,
-                                                           part_off(q, i * 8 + j), 0, SC1);
+                    for (int j = 0; j < 8; ++j)
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), prs,
+                                                               part_off(q, i * 8 + j), 0, SC1);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)                // constant indices into acc
+                    if (i < live_rt) {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), prs,
+                                                                   part_off(q, i * 8 + j), 0, SC1);
+                    }
+            }
             __builtin_amdgcn_s_waitcnt(0x0F70);            // vmcnt(0): the partial has landed
             __syncthreads();
             if (t == 0) {
@@ -497,6 +509,7 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
             // dependent round trips at the end of the launch)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                if (i >= live_rt) continue;                // dead row tiles: never stored
                 f32x4 sum[8];
                 for (int pq = 0; pq < a.split; ++pq) {
                     f32x4 v[8];
@@ -697,6 +710,8 @@ PcPlan pc_plan(int M, int K, const int* widths, int groups)
     // a launch of at most half a wave of tiles (small M: one row tile of few columns, e.g. the
     // 40 tiles of a 17408 -> 5120 layer) splits every tile, so that the pieces fill the CUs
     if (full == 0 && 2 * tail <= PC_CUS) p.split = std::min(PC_CUS / tail, (K / KSTEP) / 8);
+    // (more than half a wave and less than one, e.g. the 136 tiles of a 5120 -> 17408 layer at
+    // M <= 256, stays unsplit: 5 pieces measured 9-50 % slower from M = 33 on)
     if (p.split < 2) p.split = 1;
     p.n_full = p.split > 1 ? full * PC_CUS : p.tiles;
     p.ws_bytes = p.split > 1 ? PC_COUNTER_BYTES + (size_t) (p.tiles - p.n_full) * p.split * PC_PIECE_BYTES : 0;

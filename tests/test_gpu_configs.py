@@ -119,16 +119,19 @@ def test_config4_grouped_gate_up():
         assert_close(y[rows, g * n:(g + 1) * n].cpu().numpy(), cpu.linear(x[rows], tr, bits, su, sv, 2), ("gu", g))
 
 
-@pytest.mark.parametrize("name,m,k,n", [("down", 64, 17408, 5120), ("o", 40, 5120, 5120), ("qkv-k", 200, 5120, 1024)])
+@pytest.mark.parametrize("name,m,k,n", [("down", 64, 17408, 5120), ("o", 40, 5120, 5120), ("qkv-k", 200, 5120, 1024),
+                                        ("gate", 33, 5120, 17408), ("gate", 100, 5120, 17408)])
 def test_small_m_prefill_splits_every_tile(name, m, k, n):
     """M in (32, 256]: one row tile of few column tiles (down: 40) is split along K into pieces
-    (down: 6 of ~45 steps) so the launch fills the CUs.  Oracle on rows spread over the tile,
+    (down: 6 of ~45 steps) so the launch fills the CUs (gate, 136 tiles, stays unsplit).  The
+    rows past M of the single row tile are dead (no loads, no MFMAs, no partials; M = 100 leaves
+    a consumer wave with 3 of its 4 row tiles live).  Oracle on rows spread over the tile,
     repeatable bitwise, and equal to the unsplit reference entry point to the parity bar."""
     bits = 4
     tr, su, sv = synth.layer("smallm", name, k, n, bits)
     x = synth.activations(synth.key_of("smallm", name, "x"), m, k)
     X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
-    assert plan(m, k, [n]) > 0
+    assert (plan(m, k, [n]) > 0) == (name != "gate")
     print(f"small-M split {name}: m={m} k={k} n={n}", flush=True)
     y = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, False, True)
     y2 = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, False, True)
