@@ -71,12 +71,11 @@ int exl3_reconstruct_slice(void* W, int64_t ldw, const void* trellis, int k, int
 int exl3_had_r_128(const void* in, int64_t ld_in, void* out, int64_t ld_out, int rows, int cols, const void* pre,
                    const void* post, float scale, void* stream);
 
-/* The same transform with float32 accumulation: the values the prefill GEMM uses for its input and
- * output transforms, which can differ from exl3_had_r_128's exact float64 result in the last fp16
- * place.  Without post (the input side) it runs on the matrix cores (fp16 products, fp32 sums:
- * the prefill's input transforms); with post (the output side) as float32 butterflies (the prefill
- * epilogue's values, which every lane layout of it gives bitwise).  (The fused GEMV's transforms
- * are float64, exl3_had_r_128's values.)
+/* The same transform with float32 accumulation on the matrix cores (fp16 products, fp32 sums):
+ * bitwise the values the prefill GEMM uses for its input transforms (pre) and in its epilogue
+ * (post), which can differ from exl3_had_r_128's exact float64 result in the last fp16 place (by
+ * at most the error of an fp32 summation of a block's 128 terms before that rounding).  (The fused
+ * GEMV's transforms are float64, exl3_had_r_128's values.)
  * No counterpart of its own in the reference (whose had_r_128 serves both roles, ops.py:88,97).
  * Callers: exl3rocm's reconstruct + hgemm_recon prefill route, so that it stays bitwise equal to
  * the fused prefill route. */

@@ -101,9 +101,8 @@ __device__ __forceinline__ f16 f64_to_f16_rto(double v)
 //               GEMV's input and output transforms (the reference's strict M = 1 gates assume
 //               correctly rounded fp16 values).
 //   T = float:  24-bit sums, one rounding per stage; the fp16 result can differ from the exact one
-//               in the last place.  Half the VALU cycles and half the lane moves of double; used by
-//               the prefill's transforms (and exl3_had_r_128_f32), whose outputs are checked to the
-//               rel-L2 bar.
+//               in the last place.  No caller at present: the prefill's float32 transforms run on
+//               the matrix cores (had128_mfma16 below).
 // ------------------------------------------------------------------------------------------
 template <int CTRL>
 __device__ __forceinline__ double dpp_x(double x)
@@ -311,6 +310,72 @@ __device__ __forceinline__ uint32_t had128_x2(uint32_t in, uint32_t pre, bool ha
 
 // the Hadamard scale of every reference call site, per element type
 template <class T> constexpr T r_scale() { return (T) R_SCALE; }
+
+// ------------------------------------------------------------------------------------------
+// 128-point Hadamard of 16 rows on the matrix cores (float32 sums): D = H^T X^T per 16-column
+// tile t (v_mfma_f32_16x16x32_f16, K = 128 in four 32-steps s).  The B operand is the rows' input
+// (lane l: row l & 15, the 8 columns 32 s + 8 (l >> 4) .. + 7), the A operand the +-1 entries
+// H[c(t, i)][32 s + k] (lane l: i = l & 15, the same k), with output column
+// c(t, i) = 32 (t >> 1) + 8 (i >> 2) + 4 (t & 1) + (i & 3), so that lane l of tiles 2p and 2p + 1
+// holds the 8 consecutive outputs 32 p + 8 (l >> 4) .. + 7 of its row.  The sign
+// (-1)^popcount(c & (32 s + k)) splits into (-1)^popcount((t >> 1) & s), which flips a whole
+// 32-step (taken on B: its negated copy), and a part that depends on the lane, the element and
+// t & 1 only: the two constant A fragments below.  The products are exact and the sums fp32, so
+// each output is the rounding of a value within the error bound of an fp32 summation of the
+// block's 128 terms.  Every caller (the standalone float transform and the prefill epilogues)
+// runs this same instruction sequence: their values agree bitwise.
+// ------------------------------------------------------------------------------------------
+struct HadMfmaA {
+    f16x8 a[2];
+};
+
+__device__ __forceinline__ HadMfmaA had_mfma_a()
+{
+    const int lane = __lane_id(), j = lane & 15, g = lane >> 4;
+    HadMfmaA A;
+    // c & k: bits 0-1 (j & 3) & (e & 3), bit 2 (t & 1) & (e >> 2), bits 3-4 (j >> 2) & g
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int par = (__builtin_popcount((j & 3) & (e & 3)) + (tau & (e >> 2)) + __builtin_popcount((j >> 2) & g)) & 1;
+            A.a[tau][e] = par ? (f16) -1.0f : (f16) 1.0f;
+        }
+    return A;
+}
+
+// xb[s]: this lane's row input (pre-scale applied) at columns 32 s + 8 (lane >> 4); emit(p, y) is
+// called for p = 0 .. 3 as soon as tile pair p is done, y = the row's outputs 32 p + 8 (lane >> 4)
+// .. + 7, fp16(D * scale) [* post[p] in fp16] (a caller's store then overlaps the next pair's MFMAs)
+template <class Emit>
+__device__ __forceinline__ void had128_mfma16(const HadMfmaA& A, const u32x4 (&xb)[4], float scale, bool has_post,
+                                              const u32x4 (&post)[4], Emit&& emit)
+{
+    f16x8 bp[4], bn[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        bp[s] = __builtin_bit_cast(f16x8, xb[s]);
+        bn[s] = __builtin_bit_cast(f16x8, xb[s] ^ u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u});
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        f32x4 acc[2];
+#pragma unroll
+        for (int tau = 0; tau < 2; ++tau) {
+            acc[tau] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const bool neg = __builtin_popcount(p & s) & 1;          // (t >> 1) & s, t = 2 p + tau
+                acc[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A.a[tau], neg ? bn[s] : bp[s], acc[tau], 0, 0, 0);
+            }
+        }
+        f16x8 y;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = (f16) (acc[e >> 2][e & 3] * scale);
+        if (has_post) y = y * __builtin_bit_cast(f16x8, post[p]);
+        emit(p, __builtin_bit_cast(u32x4, y));
+    }
+}
 
 // ------------------------------------------------------------------------------------------
 // Codebook constants

@@ -243,14 +243,21 @@ __global__ void __launch_bounds__(Tile<MT>::THREADS) gemm_kernel(const uint16_t*
                     ct[r * TL::C_ROW + c] = f16_bits((f16) acc[i][j][v]);
                 }
         __syncthreads();
-        // 16 lanes per row: y = fp16(fp16(Had128(C)) * svh), 16-byte stores
-        const int l16 = t & 15;
-        const u32x4 sv = *reinterpret_cast<const u32x4*>(svh + col0 + 8 * l16);
-        for (int r0 = 0; r0 < MT; r0 += TL::THREADS / 16) {
-            const int r = r0 + (t >> 4);
-            const u32x4 c = *reinterpret_cast<const u32x4*>(ct + r * TL::C_ROW + 8 * l16);
-            const u32x4 res = had128_x8<float>(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, r_scale<float>());
-            if (row0 + r < M) *reinterpret_cast<u32x4*>(y + (int64_t) (row0 + r) * ldy + col0 + 8 * l16) = res;
+        // y = fp16(fp16(Had128(C)) * svh) on the matrix cores, 16 rows per wave pass
+        // (had128_mfma16: the values of exl3_had_r_128_f32 with post), 16-byte stores
+        const int jr = t & 15, gq = (t >> 4) & 3;
+        u32x4 sv[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) sv[p] = *reinterpret_cast<const u32x4*>(svh + col0 + 32 * p + 8 * gq);
+        const HadMfmaA HA = had_mfma_a();
+        for (int rg = t >> 6; rg < MT / 16; rg += TL::THREADS / 64) {
+            const int r = rg * 16 + jr;
+            u32x4 xb[4];
+#pragma unroll
+            for (int s_ = 0; s_ < 4; ++s_) xb[s_] = *reinterpret_cast<const u32x4*>(ct + r * TL::C_ROW + 32 * s_ + 8 * gq);
+            had128_mfma16(HA, xb, r_scale<float>(), true, sv, [&](int p, u32x4 v) __attribute__((always_inline)) {
+                if (row0 + r < M) *reinterpret_cast<u32x4*>(y + (int64_t) (row0 + r) * ldy + col0 + 32 * p + 8 * gq) = v;
+            });
         }
     } else {
 #pragma unroll
@@ -656,20 +663,27 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
     }
     __syncthreads();                                       // C tile complete in LDS
 
-    // ---- epilogue: y = fp16(fp16(Had128(C)) * svh), 16 lanes per row, 16-byte stores -------------
+    // ---- epilogue: y = fp16(fp16(Had128(C)) * svh) on the matrix cores, 16 rows per wave pass
+    // (had128_mfma16: the values of exl3_had_r_128_f32 with post), 16-byte stores ----------------
     const uint16_t* ct = reinterpret_cast<const uint16_t*>(lds);
-    const int l16 = t & 15;
-    const u32x4 sv = *reinterpret_cast<gc_u32x4*>(as_global(gg.svh) + col0 + 8 * l16);
+    const int jr = t & 15, gq = (t >> 4) & 3;
+    u32x4 sv[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) sv[p] = *reinterpret_cast<gc_u32x4*>(as_global(gg.svh) + col0 + 32 * p + 8 * gq);
     // the tile's rows as one raw buffer from row row0 (offsets below 256 * ldy * 2 bytes); the
     // stores write through L2 (device scope), so the end-of-kernel writeback finds no dirty output
     const __amdgpu_buffer_rsrc_t ysrc = __builtin_amdgcn_make_buffer_rsrc(gg.y + (int64_t) row0 * a.ldy, 0, 0x7FFFFFFF,
                                                                           RAW_BUFFER_FLAGS);
-    for (int r0 = 0; r0 < PC::MT && row0 + r0 < M; r0 += PC::THREADS / 16) {
-        const int r = r0 + (t >> 4);
-        const u32x4 c = *reinterpret_cast<const u32x4*>(ct + r * PC::C_ROW + 8 * l16);
-        const u32x4 res = had128_x8<float>(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, r_scale<float>());
-        if (row0 + r < M)
-            __builtin_amdgcn_raw_buffer_store_b128(res, ysrc, (uint32_t) (((int64_t) r * a.ldy + col0 + 8 * l16) * 2), 0, SC1);
+    const HadMfmaA HA = had_mfma_a();
+    for (int rg = t >> 6; rg < PC::MT / 16 && row0 + 16 * rg < M; rg += PC::THREADS / 64) {
+        const int r = rg * 16 + jr;
+        u32x4 xb[4];
+#pragma unroll
+        for (int s_ = 0; s_ < 4; ++s_) xb[s_] = *reinterpret_cast<const u32x4*>(ct + r * PC::C_ROW + 32 * s_ + 8 * gq);
+        had128_mfma16(HA, xb, r_scale<float>(), true, sv, [&](int p, u32x4 v) __attribute__((always_inline)) {
+            if (row0 + r < M)
+                __builtin_amdgcn_raw_buffer_store_b128(v, ysrc, (uint32_t) (((int64_t) r * a.ldy + col0 + 32 * p + 8 * gq) * 2), 0, SC1);
+        });
     }
 }
 

@@ -94,9 +94,8 @@ struct HadGroups {
     uint16_t* out[EXL3_MAX_GROUPS];
 };
 
-// T: the butterflies' element type (double: exl3_had_r_128 and the GEMV's pre-rotation, the same
-// values as the GEMV's in-kernel transforms; float: the prefill's input transforms and
-// exl3_had_r_128_f32, the same values as the prefill epilogue's)
+// The exact transform (exl3_had_r_128 and the GEMV's pre-rotation: the same values as the GEMV's
+// in-kernel transforms), T = double butterflies; the float32 transform is had_mfma_kernel below.
 // in_up (may be null): the input rows are fp16(fp16(silu(in)) * in_up) (a gated MLP's activation)
 // Every group's output of a block comes from one read of the input block (a fused module's groups
 // differ only in their pre-scale).
@@ -141,22 +140,13 @@ __global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ i
     }
 }
 
-// Input-side float32 transform on the matrix cores: y = fp16(fp16(x * pre) H * r * scale) with
-// fp32 accumulation, H the natural-order Sylvester matrix (symmetric, entries +-1).  One wave per
-// 16 rows x one 128-block, all groups from one read of x.  D = H^T X^T per 16-column tile t of the
-// block (v_mfma_f32_16x16x32_f16, K = 128 in four 32-steps s): the B operand is the rows' input
-// (lane l: row l & 15, the 8 columns 32 s + 8 (l >> 4) .. + 7, one 16-byte load), the A operand the
-// +-1 entries H[c(t, i)][32 s + k] (lane l: i = l & 15, the same k), with output column
-// c(t, i) = 32 (t >> 1) + 8 (i >> 2) + 4 (t & 1) + (i & 3), so that lane l of tiles 2p and 2p + 1
-// holds the 8 consecutive outputs 32 p + 8 (l >> 4) .. + 7 of its row (one 16-byte store).  The
-// sign (-1)^popcount(c & (32 s + k)) splits into (-1)^popcount((t >> 1) & s), which flips a whole
-// 32-step (taken on B: its negated copy), and a part that depends on the lane, the element and
-// t & 1 only: two constant A fragments.
-// The products are exact and the sums fp32, so each output is the fp16 rounding of a value within
-// a few fp32 units of the exact transform, as the butterflies' is (VALU ~3.5 ops per element
-// against ~15 for the float32 butterflies, which left the pass issue-bound).
+// The float32 transform on the matrix cores (had128_mfma16): y = fp16(fp16(x * pre) H * r * scale)
+// [* post], one wave per 16 rows x one 128-block, all groups from one read of x (VALU ~3.5 ops per
+// element against ~15 for float32 butterflies, which left the pass issue-bound).  Each wave reads
+// its whole tile before it writes: in place is safe.
 __global__ void __launch_bounds__(256) had_mfma_kernel(const uint16_t* __restrict__ in, int64_t ld_in, HadGroups hg,
-                                                       int groups, int64_t ld_out, int rows, int cols, float scale)
+                                                       int groups, int64_t ld_out, int rows, int cols,
+                                                       const uint16_t* __restrict__ post, float scale)
 {
     const int nblk = cols / 128;
     const int64_t wid = ((int64_t) blockIdx.x * 256 + threadIdx.x) >> 6;
@@ -167,60 +157,34 @@ __global__ void __launch_bounds__(256) had_mfma_kernel(const uint16_t* __restric
     const int col0 = (int) (wid - rg * nblk) * 128;
     const int64_t row = rg * 16 + j;
     const bool live = row < rows;
-    // B: this lane's row, columns 32 s + 8 g .. + 7 (rows past the end read zeros)
-    u32x4 xb[4];
+    u32x4 xb[4], pv[4];
 #pragma unroll
-    for (int s_ = 0; s_ < 4; ++s_)
+    for (int s_ = 0; s_ < 4; ++s_) {
         xb[s_] = live ? *reinterpret_cast<gc_u32x4*>(as_global(in) + row * ld_in + col0 + 32 * s_ + 8 * g)
                       : u32x4{0u, 0u, 0u, 0u};
-    // A: +-1 of H[c(t, j)][32 s + 8 g + e] for t & 1 = 0 / 1, up to the sign of (t >> 1) & s:
-    // c & k has bits 0-1 (j & 3) & (e & 3), bit 2 (t & 1) & (e >> 2), bits 3-4 (j >> 2) & g
-    f16x8 ha[2];
-#pragma unroll
-    for (int tau = 0; tau < 2; ++tau)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int par = (__builtin_popcount((j & 3) & (e & 3)) + (tau & (e >> 2)) + __builtin_popcount((j >> 2) & g)) & 1;
-            ha[tau][e] = par ? (f16) -1.0f : (f16) 1.0f;
-        }
+        pv[s_] = post ? *reinterpret_cast<gc_u32x4*>(as_global(post) + col0 + 32 * s_ + 8 * g) : u32x4{0u, 0u, 0u, 0u};
+    }
+    const HadMfmaA A = had_mfma_a();
     for (int gi = 0; gi < groups; ++gi) {
         // constant indices into the argument struct (a runtime index would copy it to scratch)
         const uint16_t* pre = gi == 0 ? hg.pre[0] : gi == 1 ? hg.pre[1] : gi == 2 ? hg.pre[2] : hg.pre[3];
         uint16_t* out = gi == 0 ? hg.out[0] : gi == 1 ? hg.out[1] : gi == 2 ? hg.out[2] : hg.out[3];
-        f16x8 bp[4], bn[4];
+        u32x4 xs[4];
 #pragma unroll
         for (int s_ = 0; s_ < 4; ++s_) {
             f16x8 x = __builtin_bit_cast(f16x8, xb[s_]);
             if (pre) x = x * __builtin_bit_cast(f16x8, *reinterpret_cast<gc_u32x4*>(as_global(pre) + col0 + 32 * s_ + 8 * g));
-            bp[s_] = x;
-            bn[s_] = __builtin_bit_cast(f16x8, __builtin_bit_cast(u32x4, x) ^ u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u});
+            xs[s_] = __builtin_bit_cast(u32x4, x);
         }
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            f32x4 acc[2];
-#pragma unroll
-            for (int tau = 0; tau < 2; ++tau) {
-                acc[tau] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int s_ = 0; s_ < 4; ++s_) {
-                    const bool neg = __builtin_popcount(p & s_) & 1;    // (t >> 1) & s, t = 2 p + tau
-                    acc[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ha[tau], neg ? bn[s_] : bp[s_], acc[tau], 0, 0, 0);
-                }
-            }
-            if (live) {
-                f16x8 y;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) y[e] = (f16) (acc[e >> 2][e & 3] * scale);
-                *reinterpret_cast<g_u32x4*>(as_global(out) + row * ld_out + col0 + 32 * p + 8 * g) = __builtin_bit_cast(u32x4, y);
-            }
-        }
+        had128_mfma16(A, xs, scale, post != nullptr, pv, [&](int p, u32x4 v) __attribute__((always_inline)) {
+            if (live) *reinterpret_cast<g_u32x4*>(as_global(out) + row * ld_out + col0 + 32 * p + 8 * g) = v;
+        });
     }
 }
 
 // had_r_128 of one input into `groups` outputs, group i scaled by pre[i] (may be null): one launch
-// (the prefill's input transforms of a fused module); exact: float64 butterflies; else float32,
-// on the matrix cores for input-side transforms (no post scale, no gated input) and as butterflies
-// for output-side ones (the prefill epilogue's values)
+// (the prefill's input transforms of a fused module); exact: float64 butterflies, else float32
+// sums on the matrix cores (the prefill's input transforms and epilogue values)
 int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, int rows, int cols, const void* const* pre,
                int groups, const void* post, float scale, void* stream, bool exact, const void* in_up)
 {
@@ -238,18 +202,17 @@ int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, 
     if (rows == 0) return EXL3_OK;
     const int64_t jobs = (int64_t) rows * (cols / 128);           // 8 lanes each
     const dim3 grid((unsigned) ((jobs + 31) / 32));
-    if (!exact && !post && !in_up) {
+    if (!exact && in_up) return EXL3_EINVAL;                  // the gated input exists in the exact form only
+    if (!exact) {
         const int64_t waves = ((int64_t) rows + 15) / 16 * (cols / 128);
         hipLaunchKernelGGL(had_mfma_kernel, dim3((unsigned) ((waves + 3) / 4)), dim3(256), 0, (hipStream_t) stream,
-                           (const uint16_t*) in, ld_in, hg, groups, ld_out, rows, cols, (float) (R_SCALE * (double) scale));
-    } else if (exact)
+                           (const uint16_t*) in, ld_in, hg, groups, ld_out, rows, cols, (const uint16_t*) post,
+                           (float) (R_SCALE * (double) scale));
+    } else {
         hipLaunchKernelGGL(had_kernel<double>, grid, dim3(256), 0, (hipStream_t) stream, (const uint16_t*) in,
                            (const uint16_t*) in_up, ld_in, hg, groups, ld_out, rows, cols, (const uint16_t*) post,
                            R_SCALE * (double) scale);
-    else
-        hipLaunchKernelGGL(had_kernel<float>, grid, dim3(256), 0, (hipStream_t) stream, (const uint16_t*) in,
-                           (const uint16_t*) in_up, ld_in, hg, groups, ld_out, rows, cols, (const uint16_t*) post,
-                           (float) (R_SCALE * (double) scale));
+    }
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 

@@ -147,27 +147,35 @@ def test_had_r_128_f32_vs_exact():
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 128), (37, 384), (16, 5120), (300, 1024)])
-def test_had_r_128_f32_input_side_ragged_and_in_place(rows, cols):
-    """The input-side float32 transform (matrix cores, 16 rows per wave) on row counts that are
-    not multiples of 16, in place and out of place, with and without pre: nearly all outputs equal
-    to the exact transform's, every one within the exact value's fp16 rounding plus the error bound
-    of any fp32 summation of the block's 128 terms (127 u sum|terms|, u = 2^-24), and no row outside
-    the call touched."""
+def test_had_r_128_f32_ragged_and_in_place(rows, cols):
+    """The float32 transform (matrix cores, 16 rows per wave) on row counts that are not multiples
+    of 16, in place, with pre, post or neither: nearly all outputs equal to the exact transform's,
+    every one within the exact value's fp16 rounding plus the error bound of any fp32 summation of
+    the block's 128 terms (127 u sum|terms|, u = 2^-24; with post, that bound and the pre-post
+    value's rounding scaled by |post|), and no row outside the call touched."""
     rng = np.random.default_rng(rows + cols)
     x = (rng.standard_normal((rows + 3, cols)) * 3).astype(np.float16)
     su = synth.scales(rows, cols)
-    X, SU = to_dev(x, su)
-    for pre in (SU, None):
+    sv = synth.scales(rows + 1, cols)
+    X, SU, SV = to_dev(x, su, sv)
+    for pre, post in ((SU, None), (None, None), (None, SV)):
         ex = X.clone()
-        E.had_r_128(X[:rows], ex[:rows], pre, None, 1.0)
+        E.had_r_128(X[:rows], ex[:rows], pre, post, 1.0)
         fa = X.clone()
-        E.had_r_128(fa[:rows], fa[:rows], pre, None, 1.0, exact=False)       # in place
+        E.had_r_128(fa[:rows], fa[:rows], pre, post, 1.0, exact=False)       # in place
         e = ex.cpu().numpy()[:rows].astype(np.float64)
         f = fa.cpu().numpy()
         xs = (x[:rows] * su).astype(np.float16) if pre is not None else x[:rows]
-        mag =np.abs(xs.astype(np.float64)).reshape(rows, -1, 128).sum(axis=2) * 0.088388347648
-        bound = np.repeat(mag, 128, axis=1) * 127 * 2.0 ** -24 + np.spacing(np.abs(e).astype(np.float16)).astype(np.float64)
-        assert (np.abs(f[:rows].astype(np.float64) - e) <= bound).all()
+        mag = np.abs(xs.astype(np.float64)).reshape(rows, -1, 128).sum(axis=2) * 0.088388347648
+        bound = np.repeat(mag, 128, axis=1) * 127 * 2.0 ** -24
+        if post is not None:
+            # fp16(a * post), with a within (bound + a's own rounding) of the exact pre-post value
+            a_e = X.clone()
+            E.had_r_128(X[:rows], a_e[:rows], None, None, 1.0)
+            a_e = a_e.cpu().numpy()[:rows]
+            bound = (bound + np.spacing(np.abs(a_e)).astype(np.float64)) * np.abs(sv.astype(np.float64))
+        bound = bound + np.spacing(np.abs(e).astype(np.float16)).astype(np.float64)
+        assert (np.abs(f[:rows].astype(np.float64) - e) <= bound).all(), (pre is not None, post is not None)
         assert (f[:rows].view(np.int16) != ex.cpu().numpy()[:rows].view(np.int16)).mean() < 0.01
         assert np.array_equal(f[rows:].view(np.int16), x[rows:].view(np.int16)), "rows past the call untouched"
 
