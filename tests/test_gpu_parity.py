@@ -461,6 +461,24 @@ def test_prefill_split_tail_parity_and_determinism():
     assert_close(y1[:, c_split:].cpu().numpy(), y0[:, c_split:].cpu().numpy(), "split vs unsplit")
 
 
+def test_prefill_tile_kernel_matches_pc_kernel(monkeypatch):
+    """The 128 x 128 fused-epilogue GEMM (taken for operands beyond 32-bit buffer offsets; forced
+    here with EXL3_GEMM_KERNEL=tile) equals the producer/consumer kernel bitwise on unsplit tiles
+    (each output sees the same MFMA sequence, and both epilogues run the same matrix-core output
+    transform), ragged rows included, and meets the oracle bar."""
+    m, k, n, bits = 300, 1024, 384, 4
+    x, tr, su, sv = layer(k, n, bits, m=m)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    y_pc = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    E.exl3_gemm_trellis(X, T, y_pc, SU, torch.empty_like(X), SV, bits, False, True)     # unsplit
+    monkeypatch.setenv("EXL3_GEMM_KERNEL", "tile")
+    y_t = torch.full((m, n), float("nan"), dtype=torch.float16, device=DEV)
+    E.exl3_gemm_trellis(X, T, y_t, SU, torch.empty_like(X), SV, bits, False, True)
+    torch.cuda.synchronize()
+    assert torch.equal(y_t.view(torch.int16), y_pc.view(torch.int16))
+    assert_close(y_t.cpu().numpy(), cpu.linear(x, tr, bits, su, sv, 2), "tile kernel")
+
+
 def test_linear_groups_prefill_matches_per_group_linear():
     """linear_groups at M > 32 (one grouped GEMM launch per equal-K run, mixed bitrates split into
     runs) == the concatenation of per-group linear calls, bitwise."""
