@@ -461,6 +461,37 @@ def test_prefill_split_tail_parity_and_determinism():
     assert_close(y1[:, c_split:].cpu().numpy(), y0[:, c_split:].cpu().numpy(), "split vs unsplit")
 
 
+def test_prefill_split_tail_graph_replays():
+    """A prefill with a split tail (260 tiles: 256 whole, 4 split along K) captured in a graph after
+    an eager warm-up on the capture stream (which sizes its workspace): every replay, with eager
+    work and synchronisations between them, equals the eager result bitwise (the last piece of
+    each split tile resets its counter for the next replay; no memset node in the graph)."""
+    m, k, bits = 256, 1024, 4
+    n = 128 * 260
+    tr, su, sv = synth.layer("pfsplit-graph", 0, k, n, bits)
+    x = synth.activations(synth.key_of("pfsplit-graph", "x"), m, k)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        eager = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, False, True)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        y = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, False, True)
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), eager.view(torch.int16))
+        with torch.cuda.stream(s):
+            again = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, False, True)   # eager between replays
+        torch.cuda.synchronize()
+        assert torch.equal(again.view(torch.int16), eager.view(torch.int16))
+
+
 def test_prefill_tile_kernel_matches_pc_kernel(monkeypatch):
     """The 128 x 128 fused-epilogue GEMM (taken for operands beyond 32-bit buffer offsets; forced
     here with EXL3_GEMM_KERNEL=tile) equals the producer/consumer kernel bitwise on unsplit tiles
