@@ -1,14 +1,15 @@
 // exl3_gemm.hip -- prefill (large-M) EXL3 linear and dense fp16 GEMM for gfx950.
 //
 // exl3_gemm_trellis: y = had_out(fp16(had_in(x) . W), svh) in two launches:
-//   1. had_in   xh = fp16(Had128(fp16(x * suh)))            (had_kernel, float32 butterflies)
-//   2. GEMM     C = fp16(xh . W) on 128 x 128 output tiles, K step 64: each step the workgroup
-//               decodes its 4 x 8 trellis tiles (one q-block per thread) straight into LDS in
-//               MFMA B-fragment order and stages the xh rows in A-fragment order;
-//               v_mfma_f32_16x16x32_f16, fp32 accumulation; LDS double-buffered.  The epilogue
-//               applies y = fp16(fp16(Had128(C)) * svh) to the tile's whole 128-column blocks
-//               (float32 butterflies, the values of exl3_had_r_128_f32: +1.1 % over float64 on
-//               the configuration-4 chunk; the rows are checked to the rel-L2 bar).
+//   1. had_in   xh = fp16(Had128(fp16(x * suh)))    (had_mfma_kernel: fp32 sums on the matrix cores)
+//   2. GEMM     C = fp16(xh . W): the producer / consumer kernel below (256 x 128 tiles), or for
+//               operands beyond 32-bit buffer offsets the 128 x 128 kernel here, K step 64: each
+//               step the workgroup decodes its 4 x 8 trellis tiles (one q-block per thread)
+//               straight into LDS in MFMA B-fragment order and stages the xh rows in A-fragment
+//               order; v_mfma_f32_16x16x32_f16, fp32 accumulation; LDS double-buffered.  Both
+//               epilogues apply y = fp16(fp16(Had128(C)) * svh) to the tile's whole 128-column
+//               blocks on the matrix cores (had128_mfma16, the values of exl3_had_r_128_f32; the
+//               rows are checked to the rel-L2 bar).
 // exl3_hgemm_recon is the same GEMM with a dense fp16 W[k, n] as the B source and a plain
 // fp16 C epilogue.
 #include "exl3_device.h"
