@@ -106,6 +106,15 @@ int exl3_gemv(const void* x, int64_t ldx, const void* trellis, void* y, int64_t 
               const void* svh, int m, int k, int n, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
               void* stream);
 
+/* exl3_gemv with an fp32 output y[n]: C = H(x*suh) . W stays fp32 (no fp16 rounding) and
+ * y = (float) (H(C) * r) * svh (float64 butterflies over the fp32 C).  m != 1 declines (returns 1)
+ * without touching y.  Replaces `exl3_gemv(A, B, C, ...)` called with a float32 C (reference
+ * tests/test_fused_had.py:59-65,153-158; the fused epilogue's c_fp32 form,
+ * patches/experimental-full.patch:638-653). */
+int exl3_gemv_f32(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh, void* A_had,
+                  const void* svh, int m, int k, int n, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
+                  void* stream);
+
 /* 1 <= m <= 32 EXL3 linear, output rows with stride ldy.
  * A_had: optional fp16 scratch of m * k elements (groups * m * k for the grouped forms).  When
  * given and m >= 8 (EXL3_GEMV_PREROT_M), the input is rotated once per group into it,

@@ -271,14 +271,10 @@ __device__ __forceinline__ void had128_x16(const u32x4 (&in)[2], const u32x4 (&p
 // (ds_swizzle), bit 6 lane xor 32 (v_permlane32_swap).  A fourth of wht128_x8's instructions per
 // lane: the latency form for the GEMV's single-row input and output transforms, which are on every
 // launch's critical path.
+// The stages of the single-row layout after bit 0 (v = {a + b, a - b} of the lane's two elements).
 template <class T>
-__device__ __forceinline__ uint32_t had128_x2(uint32_t in, uint32_t pre, bool has_pre, uint32_t post, bool has_post,
-                                              T scale)
+__device__ __forceinline__ void wht128_x2_rest(T (&v)[2])
 {
-    f16x2 x = __builtin_bit_cast(f16x2, in);
-    if (has_pre) x = x * __builtin_bit_cast(f16x2, pre);
-    const T a = (T) x[0], b = (T) x[1];
-    T v[2] = {a + b, a - b};
     const int l = __lane_id();
     T p[2];
 #pragma unroll
@@ -303,9 +299,32 @@ __device__ __forceinline__ uint32_t had128_x2(uint32_t in, uint32_t pre, bool ha
         halves_x(v[i], lo, hi);
         v[i] = __builtin_fma(l & 32 ? T(-1) : T(1), hi, lo);
     }
+}
+
+template <class T>
+__device__ __forceinline__ uint32_t had128_x2(uint32_t in, uint32_t pre, bool has_pre, uint32_t post, bool has_post,
+                                              T scale)
+{
+    f16x2 x = __builtin_bit_cast(f16x2, in);
+    if (has_pre) x = x * __builtin_bit_cast(f16x2, pre);
+    const T a = (T) x[0], b = (T) x[1];
+    T v[2] = {a + b, a - b};
+    wht128_x2_rest(v);
     f16x2 y = {scaled_f16(v[0], scale), scaled_f16(v[1], scale)};
     if (has_post) y = y * __builtin_bit_cast(f16x2, post);
     return __builtin_bit_cast(uint32_t, y);
+}
+
+// The same layout on two fp32 inputs with an fp32 output: float64 butterflies (exact sums of the
+// fp32 values while a block spans at most 22 binades), then (float) (v * scale) * post, post the
+// lane's two fp16 scale values (the fp32-output GEMV's output transform)
+__device__ __forceinline__ void had128_x2_f32(float a, float b, uint32_t post, double scale, float& o0, float& o1)
+{
+    double v[2] = {(double) a + (double) b, (double) a - (double) b};
+    wht128_x2_rest(v);
+    const f16x2 p = __builtin_bit_cast(f16x2, post);
+    o0 = (float) (v[0] * scale) * (float) p[0];
+    o1 = (float) (v[1] * scale) * (float) p[1];
 }
 
 // the Hadamard scale of every reference call site, per element type

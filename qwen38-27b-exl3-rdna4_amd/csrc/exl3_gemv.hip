@@ -395,8 +395,9 @@ int silu_prerot_rows()
 int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widths, int groups,
                 const int64_t* const* tabs, int64_t ldy, int m, int k, int K, int mcg, int mul1, void* ws,
                 size_t ws_bytes, void* stream, bool gated = false, void* xr = nullptr, int approx = 0,
-                const void* x_up = nullptr)
+                const void* x_up = nullptr, bool f32out = false)
 {
+    if (f32out && (m != 1 || gated || tabs || approx || x_up)) return EXL3_EINVAL;
     if (x_up && (gated || tabs || approx || (((uintptr_t) x_up) & 15))) return EXL3_EINVAL;
     if (approx && (gated || approx > 2)) return EXL3_EINVAL;
     if (gated && (groups != 2 || tabs || widths[0] != widths[1] || ldy < widths[0])) return EXL3_EINVAL;
@@ -474,6 +475,7 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
     a.ldy = ldy;
     a.counters = (uint32_t*) ws;
     a.part = (float*) ((char*) ws + COUNTER_BYTES);
+    if (f32out) return launch_gemv_f32out(a, K, codebook_of(mcg, mul1), p.total_wgs, (hipStream_t) stream);
     if (approx) return launch_gemv_approx(a, K, 2 + approx, p.total_wgs, (hipStream_t) stream);
     if (a.x_up) return launch_gemv_silu_in(a, K, codebook_of(mcg, mul1), p.total_wgs, (hipStream_t) stream);
     return gated ? launch_gemv_gated(a, K, codebook_of(mcg, mul1), p.total_wgs, (hipStream_t) stream)
@@ -557,6 +559,18 @@ int exl3_gemv(const void* x, int64_t ldx, const void* trellis, void* y, int64_t 
     if (m != 1) return EXL3_DECLINED;
     GemvGroup g{(const uint32_t*) trellis, (const uint16_t*) suh, (const uint16_t*) svh, (uint16_t*) y};
     return gemv_common(x, ldx, &g, &n, 1, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream);
+}
+
+int exl3_gemv_f32(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh, void* A_had,
+                  const void* svh, int m, int k, int n, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
+                  void* stream)
+{
+    (void) A_had;
+    if (!trellis || !y || !suh || !svh) return EXL3_EINVAL;
+    if (m != 1) return EXL3_DECLINED;
+    GemvGroup g{(const uint32_t*) trellis, (const uint16_t*) suh, (const uint16_t*) svh, (uint16_t*) y};
+    return gemv_common(x, ldx, &g, &n, 1, nullptr, ldy, m, k, K, mcg, mul1, workspace, ws_bytes, stream, false, nullptr, 0,
+                       nullptr, true);
 }
 
 int exl3_gemv_mr(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh, void* A_had,

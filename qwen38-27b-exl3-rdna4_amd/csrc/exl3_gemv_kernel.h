@@ -202,8 +202,10 @@ struct Split {
 //   FORM_PLAIN   the EXL3 linear of each group;
 //   FORM_GATED   groups 0 (gate) and 1 (up) of equal width; the workgroup completing a block of
 //                both writes fp16(fp16(silu(gate)) * up) to g[0].y instead of the two outputs;
-//   FORM_SILU_IN the input rows are fp16(fp16(silu(x)) * x_up), formed as they load.
-enum { FORM_PLAIN = 0, FORM_GATED = 1, FORM_SILU_IN = 2 };
+//   FORM_SILU_IN the input rows are fp16(fp16(silu(x)) * x_up), formed as they load;
+//   FORM_F32OUT  the plain linear with an fp32 output (single row only): C stays fp32 (no fp16
+//                rounding) and y = (float) (H C r) * svh.
+enum { FORM_PLAIN = 0, FORM_GATED = 1, FORM_SILU_IN = 2, FORM_F32OUT = 3 };
 
 template <int BITS, int CB, int MT_, int FORM>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_SIMD, WAVES_PER_SIMD))) gemv_kernel(GemvArgs a)
@@ -938,7 +940,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                         for (int ii = 0; ii < RED_BATCH; ++ii)
                             if (cc0 + ii < nc) sum += v[ii];
                     }
-                    lds_c[(r * M + (el >> 7)) * A_ROW + (el & 127)] = f16_bits((f16) sum);
+                    if constexpr (FORM == FORM_F32OUT)
+                        reinterpret_cast<float*>(lds_c)[r * 128 + el] = sum;          // single row: el < 128
+                    else
+                        lds_c[(r * M + (el >> 7)) * A_ROW + (el & 127)] = f16_bits((f16) sum);
                 }
             } else {
                 for (int e0 = threadIdx.x; e0 < total; e0 += 512) {
@@ -1011,7 +1016,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 __syncthreads();
                 continue;
             }
-            if constexpr (MT_ == 0) {
+            if constexpr (MT_ == 0 && FORM == FORM_F32OUT) {
+                // fp32 output: the block's fp32 C, float64 butterflies, (float) (v r) * svh
+                if (wave < rb) {
+                    const int cb = seg0_cb + b0 + s_list[r0 + wave];
+                    const float* cf = reinterpret_cast<const float*>(lds_c) + wave * 128 + 2 * lane;
+                    float o0, o1;
+                    had128_x2_f32(cf[0], cf[1], sv_first.x, r_scale<double>(), o0, o1);
+                    __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(o0), __float_as_uint(o1)}, ysrc,
+                                                          (uint32_t) ((cb * 128 + 2 * lane) * 4), 0, SC1);
+                }
+                __syncthreads();                               // lds_c free for the next blocks
+                continue;
+            } else if constexpr (MT_ == 0) {
                 // output Hadamard + svh of a single row: one wave per block, two columns a lane
                 if (wave < rb) {
                     const int cb = seg0_cb + b0 + s_list[r0 + wave];
@@ -1042,11 +1059,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     }
 }
 
-// LDS: chunk_units x (m + 1) input rows, then the C rows of the blocks reduced side by side
-inline size_t lds_bytes(int M, int cu, bool gated)
+// LDS: chunk_units x (m + 1) input rows, then the C rows of the blocks reduced side by side (the
+// fp32-output form: two fp32 rows of 128, the room of four fp16 rows)
+inline size_t lds_bytes(int M, int cu, bool gated, bool f32out = false)
 {
     // blocks (gated: pairs) reduced side by side x rows: as RB in the kernel
-    const int c_rows = gated ? (M == 1 ? 4 : 2 * M) : (M <= 8 ? 2 * M : M);
+    const int c_rows = gated || f32out ? (M == 1 ? 4 : 2 * M) : (M <= 8 ? 2 * M : M);
     return ((size_t) cu * (M + 1) + c_rows) * A_ROW * 2;
 }
 
@@ -1054,7 +1072,7 @@ template <int BITS, int CB, int MT_, int FORM>
 int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t stream)
 {
     hipLaunchKernelGGL((gemv_kernel<BITS, CB, MT_, FORM>), dim3(wgs), dim3(256),
-                       lds_bytes(a.M, a.chunk_units, FORM == FORM_GATED), stream, a);
+                       lds_bytes(a.M, a.chunk_units, FORM == FORM_GATED, FORM == FORM_F32OUT), stream, a);
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 
@@ -1094,5 +1112,7 @@ int launch_gemv_impl(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s
 // gated instantiations live in exl3_gemv_gated.hip, SiLU-input ones in exl3_gemv_silu.hip
 int launch_gemv_gated(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s);
 int launch_gemv_silu_in(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s);
+// the fp32-output single-row instantiations live in exl3_gemv_f32.hip
+int launch_gemv_f32out(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s);
 // approximate mul1 instantiations (codebook ids 3 and 4) live in exl3_gemv_approx.hip
 int launch_gemv_approx(const GemvArgs& a, int bits, int cb, int wgs, hipStream_t s);

@@ -33,6 +33,7 @@ SIGNATURES = {
     "exl3_gemv_workspace_size": (_sz, [_i, _i, _i, _i, _i]),
     "exl3_gemv_mr_supported": (_i, [_i, _i, _i, _i, _i, _i]),
     "exl3_gemv": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
+    "exl3_gemv_f32": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "exl3_gemv_mr": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "exl3_gemv_mr_grouped": (_i, [_p, _i64, _pp, _p, _i64, _pp, _p, _pp, _i, _i, _i, _i, _i, _i, _i, _i, _p, _sz,
                                   _p]),

@@ -156,8 +156,9 @@ def _rows(x: torch.Tensor):
     return x2, x2.shape[0], k
 
 
-def _ldy(y: torch.Tensor, n: int) -> int:
-    _need(y.dtype == torch.float16 and y.stride(-1) == 1, "output must be fp16 with unit column stride")
+def _ldy(y: torch.Tensor, n: int, fp32: bool = False) -> int:
+    want = torch.float32 if fp32 else torch.float16
+    _need(y.dtype == want and y.stride(-1) == 1, f"output must be {'fp32' if fp32 else 'fp16'} with unit column stride")
     return y.stride(-2) if y.dim() >= 2 and y.shape[-2] > 1 else max(n, y.shape[-1])
 
 
@@ -166,16 +167,20 @@ def exl3_gemv_mr_supported(m: int, k: int, n: int, K: int, mcg: bool, mul1: bool
 
 
 def exl3_gemv(A, B, C, suh, A_had, svh, mcg: bool, mul1: bool) -> int:
-    """M == 1 linear; returns 0 (done) or 1 (declined, C untouched)."""
+    """M == 1 linear; returns 0 (done) or 1 (declined, C untouched).  A float32 C takes the fp32
+    output (C = H(x suh) . W kept in fp32, y = H(C) r svh; reference tests/test_fused_had.py:153-158)."""
     _cuda(A, B, C, suh, svh)
+    _need(C.dtype in (torch.float16, torch.float32), "exl3_gemv: fp16 or fp32 output")
     x2, m, k = _rows(A)
     n = svh.shape[0]
     K = _bits_of(B)
     ws = workspace(A.device, gemv_workspace_bytes(max(m, 1), k, n, K))
-    return L.check(L.lib().exl3_gemv(x2.data_ptr(), x2.stride(0) if m > 1 else k, B.data_ptr(), C.data_ptr(),
-                                     _ldy(C, n), suh.data_ptr(), A_had.data_ptr() if A_had is not None else None,
-                                     svh.data_ptr(), m, k, n, K, *_cb_flags(mcg, mul1), ws.data_ptr(), ws.numel(),
-                                     _stream(A)), "exl3_gemv")
+    f32 = C.dtype == torch.float32
+    fn = L.lib().exl3_gemv_f32 if f32 else L.lib().exl3_gemv
+    return L.check(fn(x2.data_ptr(), x2.stride(0) if m > 1 else k, B.data_ptr(), C.data_ptr(),
+                      _ldy(C, n, f32), suh.data_ptr(), A_had.data_ptr() if A_had is not None else None,
+                      svh.data_ptr(), m, k, n, K, *_cb_flags(mcg, mul1), ws.data_ptr(), ws.numel(),
+                      _stream(A)), "exl3_gemv")
 
 
 _prerot = None

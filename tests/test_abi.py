@@ -92,6 +92,10 @@ def test_invalid_arguments_return_before_any_launch():
     assert L.exl3_decode(None, dummy, 16, 0, 1, None) == _lib.EINVAL
     assert L.exl3_gemv(dummy, 128, dummy, dummy, 128, dummy, None, dummy, 2, 128, 128, 4, 0, 1, dummy, 1 << 20,
                        None) == _lib.DECLINED
+    assert L.exl3_gemv_f32(dummy, 128, dummy, dummy, 128, dummy, None, dummy, 2, 128, 128, 4, 0, 1, dummy, 1 << 20,
+                           None) == _lib.DECLINED
+    assert L.exl3_gemv_f32(dummy, 128, dummy, None, 128, dummy, None, dummy, 1, 128, 128, 4, 0, 1, dummy, 1 << 20,
+                           None) == _lib.EINVAL
     assert L.exl3_gemv_mr(dummy, 128, dummy, dummy, 128, dummy, None, dummy, 40, 128, 128, 4, 0, 1, dummy, 1 << 20,
                           None) == _lib.DECLINED
     assert L.exl3_gemv_mr(dummy, 128, dummy, dummy, 128, dummy, None, dummy, 1, 128, 128, 4, 0, 1, dummy, 0,

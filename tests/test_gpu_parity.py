@@ -349,6 +349,29 @@ def test_zero_input():
     assert torch.isfinite(y).all() and y.abs().max().item() == 0.0
 
 
+@pytest.mark.parametrize("k,n,bits,cb", [(512, 256, 4, 2), (5120, 1024, 4, 2), (17408, 5120, 3, 1), (1024, 768, 8, 0)])
+def test_gemv_fp32_output_vs_float64(k, n, bits, cb):
+    """The fp32-output M = 1 GEMV (the reference's exl3_gemv with a float32 C): against the oracle's
+    arithmetic in float64 with C left unrounded -- y = H(xh . W) r svh, xh the oracle's fp16 input
+    transform, W its decoded fp16 weights -- to fp32 accumulation accuracy, and within the fp16
+    form's roundings of the fp16 output."""
+    import scipy.linalg
+    x, tr, su, sv = layer(k, n, bits)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    y32 = torch.full((1, n), float("nan"), dtype=torch.float32, device=DEV)
+    y16 = torch.empty(1, n, dtype=torch.float16, device=DEV)
+    assert E.exl3_gemv(X, T, y32, SU, None, SV, cb == 1, cb == 2) == 0
+    assert E.exl3_gemv(X, T, y16, SU, None, SV, cb == 1, cb == 2) == 0
+    torch.cuda.synchronize()
+    xh = cpu.had_in(x, su).astype(np.float64)
+    C = xh @ cpu.reconstruct(tr, bits, cb).astype(np.float64)
+    ref = (C.reshape(1, -1, 128) @ scipy.linalg.hadamard(128)).reshape(1, -1) * 0.088388347648 * sv.astype(np.float64)
+    got = y32.cpu().numpy().astype(np.float64)
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert rel < 1e-5, rel
+    assert_close(y16.cpu().numpy(), got, "fp16 form vs fp32 form")
+
+
 def test_ineligible_declines_without_modifying_outputs():
     x, tr, su, sv = layer(256, 128, 3, m=2)
     X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
