@@ -15,7 +15,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 OUT = os.path.join(HERE, "exl3rocm", "libexl3_mi355x.so")
 SOURCES = ["exl3_gemv.hip", "exl3_gemv_gated.hip", "exl3_gemv_silu.hip", "exl3_gemv_approx.hip", "exl3_gemv_f32.hip",
-           "exl3_gemm.hip", "exl3_noalloc.hip"]
+           "exl3_gemm.hip", "exl3_had.hip", "exl3_noalloc.hip"]
 # Per-source extra flags.  The trellis decode (the GEMV's loop and the prefill producers') is long
 # chains of packed-math (VOP3P) ops whose results need extra wait states on gfx950; the ILP
 # scheduler interleaves the independent chains so the hazards are hidden instead of padded with
@@ -23,6 +23,9 @@ SOURCES = ["exl3_gemv.hip", "exl3_gemv_gated.hip", "exl3_gemv_silu.hip", "exl3_g
 EXTRA = {src: ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]
          for src in ("exl3_gemv.hip", "exl3_gemv_gated.hip", "exl3_gemv_silu.hip", "exl3_gemv_approx.hip", "exl3_gemv_f32.hip",
                      "exl3_gemm.hip")}
+# The float transform's MFMA results feed VALU conversions directly: with the VGPR form of the MFMA
+# they need no accumulator-register reads (32 per group of 16 rows x 128 columns).
+EXTRA["exl3_had.hip"] = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",

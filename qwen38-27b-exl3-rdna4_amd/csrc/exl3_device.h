@@ -18,6 +18,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include "../../include/exl3_mi355x.h"
 
 namespace exl3 {
 
@@ -330,6 +331,12 @@ __device__ __forceinline__ void had128_x2_f32(float a, float b, uint32_t post, d
 // the Hadamard scale of every reference call site, per element type
 template <class T> constexpr T r_scale() { return (T) R_SCALE; }
 
+// the (pre, out) pair of each group of one launch (a fused module's input transforms read one x)
+struct HadGroups {
+    const uint16_t* pre[EXL3_MAX_GROUPS];
+    uint16_t* out[EXL3_MAX_GROUPS];
+};
+
 // ------------------------------------------------------------------------------------------
 // 128-point Hadamard of 16 rows on the matrix cores (float32 sums): D = H^T X^T per 16-column
 // tile t (v_mfma_f32_16x16x32_f16, K = 128 in four 32-steps s).  The B operand is the rows' input
@@ -338,14 +345,15 @@ template <class T> constexpr T r_scale() { return (T) R_SCALE; }
 // c(t, i) = 32 (t >> 1) + 8 (i >> 2) + 4 (t & 1) + (i & 3), so that lane l of tiles 2p and 2p + 1
 // holds the 8 consecutive outputs 32 p + 8 (l >> 4) .. + 7 of its row.  The sign
 // (-1)^popcount(c & (32 s + k)) splits into (-1)^popcount((t >> 1) & s), which flips a whole
-// 32-step (taken on B: its negated copy), and a part that depends on the lane, the element and
-// t & 1 only: the two constant A fragments below.  The products are exact and the sums fp32, so
+// 32-step, and a part that depends on the lane, the element and t & 1 only: the constant A
+// fragments below, kept with both signs so that the flip selects a fragment instead of negating
+// the input.  The products are exact and the sums fp32, so
 // each output is the rounding of a value within the error bound of an fp32 summation of the
 // block's 128 terms.  Every caller (the standalone float transform and the prefill epilogues)
 // runs this same instruction sequence: their values agree bitwise.
 // ------------------------------------------------------------------------------------------
 struct HadMfmaA {
-    f16x8 a[2];
+    f16x8 a[2], an[2];          // t & 1 = 0, 1; an = -a
 };
 
 __device__ __forceinline__ HadMfmaA had_mfma_a()
@@ -359,6 +367,7 @@ __device__ __forceinline__ HadMfmaA had_mfma_a()
         for (int e = 0; e < 8; ++e) {
             const int par = (__builtin_popcount((j & 3) & (e & 3)) + (tau & (e >> 2)) + __builtin_popcount((j >> 2) & g)) & 1;
             A.a[tau][e] = par ? (f16) -1.0f : (f16) 1.0f;
+            A.an[tau][e] = par ? (f16) 1.0f : (f16) -1.0f;
         }
     return A;
 }
@@ -370,12 +379,6 @@ template <class Emit>
 __device__ __forceinline__ void had128_mfma16(const HadMfmaA& A, const u32x4 (&xb)[4], float scale, bool has_post,
                                               const u32x4 (&post)[4], Emit&& emit)
 {
-    f16x8 bp[4], bn[4];
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        bp[s] = __builtin_bit_cast(f16x8, xb[s]);
-        bn[s] = __builtin_bit_cast(f16x8, xb[s] ^ u32x4{0x80008000u, 0x80008000u, 0x80008000u, 0x80008000u});
-    }
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
         f32x4 acc[2];
@@ -385,7 +388,8 @@ __device__ __forceinline__ void had128_mfma16(const HadMfmaA& A, const u32x4 (&x
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const bool neg = __builtin_popcount(p & s) & 1;          // (t >> 1) & s, t = 2 p + tau
-                acc[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A.a[tau], neg ? bn[s] : bp[s], acc[tau], 0, 0, 0);
+                acc[tau] = __builtin_amdgcn_mfma_f32_16x16x32_f16(neg ? A.an[tau] : A.a[tau],
+                                                                  __builtin_bit_cast(f16x8, xb[s]), acc[tau], 0, 0, 0);
             }
         }
         f16x8 y;

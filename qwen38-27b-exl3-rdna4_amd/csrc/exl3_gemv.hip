@@ -88,14 +88,10 @@ __global__ void __launch_bounds__(256) reconstruct_kernel(const uint32_t* __rest
 // had_r_128: out = fp16(Had128(in [* pre]) * r * scale) [* post]; one 8-lane group per 128-block,
 // 8 blocks per wave (reference binding `had_r_128`, vllm_plugin/exl3rocm/ops.py:88,97)
 // ============================================================================================
-// the (pre, out) pair of each group of one launch (a fused module's input transforms read one x)
-struct HadGroups {
-    const uint16_t* pre[EXL3_MAX_GROUPS];
-    uint16_t* out[EXL3_MAX_GROUPS];
-};
 
 // The exact transform (exl3_had_r_128 and the GEMV's pre-rotation: the same values as the GEMV's
-// in-kernel transforms), T = double butterflies; the float32 transform is had_mfma_kernel below.
+// in-kernel transforms), T = double butterflies; the float32 transform is had_mfma_kernel
+// (exl3_had.hip).
 // in_up (may be null): the input rows are fp16(fp16(silu(in)) * in_up) (a gated MLP's activation)
 // Every group's output of a block comes from one read of the input block (a fused module's groups
 // differ only in their pre-scale).
@@ -140,51 +136,14 @@ __global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ i
     }
 }
 
-// The float32 transform on the matrix cores (had128_mfma16): y = fp16(fp16(x * pre) H * r * scale)
-// [* post], one wave per 16 rows x one 128-block, all groups from one read of x (VALU ~3.5 ops per
-// element against ~15 for float32 butterflies, which left the pass issue-bound).  Each wave reads
-// its whole tile before it writes: in place is safe.
-__global__ void __launch_bounds__(256) had_mfma_kernel(const uint16_t* __restrict__ in, int64_t ld_in, HadGroups hg,
-                                                       int groups, int64_t ld_out, int rows, int cols,
-                                                       const uint16_t* __restrict__ post, float scale)
-{
-    const int nblk = cols / 128;
-    const int64_t wid = ((int64_t) blockIdx.x * 256 + threadIdx.x) >> 6;
-    const int64_t row_groups = ((int64_t) rows + 15) / 16;
-    if (wid >= row_groups * nblk) return;                     // uniform per wave (no barrier below)
-    const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
-    const int64_t rg = wid / nblk;
-    const int col0 = (int) (wid - rg * nblk) * 128;
-    const int64_t row = rg * 16 + j;
-    const bool live = row < rows;
-    u32x4 xb[4], pv[4];
-#pragma unroll
-    for (int s_ = 0; s_ < 4; ++s_) {
-        xb[s_] = live ? *reinterpret_cast<gc_u32x4*>(as_global(in) + row * ld_in + col0 + 32 * s_ + 8 * g)
-                      : u32x4{0u, 0u, 0u, 0u};
-        pv[s_] = post ? *reinterpret_cast<gc_u32x4*>(as_global(post) + col0 + 32 * s_ + 8 * g) : u32x4{0u, 0u, 0u, 0u};
-    }
-    const HadMfmaA A = had_mfma_a();
-    for (int gi = 0; gi < groups; ++gi) {
-        // constant indices into the argument struct (a runtime index would copy it to scratch)
-        const uint16_t* pre = gi == 0 ? hg.pre[0] : gi == 1 ? hg.pre[1] : gi == 2 ? hg.pre[2] : hg.pre[3];
-        uint16_t* out = gi == 0 ? hg.out[0] : gi == 1 ? hg.out[1] : gi == 2 ? hg.out[2] : hg.out[3];
-        u32x4 xs[4];
-#pragma unroll
-        for (int s_ = 0; s_ < 4; ++s_) {
-            f16x8 x = __builtin_bit_cast(f16x8, xb[s_]);
-            if (pre) x = x * __builtin_bit_cast(f16x8, *reinterpret_cast<gc_u32x4*>(as_global(pre) + col0 + 32 * s_ + 8 * g));
-            xs[s_] = __builtin_bit_cast(u32x4, x);
-        }
-        had128_mfma16(A, xs, scale, post != nullptr, pv, [&](int p, u32x4 v) __attribute__((always_inline)) {
-            if (live) *reinterpret_cast<g_u32x4*>(as_global(out) + row * ld_out + col0 + 32 * p + 8 * g) = v;
-        });
-    }
-}
+// the float transform's launch (exl3_had.hip)
+void launch_had_mfma(const uint16_t* in, int64_t ld_in, const HadGroups& hg, int groups, int64_t ld_out, int rows,
+                     int cols, const uint16_t* post, float scale, bool has_pre, hipStream_t s);
 
-// had_r_128 of one input into `groups` outputs, group i scaled by pre[i] (may be null): one launch
-// (the prefill's input transforms of a fused module); exact: float64 butterflies, else float32
-// sums on the matrix cores (the prefill's input transforms and epilogue values)
+// had_r_128 of one input into `groups` outputs, group i scaled by pre[i] (may be null; the float32
+// form takes a pre for every group or for none): one launch (the prefill's input transforms of a
+// fused module); exact: float64 butterflies, else float32 sums on the matrix cores (the prefill's
+// input transforms and epilogue values)
 int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, int rows, int cols, const void* const* pre,
                int groups, const void* post, float scale, void* stream, bool exact, const void* in_up)
 {
@@ -205,9 +164,13 @@ int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, 
     if (!exact && in_up) return EXL3_EINVAL;                  // the gated input exists in the exact form only
     if (!exact) {
         const int64_t waves = ((int64_t) rows + 15) / 16 * (cols / 128);
-        hipLaunchKernelGGL(had_mfma_kernel, dim3((unsigned) ((waves + 3) / 4)), dim3(256), 0, (hipStream_t) stream,
-                           (const uint16_t*) in, ld_in, hg, groups, ld_out, rows, cols, (const uint16_t*) post,
-                           (float) (R_SCALE * (double) scale));
+        if (waves >= (1ll << 31)) return EXL3_EINVAL;
+        const float sc = (float) (R_SCALE * (double) scale);
+        int n_pre = 0;
+        for (int i = 0; i < groups; ++i) n_pre += hg.pre[i] != nullptr;
+        if (n_pre != 0 && n_pre != groups) return EXL3_EINVAL;      // pre for every group or for none
+        launch_had_mfma((const uint16_t*) in, ld_in, hg, groups, ld_out, rows, cols, (const uint16_t*) post, sc,
+                        n_pre != 0, (hipStream_t) stream);
     } else {
         hipLaunchKernelGGL(had_kernel<double>, grid, dim3(256), 0, (hipStream_t) stream, (const uint16_t*) in,
                            (const uint16_t*) in_up, ld_in, hg, groups, ld_out, rows, cols, (const uint16_t*) post,

@@ -6,7 +6,7 @@ Restated from the kernel's formulas (lane l: row / column index l & 15, k-chunk 
 element e of the lane's 8-element fragment):
   * output column of tile t, A-row i:  c(t, i) = 32 (t >> 1) + 8 (i >> 2) + 4 (t & 1) + (i & 3)
   * input index of step s:            k = 32 s + 8 g + e
-  * A fragment sign:                  (-1)^popcount((t >> 1) & s)  [taken on B as its negated copy]
+  * A fragment sign:                  (-1)^popcount((t >> 1) & s)  [selects the negated A fragment]
                                       * (-1)^(popcount((j & 3) & (e & 3)) + (t & 1)(e >> 2)
                                                + popcount((j >> 2) & g))
 and the result layout D[4 g + e][j] (lane l holds 4 consecutive rows of column j = l & 15).
