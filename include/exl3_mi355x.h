@@ -245,6 +245,19 @@ int exl3_gemm_trellis_grouped(const void* x, int64_t ldx, const void* const* tre
                               int m, int k, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
                               void* stream);
 
+/* Gated MLP output for any m (the prefill form of exl3_gemv_silu_in): the exl3_gemm_trellis_grouped
+ * prefill of one group over the input x = fp16(fp16(silu(gate)) * up) (the exl3_silu_mul
+ * roundings), formed by the input transform as it loads the rows; gate and up rows ldx apart (a
+ * gated module's grouped [m, 2k] output: gate = y, up = y + k, ldx = 2k).  xh: [m, k] fp16
+ * scratch (the rotated activation); workspace / ws_bytes: exl3_gemm_trellis_workspace_size(m, k,
+ * &n, 1).  Bitwise equal to exl3_silu_mul followed by exl3_gemm_trellis_grouped.  No counterpart in
+ * the reference: its down projection reads the SiluAndMul output (reference
+ * docs/EFFICIENCY_INVESTIGATION.md:36-66 proposes fusing the activation).  Callers: exl3rocm's
+ * silu_mul_linear op for m > 32.  Removes the activation launch and its [m, k] write and read. */
+int exl3_gemm_trellis_silu_in(const void* gate, const void* up, int64_t ldx, const void* trellis, void* y, int64_t ldy,
+                              const void* suh, void* xh, const void* svh, int m, int k, int n, int K, int mcg, int mul1,
+                              void* workspace, size_t ws_bytes, void* stream);
+
 /* Workspace bytes exl3_gemm_trellis_grouped uses to balance the launch's last, partial wave of
  * output tiles (those tiles are split along K; fp32 partials and completion counters).  0 when the
  * shape needs none.  Zero before the first call; every call leaves its counters zero.  With a

@@ -331,6 +331,35 @@ __device__ __forceinline__ void had128_x2_f32(float a, float b, uint32_t post, d
 // the Hadamard scale of every reference call site, per element type
 template <class T> constexpr T r_scale() { return (T) R_SCALE; }
 
+// SiLU-and-mul of 8 fp16 pairs with the activation kernels' roundings: silu in fp32
+// (g / (1 + exp(-g))) rounded to fp16, then the fp16 product (exact in fp32) rounded once.
+__device__ __forceinline__ u32x4 silu_mul_x8(u32x4 g, u32x4 u)
+{
+    const f16x8 gh = __builtin_bit_cast(f16x8, g), uh = __builtin_bit_cast(f16x8, u);
+    f16x8 r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float gf = (float) gh[i];
+        const f16 act = (f16) (gf / (1.0f + expf(-gf)));
+        r[i] = (f16) ((float) act * (float) uh[i]);
+    }
+    return __builtin_bit_cast(u32x4, r);
+}
+
+// the same for two elements (one 32-bit register)
+__device__ __forceinline__ uint32_t silu_mul_x2(uint32_t g, uint32_t u)
+{
+    const f16x2 gh = __builtin_bit_cast(f16x2, g), uh = __builtin_bit_cast(f16x2, u);
+    f16x2 r;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const float gf = (float) gh[i];
+        const f16 act = (f16) (gf / (1.0f + expf(-gf)));
+        r[i] = (f16) ((float) act * (float) uh[i]);
+    }
+    return __builtin_bit_cast(uint32_t, r);
+}
+
 // the (pre, out) pair of each group of one launch (a fused module's input transforms read one x)
 struct HadGroups {
     const uint16_t* pre[EXL3_MAX_GROUPS];

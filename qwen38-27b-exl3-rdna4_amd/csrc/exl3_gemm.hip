@@ -793,10 +793,12 @@ int launch_trellis_gemm_cb(int cb, const uint16_t* const* xh, int64_t ldx, const
     return launch_trellis_gemm<BITS, 2>(xh, ldx, tr, y, ldy, svh, widths, groups, M, K, ws, wsb, s);
 }
 
-// x -> per-group xh (input Hadamards), then one GEMM launch over every group's tiles
+// x -> per-group xh (input Hadamards), then one GEMM launch over every group's tiles; x_up (may be
+// null): the input rows are fp16(fp16(silu(x)) * x_up), formed by the transform as it loads them
 int gemm_trellis_common(const void* x, int64_t ldx, const void* const* trellis, uint16_t* const* y, int64_t ldy,
                         const void* const* suh, uint16_t* xh, const void* const* svh, const int* widths, int groups,
-                        int m, int k, int K, int mcg, int mul1, void* ws, size_t wsb, hipStream_t s)
+                        int m, int k, int K, int mcg, int mul1, void* ws, size_t wsb, hipStream_t s,
+                        const void* x_up = nullptr)
 {
     const uint16_t* xhs[EXL3_MAX_GROUPS];
     const uint16_t* svs[EXL3_MAX_GROUPS];
@@ -808,7 +810,7 @@ int gemm_trellis_common(const void* x, int64_t ldx, const void* const* trellis, 
         svs[i] = (const uint16_t*) svh[i];
     }
     // the groups' input transforms (one x, each group's suh) in one launch
-    const int rc = launch_had(x, ldx, xo, k, m, k, suh, groups, nullptr, 1.0f, s, false, nullptr);
+    const int rc = launch_had(x, ldx, xo, k, m, k, suh, groups, nullptr, 1.0f, s, false, x_up);
     if (rc) return rc;
     const int cb = codebook_of(mcg, mul1);
     switch (K) {
@@ -882,6 +884,21 @@ int exl3_gemm_trellis_grouped(const void* x, int64_t ldx, const void* const* tre
     if (m == 0) return EXL3_OK;
     return gemm_trellis_common(x, ldx, trellis, ys, ldy, suh, (uint16_t*) xh, svh, widths, groups, m, k, K, mcg, mul1,
                                workspace, ws_bytes, (hipStream_t) stream);
+}
+
+int exl3_gemm_trellis_silu_in(const void* gate, const void* up, int64_t ldx, const void* trellis, void* y, int64_t ldy,
+                              const void* suh, void* xh, const void* svh, int m, int k, int n, int K, int mcg, int mul1,
+                              void* workspace, size_t ws_bytes, void* stream)
+{
+    if (!gate || !up || !trellis || !y || !suh || !xh || !svh || m < 0 || K < 1 || K > 8 || k % 128 || n % 128 ||
+        k < 128 || n < 128 || ldx < k || ldy < n || ldx % 8 || ldy % 8 || (((uintptr_t) gate) & 15) ||
+        (((uintptr_t) up) & 15) || (((uintptr_t) xh) & 15) || (((uintptr_t) y) & 15) || (((uintptr_t) svh) & 15) ||
+        (((uintptr_t) trellis) & 15))
+        return EXL3_EINVAL;
+    if (m == 0) return EXL3_OK;
+    uint16_t* yp = (uint16_t*) y;
+    return gemm_trellis_common(gate, ldx, &trellis, &yp, ldy, &suh, (uint16_t*) xh, &svh, &n, 1, m, k, K, mcg, mul1,
+                               workspace, ws_bytes, (hipStream_t) stream, up);
 }
 
 int exl3_gemm(const void* x, int64_t ldx, const void* trellis, void* y, int64_t ldy, const void* suh, void* A_had,

@@ -137,8 +137,8 @@ __global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ i
 }
 
 // the float transform's launch (exl3_had.hip)
-void launch_had_mfma(const uint16_t* in, int64_t ld_in, const HadGroups& hg, int groups, int64_t ld_out, int rows,
-                     int cols, const uint16_t* post, float scale, bool has_pre, hipStream_t s);
+void launch_had_mfma(const uint16_t* in, const uint16_t* up, int64_t ld_in, const HadGroups& hg, int groups,
+                     int64_t ld_out, int rows, int cols, const uint16_t* post, float scale, bool has_pre, hipStream_t s);
 
 // had_r_128 of one input into `groups` outputs, group i scaled by pre[i] (may be null; the float32
 // form takes a pre for every group or for none): one launch (the prefill's input transforms of a
@@ -161,7 +161,6 @@ int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, 
     if (rows == 0) return EXL3_OK;
     const int64_t jobs = (int64_t) rows * (cols / 128);           // 8 lanes each
     const dim3 grid((unsigned) ((jobs + 31) / 32));
-    if (!exact && in_up) return EXL3_EINVAL;                  // the gated input exists in the exact form only
     if (!exact) {
         const int64_t waves = ((int64_t) rows + 15) / 16 * (cols / 128);
         if (waves >= (1ll << 31)) return EXL3_EINVAL;
@@ -169,8 +168,8 @@ int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, 
         int n_pre = 0;
         for (int i = 0; i < groups; ++i) n_pre += hg.pre[i] != nullptr;
         if (n_pre != 0 && n_pre != groups) return EXL3_EINVAL;      // pre for every group or for none
-        launch_had_mfma((const uint16_t*) in, ld_in, hg, groups, ld_out, rows, cols, (const uint16_t*) post, sc,
-                        n_pre != 0, (hipStream_t) stream);
+        launch_had_mfma((const uint16_t*) in, (const uint16_t*) in_up, ld_in, hg, groups, ld_out, rows, cols,
+                        (const uint16_t*) post, sc, n_pre != 0, (hipStream_t) stream);
     } else {
         hipLaunchKernelGGL(had_kernel<double>, grid, dim3(256), 0, (hipStream_t) stream, (const uint16_t*) in,
                            (const uint16_t*) in_up, ld_in, hg, groups, ld_out, rows, cols, (const uint16_t*) post,

@@ -117,35 +117,6 @@ __device__ __forceinline__ void wait_stores_complete()
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// SiLU-and-mul of 8 fp16 pairs with the activation kernels' roundings: silu in fp32
-// (g / (1 + exp(-g))) rounded to fp16, then the fp16 product (exact in fp32) rounded once.
-__device__ __forceinline__ u32x4 silu_mul_x8(u32x4 g, u32x4 u)
-{
-    const f16x8 gh = __builtin_bit_cast(f16x8, g), uh = __builtin_bit_cast(f16x8, u);
-    f16x8 r;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const float gf = (float) gh[i];
-        const f16 act = (f16) (gf / (1.0f + expf(-gf)));
-        r[i] = (f16) ((float) act * (float) uh[i]);
-    }
-    return __builtin_bit_cast(u32x4, r);
-}
-
-// the same for two elements (one 32-bit register)
-__device__ __forceinline__ uint32_t silu_mul_x2(uint32_t g, uint32_t u)
-{
-    const f16x2 gh = __builtin_bit_cast(f16x2, g), uh = __builtin_bit_cast(f16x2, u);
-    f16x2 r;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const float gf = (float) gh[i];
-        const f16 act = (f16) (gf / (1.0f + expf(-gf)));
-        r[i] = (f16) ((float) act * (float) uh[i]);
-    }
-    return __builtin_bit_cast(uint32_t, r);
-}
-
 // a wave-uniform 64-bit value as a scalar (readfirstlane of both halves)
 __device__ __forceinline__ int64_t uniform_i64(int64_t v)
 {

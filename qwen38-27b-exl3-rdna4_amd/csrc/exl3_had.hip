@@ -14,12 +14,14 @@ namespace {
 // has a pre-scale (else none has); POST: post is given.  The loads of x, post and the first group's
 // pre go out together, and each group's pre is requested while the group before it is transformed,
 // so a wave waits for one round trip before its first MFMA (loading each pre-scale piece where it
-// is used had put four dependent round trips per group ahead of the matrix work).  Each wave reads
-// its whole tile before it writes: in place is safe.
-template <bool PRE, bool POST>
-__global__ void __launch_bounds__(256) had_mfma_kernel(const uint16_t* __restrict__ in, int64_t ld_in, HadGroups hg,
-                                                       int groups, int64_t ld_out, int rows, int cols,
-                                                       const uint16_t* __restrict__ post, float scale)
+// is used had put four dependent round trips per group ahead of the matrix work).  UP: the input
+// rows are fp16(fp16(silu(in)) * up) (a gated MLP's activation, up's rows ld_in apart as in's),
+// formed as they load: the down projection's transform reads gate and up instead of an
+// activation pass's output.  Each wave reads its whole tile before it writes: in place is safe.
+template <bool PRE, bool POST, bool UP>
+__global__ void __launch_bounds__(256) had_mfma_kernel(const uint16_t* __restrict__ in, const uint16_t* __restrict__ up,
+                                                       int64_t ld_in, HadGroups hg, int groups, int64_t ld_out, int rows,
+                                                       int cols, const uint16_t* __restrict__ post, float scale)
 {
     // wave index in 32 bits (the host keeps waves < 2^31), divided by the block count on the scalar unit
     const uint32_t nblk = (uint32_t) cols / 128u;
@@ -35,6 +37,8 @@ __global__ void __launch_bounds__(256) had_mfma_kernel(const uint16_t* __restric
 #pragma unroll
     for (int s_ = 0; s_ < 4; ++s_) {
         xb[s_] = live ? *reinterpret_cast<gc_u32x4*>(as_global(in) + row * ld_in + col0 + 32 * s_) : u32x4{0u, 0u, 0u, 0u};
+        if constexpr (UP)
+            if (live) xb[s_] = silu_mul_x8(xb[s_], *reinterpret_cast<gc_u32x4*>(as_global(up) + row * ld_in + col0 + 32 * s_));
         if constexpr (POST) pv[s_] = *reinterpret_cast<gc_u32x4*>(as_global(post) + col0 + 32 * s_);
         if constexpr (PRE) pn[s_] = *reinterpret_cast<gc_u32x4*>(as_global(hg.pre[0]) + col0 + 32 * s_);
     }
@@ -70,13 +74,18 @@ __global__ void __launch_bounds__(256) had_mfma_kernel(const uint16_t* __restric
 }  // namespace
 
 // one launch of the float transform over `groups` outputs (launch_had, exl3_gemv.hip, has checked
-// the arguments): pre for every group (has_pre) or for none
-void launch_had_mfma(const uint16_t* in, int64_t ld_in, const HadGroups& hg, int groups, int64_t ld_out, int rows,
-                     int cols, const uint16_t* post, float scale, bool has_pre, hipStream_t s)
+// the arguments): pre for every group (has_pre) or for none; up (may be null): the input rows are
+// fp16(fp16(silu(in)) * up)
+void launch_had_mfma(const uint16_t* in, const uint16_t* up, int64_t ld_in, const HadGroups& hg, int groups,
+                     int64_t ld_out, int rows, int cols, const uint16_t* post, float scale, bool has_pre, hipStream_t s)
 {
     const int64_t waves = ((int64_t) rows + 15) / 16 * (cols / 128);
-    auto kern = has_pre ? (post ? had_mfma_kernel<true, true> : had_mfma_kernel<true, false>)
-                        : (post ? had_mfma_kernel<false, true> : had_mfma_kernel<false, false>);
-    hipLaunchKernelGGL(kern, dim3((unsigned) ((waves + 3) / 4)), dim3(256), 0, s, in, ld_in, hg, groups, ld_out, rows,
-                       cols, post, scale);
+    using K = void (*)(const uint16_t*, const uint16_t*, int64_t, HadGroups, int, int64_t, int, int, const uint16_t*, float);
+    static const K kernels[8] = {had_mfma_kernel<false, false, false>, had_mfma_kernel<false, false, true>,
+                                 had_mfma_kernel<false, true, false>,  had_mfma_kernel<false, true, true>,
+                                 had_mfma_kernel<true, false, false>,  had_mfma_kernel<true, false, true>,
+                                 had_mfma_kernel<true, true, false>,   had_mfma_kernel<true, true, true>};
+    const K kern = kernels[(has_pre ? 4 : 0) + (post ? 2 : 0) + (up ? 1 : 0)];
+    hipLaunchKernelGGL(kern, dim3((unsigned) ((waves + 3) / 4)), dim3(256), 0, s, in, up, ld_in, hg, groups, ld_out,
+                       rows, cols, post, scale);
 }

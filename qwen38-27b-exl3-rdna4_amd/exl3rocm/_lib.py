@@ -45,6 +45,7 @@ SIGNATURES = {
     "exl3_gemv_silu_mul": (_i, [_p, _i64, _pp, _p, _i64, _pp, _p, _pp, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "exl3_silu_mul": (_i, [_p, _p, _i64, _p, _i64, _i, _i, _p]),
     "exl3_gemv_silu_in": (_i, [_p, _p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
+    "exl3_gemm_trellis_silu_in": (_i, [_p, _p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "exl3_mgemm": (_i, [_p, _p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "exl3_hgemm_recon": (_i, [_p, _i64, _p, _i64, _p, _i64, _i, _i, _i, _p]),
     "exl3_gemm_trellis": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p]),

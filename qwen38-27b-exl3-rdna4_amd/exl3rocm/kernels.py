@@ -337,6 +337,31 @@ def exl3_gemv_silu_in(gate, up, B, C, suh, A_had, svh, K: int, mcg: bool, mul1: 
                                              ws.numel(), _stream(gate)), "exl3_gemv_silu_in")
 
 
+
+def exl3_gemm_trellis_silu_in(gate, up, B, C, suh, xh, svh, K: int, mcg: bool, mul1: bool) -> None:
+    """The prefill GEMM (any m) over the input fp16(fp16(silu(gate)) * up), formed by the input
+    transform as it loads the rows: gate and up are [m, k] views with equal row spacing (the two
+    halves of a gated module's grouped output).  xh: [m, k] fp16 scratch.  Bitwise equal to
+    silu_mul followed by exl3_gemm_trellis_grouped.  No counterpart in the reference extension."""
+    _cuda(gate, up, B, C, suh, svh, xh)
+    k = gate.shape[-1]
+    g2, u2 = gate.reshape(-1, k), up.reshape(-1, k)
+    m = g2.shape[0]
+    n = svh.shape[0]
+    _need(u2.shape == g2.shape, "silu_in: gate and up of one shape")
+    _need(all(t.dtype == torch.float16 and t.stride(-1) == 1 for t in (g2, u2)), "silu_in: fp16, unit stride")
+    _need(m <= 1 or g2.stride(0) == u2.stride(0), "silu_in: gate and up rows equally spaced")
+    _need(B.shape[-1] == 16 * K, "exl3_gemm_trellis_silu_in: trellis last dim must be 16*K")
+    _need(xh.numel() >= m * k and xh.dtype == torch.float16 and xh.is_contiguous(), "gemm silu_in: xh scratch [m, k] fp16")
+    ldx = g2.stride(0) if m > 1 else k
+    wa = (C_int * 1)(n)
+    ws = prefill_workspace(gate.device, int(L.lib().exl3_gemm_trellis_workspace_size(m, k, wa, 1)))
+    L.check(L.lib().exl3_gemm_trellis_silu_in(g2.data_ptr(), u2.data_ptr(), ldx, B.data_ptr(), C.data_ptr(), _ldy(C, n),
+                                              suh.data_ptr(), xh.data_ptr(), svh.data_ptr(), m, k, n, K,
+                                              *_cb_flags(mcg, mul1), ws.data_ptr() if ws is not None else None,
+                                              ws.numel() if ws is not None else 0, _stream(gate)),
+            "exl3_gemm_trellis_silu_in")
+
 def silu_mul(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor) -> None:
     """out = fp16(fp16(silu(gate)) * up) over rows of n columns (gate / up may be column slices of
     one [rows, 2n] tensor)."""

@@ -260,8 +260,10 @@ def exl3_silu_mul_linear(gu: torch.Tensor, trellis: torch.Tensor, suh: torch.Ten
     linear (the fusion is proposed in reference docs/EFFICIENCY_INVESTIGATION.md:36-66).
 
     At M <= EXL3_MR_MAX one GEMV launch forms act from gate and up as its input rows load; above
-    it (and on the approximate GEMV routes) the elementwise kernel writes act and linear runs on
-    it.  Every route equals silu_mul followed by linear, bitwise."""
+    it the prefill's input transform forms act as it loads the rows (one transform launch and one
+    GEMM launch, no act in memory); on the approximate GEMV routes and the recon prefill route the
+    elementwise kernel writes act and linear runs on it.  Every route equals silu_mul followed by
+    linear, bitwise."""
     k2 = gu.shape[-1]
     k = suh.shape[0]
     if k2 != 2 * k:
@@ -276,6 +278,9 @@ def exl3_silu_mul_linear(gu: torch.Tensor, trellis: torch.Tensor, suh: torch.Ten
         rc = E.exl3_gemv_silu_in(g2[:, :k], g2[:, k:], trellis, y, suh, None, svh, K, mcg, mul1)
         if rc != 0:
             raise RuntimeError(f"exl3rocm: GEMV declined shape m={M} k={k} n={n} K={K}")
+    elif M > MR_MAX and PREFILL_ROUTE != "recon":
+        xh = torch.empty((M, k), dtype=torch.float16, device=gu.device)
+        E.exl3_gemm_trellis_silu_in(g2[:, :k], g2[:, k:], trellis, y, suh, xh, svh, K, mcg, mul1)
     else:
         act = torch.empty((M, k), dtype=torch.float16, device=gu.device)
         E.silu_mul(g2[:, :k], g2[:, k:], act)

@@ -105,6 +105,13 @@ def test_invalid_arguments_return_before_any_launch():
                                None) == _lib.EINVAL
     assert L.exl3_mgemm(dummy, None, dummy, dummy, None, dummy, 2, 128, 128, 4, 0, 1, dummy, 1 << 20,
                         None) == _lib.EINVAL
+    # the prefill SiLU-input form: null up, unaligned gate, K out of range
+    assert L.exl3_gemm_trellis_silu_in(dummy, None, 256, dummy, dummy, 128, dummy, dummy, dummy, 64, 128, 128, 4, 0, 1,
+                                       None, 0, None) == _lib.EINVAL
+    assert L.exl3_gemm_trellis_silu_in(ctypes.c_void_p(0x1002), dummy, 256, dummy, dummy, 128, dummy, dummy, dummy, 64,
+                                       128, 128, 4, 0, 1, None, 0, None) == _lib.EINVAL
+    assert L.exl3_gemm_trellis_silu_in(dummy, dummy, 256, dummy, dummy, 128, dummy, dummy, dummy, 64, 128, 128, 9, 0, 1,
+                                       None, 0, None) == _lib.EINVAL
 
 
 def test_check_raises_on_errors():

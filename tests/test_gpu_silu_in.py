@@ -110,8 +110,9 @@ def test_silu_in_saturating_gate():
 
 @pytest.mark.parametrize("m", [1, 5, 40])
 def test_silu_mul_linear_op(m):
-    """The op: M <= 32 on the fused GEMV, M > 32 on silu_mul then the prefill; == the two-launch
-    form bitwise; rows of a [b, s, 2k] input keep their leading shape."""
+    """The op: M <= 32 on the fused GEMV, M > 32 on the prefill whose input transform forms the
+    activation; == the two-launch form bitwise; rows of a [b, s, 2k] input keep their leading
+    shape."""
     k, n, bits = 1024, 768, 4
     gu, tr, su, sv = down(k, n, bits, m, tag="silu-in-op")
     GU, T, SU, SV = to_dev(gu, tr.view(np.int16), su, sv)
@@ -148,3 +149,31 @@ def test_silu_in_graph_replays():
         assert same(y, eager)
         eager = fused(GU, T, SU, SV, k, bits, False, True)
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("m,k,n", [(300, 1024, 768), (2048, 17408, 5120)])
+def test_prefill_silu_in_matches_two_launch(m, k, n):
+    """exl3_gemm_trellis_silu_in (the prefill's input transform forms act = fp16(fp16(silu(g)) * u)
+    as it loads gate and up) == exl3_silu_mul, then the grouped prefill of act: output and rotated
+    input bitwise, with ragged rows (300: two row blocks) and at config 4's down shape (2048 x
+    17408 -> 5120: a split tail), activations spread x4; and the oracle bar on the first rows."""
+    bits = 4
+    gu, tr, su, sv = down(k, n, bits, m, tag="silu-in-prefill", spread=4.0)
+    GU, T, SU, SV = to_dev(gu, tr.view(np.int16), su, sv)
+    act = torch.empty(m, k, dtype=torch.float16, device=DEV)
+    E.silu_mul(GU[:, :k], GU[:, k:], act)
+    want = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    xh0 = torch.empty(m, k, dtype=torch.float16, device=DEV)
+    E.exl3_gemm_trellis_grouped(act, [T], want, [SU], xh0, [SV], bits, False, True)
+    y = torch.full((m, n), float("nan"), dtype=torch.float16, device=DEV)
+    xh = torch.full((m, k), float("nan"), dtype=torch.float16, device=DEV)
+    E.exl3_gemm_trellis_silu_in(GU[:, :k], GU[:, k:], T, y, SU, xh, SV, bits, False, True)
+    torch.cuda.synchronize()
+    assert same(xh, xh0)
+    assert same(y, want)
+    if m <= 300:
+        g = gu[:4, :k].astype(np.float64)
+        u = gu[:4, k:].astype(np.float64)
+        with np.errstate(over="ignore"):
+            a = O.to_f16(O.to_f16(g / (1.0 + np.exp(-g))) * u)
+        assert_close(y[:4].cpu().numpy(), cpu.linear(a.astype(np.float16), tr, bits, su, sv, 2), "prefill silu_in")
