@@ -358,6 +358,49 @@ def cpu_baseline(base, bits, budget_s=8.0):
             "side": side}
 
 
+
+def prefill_mlp(torch, sets, x5120, m=2048, reps=4, rounds=5):
+    """The MLP of config 1 at M = 2048 (the prefill routes), two ways, eager, mean duration per MLP
+    over the weight copies (median of `rounds` interleaved rounds):
+      unfused_us: linear_groups(gate, up), the elementwise SiLU-and-mul kernel, linear(down);
+      silu_in_us: linear_groups(gate, up), then silu_mul_linear (the down prefill's input
+                  transform forms the activation as it loads gate and up:
+                  exl3_gemm_trellis_silu_in), no activation in memory."""
+    from exl3rocm import kernels as E
+    ops = torch.ops.exl3rocm
+    n = INTER
+    x = x5120.expand(m, HIDDEN).contiguous()
+    act = torch.empty(m, n, dtype=torch.float16, device="cuda")
+
+    def gate_up(ls):
+        w = ls.w
+        return ops.linear_groups(x, [w["gate"][0], w["up"][0]], [w["gate"][1], w["up"][1]],
+                                 [w["gate"][2], w["up"][2]], [ls.bits, ls.bits], ls.mcg, ls.mul1)
+
+    def unfused(ls):
+        gu = gate_up(ls)
+        E.silu_mul(gu[:, :n], gu[:, n:], act)
+        ops.linear(act, *ls.w["down"], ls.bits, ls.mcg, ls.mul1)
+
+    def silu_in(ls):
+        ops.silu_mul_linear(gate_up(ls), *ls.w["down"], ls.bits, ls.mcg, ls.mul1)
+
+    forms = (("unfused_us", unfused), ("silu_in_us", silu_in))
+    for _, fn in forms:
+        fn(sets[0])
+    torch.cuda.synchronize()
+    times = {tag: [] for tag, _ in forms}
+    for _ in range(rounds):
+        for tag, fn in forms:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for r in range(reps):
+                fn(sets[r % len(sets)])
+            e1.record()
+            torch.cuda.synchronize()
+            times[tag].append(e0.elapsed_time(e1) * 1e3 / reps)
+    return {"m": m, **{tag: round(sorted(v)[len(v) // 2], 1) for tag, v in times.items()}}
+
 def prefill_chunk(torch, layers=64, m=2048, bits=4, iters=2):
     """Configuration 4: M = 2048 through a 64-layer stack of the 7 linears (independent weights per
     layer, generated on the device), fp16 activations."""
@@ -563,6 +606,8 @@ def main() -> int:
     extra["approx_m1"] = approx_m1(torch, sets, x5120, x17408)
     log("gated MLP (gate/up, SiLU-and-mul, down) three ways")
     extra["gated_mlp"] = gated_mlp(torch, sets, x5120, ms=(1, 2, 4, 8, 16))
+    log("gated MLP at M=2048 (prefill routes) two ways")
+    extra["gated_mlp_prefill"] = prefill_mlp(torch, sets, x5120)
     if not args.no_sweep:
         log("small-batch crossover")
         extra["config3_small_batch"] = small_batch(torch, sets)
