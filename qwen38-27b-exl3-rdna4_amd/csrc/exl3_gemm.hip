@@ -340,6 +340,10 @@ struct PcArgs {
     // leaves its fp32 partial tile in `part`; the last of a tile's pieces (completion counter)
     // adds them in piece order and applies the epilogue.
     int n_full, split;
+    // cut > 0 (split 2): a tile's pieces are K steps [0, cut) and [cut, all) (unequal), and the
+    // items hold every tile's first piece before any second piece (the long pieces go first; the
+    // short ones fill the CUs that finish early)
+    int cut;
     f32x4* part;                // [(tiles - n_full) * split][32][256] partial tiles
     uint32_t part_bytes;        // their size (the raw buffer's range)
     uint32_t* counters;         // [tiles - n_full], zero between calls (the last piece resets)
@@ -385,8 +389,14 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
         u = a.xcd_remap ? (b & 7) * (a.n_full / 8) + (b >> 3) : b;    // consecutive tiles share an XCD
     } else {
         const int bb = b - a.n_full;
-        u = a.n_full + bb / a.split;
-        q = bb - (bb / a.split) * a.split;
+        if (a.cut) {
+            const int tail = a.total - a.n_full;
+            q = bb >= tail;
+            u = a.n_full + bb - q * tail;
+        } else {
+            u = a.n_full + bb / a.split;
+            q = bb - (bb / a.split) * a.split;
+        }
     }
     // constant indices only into the kernel-argument struct (a runtime index copies it to scratch)
     int gi = 0;
@@ -400,8 +410,8 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
     const int M = a.M;
     // K steps [sb, sb + steps) of the tile (all of them unless this item is a piece)
     const int all_steps = a.K / KSTEP;
-    const int sb = piece ? q * all_steps / a.split : 0;
-    const int steps = piece ? (q + 1) * all_steps / a.split - sb : all_steps;
+    const int sb = !piece ? 0 : a.cut ? (q ? a.cut : 0) : q * all_steps / a.split;
+    const int steps = !piece ? all_steps : a.cut ? (q ? all_steps - a.cut : a.cut) : (q + 1) * all_steps / a.split - sb;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
     auto stage = [&](int s) __attribute__((always_inline)) { return lds + (s % PC::STAGES) * PC::BUF; };
     // partial tile of piece pq of this tile: consumer thread t's 32 accumulator quads, 16 B apart
@@ -710,7 +720,7 @@ constexpr size_t PC_COUNTER_BYTES = 4096;      // workspace head: completion cou
 constexpr size_t PC_PIECE_BYTES = (size_t) PC::MT * NT_COLS * 4;   // one fp32 partial tile
 
 struct PcPlan {
-    int tiles, n_full, split;
+    int tiles, n_full, split, cut;
     size_t ws_bytes;                           // 0: no split
 };
 
@@ -725,8 +735,15 @@ PcPlan pc_plan(int M, int K, const int* widths, int groups)
     // a launch of at most half a wave of tiles (small M: one row tile of few columns, e.g. the
     // 40 tiles of a 17408 -> 5120 layer) splits every tile, so that the pieces fill the CUs
     if (full == 0 && 2 * tail <= PC_CUS) p.split = std::min(PC_CUS / tail, (K / KSTEP) / 8);
-    // (more than half a wave and less than one, e.g. the 136 tiles of a 5120 -> 17408 layer at
-    // M <= 256, stays unsplit: 5 pieces measured 9-50 % slower from M = 33 on)
+    // more than half a wave and at most two thirds of one (e.g. the 136 tiles of a 5120 -> 17408
+    // layer at M <= 256): two unequal pieces per tile, 2/3 and 1/3 of the K steps.  The long pieces
+    // and some short ones start at once; the other short ones (2 tiles - CUs of them, at most the
+    // CUs - tiles that took a short one) follow on the CUs whose short piece ended, so the launch
+    // takes ~2/3 of the steps (5 equal pieces measured 9-50 % slower than unsplit from M = 33 on)
+    if (full == 0 && 2 * tail > PC_CUS && 3 * tail <= 2 * PC_CUS && K / KSTEP >= 16) {
+        p.split = 2;
+        p.cut = (2 * (K / KSTEP) + 2) / 3;
+    }
     if (p.split < 2) p.split = 1;
     p.n_full = p.split > 1 ? full * PC_CUS : p.tiles;
     p.ws_bytes = p.split > 1 ? PC_COUNTER_BYTES + (size_t) (p.tiles - p.n_full) * p.split * PC_PIECE_BYTES : 0;
@@ -757,6 +774,7 @@ int launch_trellis_gemm(const uint16_t* const* xh, int64_t ldx, const void* cons
     PcPlan pl = pc_plan(M, K, widths, groups);
     if (pl.split > 1 && (!ws || ws_bytes < pl.ws_bytes || pl.ws_bytes - PC_COUNTER_BYTES >= (1ull << 31))) {
         pl.split = 1;
+        pl.cut = 0;
         pl.n_full = pl.tiles;
     }
     PcArgs a{};
@@ -774,6 +792,7 @@ int launch_trellis_gemm(const uint16_t* const* xh, int64_t ldx, const void* cons
     a.total = tiles;
     a.n_full = pl.n_full;
     a.split = pl.split;
+    a.cut = pl.cut;
     a.xcd_remap = a.n_full % 8 == 0;
     if (pl.split > 1) {
         a.counters = (uint32_t*) ws;

@@ -484,6 +484,28 @@ def test_prefill_split_tail_parity_and_determinism():
     assert_close(y1[:, c_split:].cpu().numpy(), y0[:, c_split:].cpu().numpy(), "split vs unsplit")
 
 
+
+@pytest.mark.parametrize("m", [64, 200])
+def test_prefill_unequal_two_piece_split(m):
+    """136 output tiles (one row tile of a 5120 -> 17408-wide layer, 128 < tiles <= 2/3 of the CUs):
+    every tile in two unequal pieces along K (11 and 5 of 16 steps here), all long pieces dispatched
+    before the short ones.  Matches the oracle on a column slice crossing both piece kinds' tiles
+    and the unsplit launch to the bar, and repeat calls are bitwise equal."""
+    k, n, bits = 1024, 17408, 4
+    tr, su, sv = synth.layer("pf2piece", 0, k, n, bits)
+    x = synth.activations(synth.key_of("pf2piece", "x", m), m, k)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    y1 = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, False, True)
+    y2 = torch.ops.exl3rocm.linear(X, T, SU, SV, bits, False, True)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    y0 = torch.empty_like(y1)                                   # reference entry point: never split
+    E.exl3_gemm_trellis(X, T, y0, SU, torch.empty_like(X), SV, bits, False, True)
+    assert_close(y1.cpu().numpy(), y0.cpu().numpy(), "two pieces vs unsplit")
+    c0, c1 = 128 * 60, 128 * 68
+    sub = np.ascontiguousarray(tr[:, c0 // 16:c1 // 16, :])
+    ref = cpu.linear(x[:8], sub, bits, su, np.ascontiguousarray(sv[c0:c1]), 2)
+    assert_close(y1[:8, c0:c1].cpu().numpy(), ref, "two pieces vs oracle")
+
 def test_prefill_split_tail_graph_replays():
     """A prefill with a split tail (260 tiles: 256 whole, 4 split along K) captured in a graph after
     an eager warm-up on the capture stream (which sizes its workspace): every replay, with eager
