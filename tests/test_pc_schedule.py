@@ -109,13 +109,18 @@ STAGES = 3
 
 def pc_steps_of_plan(M, K, widths):
     """Step counts of every item of a pc_plan launch: whole tiles K / 64, pieces of the split tail
-    [q * all / split, (q + 1) * all / split) (exl3_gemm.hip pc_plan / gemm_pc_kernel)."""
+    [q * all / split, (q + 1) * all / split), or the two unequal pieces [0, cut), [cut, all) of a
+    launch of more than half and at most two thirds of a wave (exl3_gemm.hip pc_plan /
+    gemm_pc_kernel)."""
     tiles = sum(((M + 255) // 256) * (w // 128) for w in widths)
     full, tail = divmod(tiles, 256)
     all_steps = K // 64
     split = min(256 // tail, all_steps // 8) if full >= 1 and tail > 0 else 1
     if full == 0 and 2 * tail <= 256:
         split = min(256 // tail, all_steps // 8)
+    if full == 0 and 2 * tail > 256 and 3 * tail <= 512 and all_steps >= 16:
+        cut = (2 * all_steps + 2) // 3
+        return {all_steps, cut, all_steps - cut}
     if split < 2:
         split = 1
     out = {all_steps}
@@ -173,8 +178,28 @@ def test_schedule_model_flags_a_two_stage_ring():
 def test_plans_produce_only_modelled_step_counts():
     shapes = [(2048, 5120, [5120]), (2048, 17408, [5120]), (2048, 5120, [17408, 17408]),
               (2048, 5120, [5120, 1024, 1024]), (600, 256, [384]), (256, 1024, [128] * 4), (33, 128, [128]),
-              (64, 17408, [5120]), (40, 5120, [5120]), (96, 1024, [512, 384])]
+              (64, 17408, [5120]), (40, 5120, [5120]), (96, 1024, [512, 384]),
+              (33, 5120, [17408]), (64, 1024, [17408]), (768, 5120, [5120, 1024, 1024])]
     for M, K, widths in shapes:
         for st in pc_steps_of_plan(M, K, widths):
             assert st >= 2, (M, K, widths, st)
             test_stage_schedule(st)
+
+
+def test_unequal_pieces_plan_matches_the_library():
+    """The two-piece plan modelled above is the library's: its workspace (4 KB of counters plus
+    one fp32 partial tile per piece) for launches of 136 and 168 tiles, and none of it for 170 <
+    tiles < 256 (no split, no workspace) and equal pieces for at most half a wave."""
+    import ctypes
+    from exl3rocm import _lib
+    L = _lib.lib()
+
+    def ws(M, K, widths):
+        return L.exl3_gemm_trellis_workspace_size(M, K, (ctypes.c_int * len(widths))(*widths), len(widths))
+
+    piece = 256 * 128 * 4
+    assert ws(33, 5120, [17408]) == 4096 + 136 * 2 * piece
+    assert ws(768, 5120, [5120, 1024, 1024]) == 4096 + 168 * 2 * piece
+    assert pc_steps_of_plan(33, 5120, [17408]) == {80, 54, 26}
+    assert ws(33, 5120, [17408 + 128 * 60]) == 0                 # 196 tiles: unsplit, no workspace
+    assert ws(33, 5120, [128 * 100]) == 4096 + 100 * 2 * piece   # 100 tiles: 2 equal pieces (min(256 / 100, 10))
