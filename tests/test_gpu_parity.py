@@ -197,6 +197,20 @@ def test_had_r_128_bitexact():
                                   .view(np.uint16))
 
 
+
+def test_had_r_128_bitexact_full_fp16_range():
+    """The exact transform on blocks spanning the whole fp16 range (+-65504 beside 2^-24 and every
+    binade between): float64 sums of fp16 data are exact whatever the span (test_oracle pins the
+    arithmetic), so the kernel's butterflies equal the oracle's bit for bit here too."""
+    from test_oracle import _full_range_blocks
+    x = _full_range_blocks(np.random.default_rng(41), 48).reshape(16, 384)
+    X = to_dev(x)[0]
+    out = torch.empty_like(X)
+    E.had_r_128(X, out, None, None, 1.0)
+    want = O.to_f16(O.had128(x.astype(np.float64), O.R_SCALE)).astype(np.float16)
+    assert np.isfinite(want.astype(np.float32)).all()
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint16), want.view(np.uint16))
+
 # ---------------------------------------------------------------------------------- GEMV
 GEMV_CASES = [
     (256, 128, 3, 2), (512, 256, 3, 2), (1024, 512, 3, 2), (4096, 4096, 4, 1),

@@ -324,3 +324,34 @@ def test_int8_slice_sums_are_exact_in_fp32():
     assert int(acc) == worst
     k_sum = np.float32(1024.0) * np.float32(O.K_INV) + np.float32(O.K_BIAS)
     assert float(k_sum) == 1024.0 * O.K_INV + O.K_BIAS == -3.453125
+
+
+
+def _full_range_blocks(rng, rows):
+    """fp16 rows of 128 spanning the whole fp16 range: +-65504, the smallest subnormal 2^-24, and
+    the rest spread over every binade from 2^-24 to 2^10, random signs (so the scaled outputs stay
+    below 65504)."""
+    e = rng.integers(-24, 11, size=(rows, 128)).astype(np.float64)
+    m = 1.0 + rng.integers(0, 1024, size=(rows, 128)) / 1024.0
+    x = (np.where(rng.integers(0, 2, size=(rows, 128)) == 1, -1.0, 1.0) * m * np.exp2(e)).astype(np.float16)
+    x[:, 0], x[:, 1], x[:, 2] = np.float16(65504.0), np.float16(-65504.0), np.float16(2.0 ** -24)
+    x[:, 3] = -np.float16(2.0 ** -24)
+    return x
+
+
+def test_float64_block_sums_of_fp16_are_exact():
+    """The exactness the float64 Hadamards rest on: every fp16 value is an integer multiple of
+    2^-24 below 2^16 in magnitude, so any sum of 128 of them (every partial sum of any order) is an
+    integer of at most 47 bits in units of 2^-24, inside float64's 53-bit significand.  Checked on
+    blocks spanning the full fp16 range: the oracle's float64 butterflies (scale 1) equal the exact
+    integer transform in units of 2^-24 for every output."""
+    rng = np.random.default_rng(40)
+    x = _full_range_blocks(rng, 64)
+    units = (x.astype(np.float64) * 2.0 ** 24).astype(np.int64)          # exact: fp16 * 2^24 is an integer
+    assert np.array_equal(units.astype(np.float64) / 2.0 ** 24, x.astype(np.float64))
+    i = np.arange(128)
+    H = np.where(np.vectorize(lambda v: bin(v).count("1"))(i[:, None] & i[None, :]) & 1, -1, 1).astype(np.int64)
+    exact = units @ H                                                    # int64: |sum| < 128 * 2^40
+    got = O.had128(x.astype(np.float64), 1.0)
+    assert np.array_equal(got * 2.0 ** 24, exact.astype(np.float64))
+    assert np.abs(exact).max() < 2 ** 47
