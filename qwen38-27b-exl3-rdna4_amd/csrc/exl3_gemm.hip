@@ -714,7 +714,8 @@ int launch_gemm_pc(const PcArgs& a, int items, hipStream_t s)
 
 // Tile plan of one producer/consumer launch: whole tiles for every full wave over the CUs (one
 // workgroup per CU), the last, partial wave's tiles split along K into up to CUs / tail pieces of
-// at least 8 K steps, so the launch ends in balance.  A function of the shape only.
+// at least 8 K steps (or, below one wave, the two unequal pieces below: at least 5), so the launch
+// ends in balance.  A function of the shape only.
 constexpr int PC_CUS = 256;                    // MI355X compute units
 constexpr size_t PC_COUNTER_BYTES = 4096;      // workspace head: completion counters of split tiles
 constexpr size_t PC_PIECE_BYTES = (size_t) PC::MT * NT_COLS * 4;   // one fp32 partial tile
