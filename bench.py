@@ -490,14 +490,18 @@ def small_batch(torch, sets, ms=(1, 4, 8, 16, 32), gemm_ms=(4, 8, 16, 32, 33, 64
         for m in ms:
             x = xs[m]
             row[f"m{m}_us"] = graph_us(lambda ls, x=x: torch.ops.exl3rocm.linear(x, *ls.w[name], ls.bits, ls.mcg, ls.mul1))
-        gemm = {}
+        gemm, unsplit = {}, {}
         for m in gemm_ms:
             x = xs[m]
             y = torch.empty(m, n, dtype=torch.float16, device="cuda")
             xh = torch.empty(m, k, dtype=torch.float16, device="cuda")
             gemm[f"m{m}_us"] = graph_us(lambda ls, x=x, y=y, xh=xh: E.exl3_gemm_trellis_grouped(
                 x, [ls.w[name][0]], y, [ls.w[name][1]], xh, [ls.w[name][2]], ls.bits, ls.mcg, ls.mul1))
+            # the same GEMM without a workspace: its tiles unsplit (the plan's comparison)
+            unsplit[f"m{m}_us"] = graph_us(lambda ls, x=x, y=y, xh=xh: E.exl3_gemm_trellis(
+                x, ls.w[name][0], y, ls.w[name][1], xh, ls.w[name][2], ls.bits, ls.mcg, ls.mul1))
         row["prefill_gemm"] = gemm
+        row["prefill_gemm_unsplit"] = unsplit
         cross = [m for m in ms if m in gemm_ms and gemm[f"m{m}_us"] < row[f"m{m}_us"]]
         row["gemm_faster_from_m"] = min(cross) if cross else "none below 33"
         res[name] = row
@@ -551,6 +555,9 @@ def main() -> int:
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true", help="only the dispatches the PMC traffic passes read")
+    ap.add_argument("--config3-only", action="store_true",
+                    help="only the configuration-3 section (the GEMV at small M, the prefill GEMM split and "
+                         "unsplit at M = 4-256; what its kernel-trace profile reads); prints its dict")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the configuration-4 prefill chunk (what the prefill PMC passes read); prints its dict")
     args = ap.parse_args()
@@ -570,6 +577,10 @@ def main() -> int:
         return traffic_probe(torch, bits, args.copies)
     if args.prefill_only:
         print(json.dumps(prefill_chunk(torch)), flush=True)
+        return 0
+    if args.config3_only:
+        _, sets = build_layers(torch, bits, args.copies)
+        print(json.dumps(small_batch(torch, sets)), flush=True)
         return 0
     log("building layer set (4 bpw, mul1) x %d copies" % args.copies)
     base, sets = build_layers(torch, bits, args.copies)
