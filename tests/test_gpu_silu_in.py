@@ -177,3 +177,32 @@ def test_prefill_silu_in_matches_two_launch(m, k, n):
         with np.errstate(over="ignore"):
             a = O.to_f16(O.to_f16(g / (1.0 + np.exp(-g))) * u)
         assert_close(y[:4].cpu().numpy(), cpu.linear(a.astype(np.float16), tr, bits, su, sv, 2), "prefill silu_in")
+
+
+def test_prefill_silu_in_graph_replays():
+    """silu_mul_linear at M = 64 (the prefill route: the input transform forms the activation, the
+    tiles split along K) captured in a graph after an eager warm-up on the capture stream (which
+    sizes its workspace): every replay, with eager work and synchronisations between them, equals
+    the eager result bitwise (the last piece of each split tile resets its counter; no memset node)."""
+    m, k, n, bits = 64, 17408, 5120, 4
+    gu, tr, su, sv = down(k, n, bits, m, tag="silu-in-prefill-graph")
+    GU, T, SU, SV = to_dev(gu, tr.view(np.int16), su, sv)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        eager = torch.ops.exl3rocm.silu_mul_linear(GU, T, SU, SV, bits, False, True)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        y = torch.ops.exl3rocm.silu_mul_linear(GU, T, SU, SV, bits, False, True)
+    for _ in range(3):
+        y.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert same(y, eager)
+        with torch.cuda.stream(s):
+            again = torch.ops.exl3rocm.silu_mul_linear(GU, T, SU, SV, bits, False, True)
+        torch.cuda.synchronize()
+        assert same(again, eager)
