@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define EXL3_ABI_VERSION 1
+#define EXL3_ABI_VERSION 2       /* 2: exl3_gemv_f32 and exl3_gemm_trellis_silu_in added */
 #define EXL3_MAX_GROUPS 4       /* groups per grouped launch (reference EXL3_GEMV_MRG_MAX) */
 #define EXL3_GEMV_MAX_ROWS 32   /* rows handled by the fused GEMV */
 #define EXL3_GEMV_COUNTER_BYTES 262144 /* workspace head reserved for completion counters (one per 128-byte line) */

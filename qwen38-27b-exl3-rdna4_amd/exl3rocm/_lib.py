@@ -15,7 +15,7 @@ OK, DECLINED, EINVAL, ELAUNCH, EWORKSPACE = 0, 1, -1, -2, -3
 MAX_GROUPS = 4
 GEMV_MAX_ROWS = 32
 NOALLOC_SCRATCH_BYTES = 17039360
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _p, _i, _i64, _sz, _f = C.c_void_p, C.c_int, C.c_int64, C.c_size_t, C.c_float
 _pp = C.POINTER(C.c_void_p)
@@ -71,12 +71,14 @@ def lib():
         if not os.path.exists(LIB_PATH):
             raise Exl3Error(f"exl3rocm: HIP library not built ({LIB_PATH}); run build_ext.py / __graft_entry__.build()")
         L = C.CDLL(LIB_PATH)
+        # the version first: a library older than these bindings lacks some of their symbols
+        L.exl3_abi_version.restype, L.exl3_abi_version.argtypes = C.c_int, []
+        if L.exl3_abi_version() != ABI_VERSION:
+            raise Exl3Error(f"exl3rocm: ABI version {L.exl3_abi_version()} != {ABI_VERSION} (rebuild the library)")
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(L, name)
             fn.restype = res
             fn.argtypes = args
-        if L.exl3_abi_version() != ABI_VERSION:
-            raise Exl3Error(f"exl3rocm: ABI version {L.exl3_abi_version()} != {ABI_VERSION}")
         _lib = L
     return _lib
 
