@@ -36,7 +36,8 @@
 extern "C" {
 #endif
 
-#define EXL3_ABI_VERSION 2       /* 2: exl3_gemv_f32 and exl3_gemm_trellis_silu_in added */
+#define EXL3_ABI_VERSION 3       /* 2: exl3_gemv_f32, exl3_gemm_trellis_silu_in; 3: exl3_gemv_silu_prerot_rows,
+                                    exl3_gemm_trellis_workspace_bound */
 #define EXL3_MAX_GROUPS 4       /* groups per grouped launch (reference EXL3_GEMV_MRG_MAX) */
 #define EXL3_GEMV_MAX_ROWS 32   /* rows handled by the fused GEMV */
 #define EXL3_GEMV_COUNTER_BYTES 262144 /* workspace head reserved for completion counters (one per 128-byte line) */
@@ -173,6 +174,12 @@ size_t exl3_gemv_workspace_size_widths(int m, int k, const int* widths, int grou
  * counterpart.  Callers: exl3rocm's kernel wrappers. */
 int exl3_gemv_prerot_rows(void);
 
+/* Rows from which exl3_gemv_silu_in forms and rotates its SiLU input once, by a separate pass into
+ * A_had, instead of in every workgroup (EXL3_GEMV_SILU_PREROT_M, default 4); below it A_had is not
+ * read.  No reference counterpart.  Callers: exl3rocm's kernel wrappers, which pass no scratch
+ * below it. */
+int exl3_gemv_silu_prerot_rows(void);
+
 /* Self-check of the GEMV's stream-K unit split (host only, no GPU): the kernels' 32-bit
  * multiply-high division forms of lo(w) and owner(u) against 64-bit arithmetic and brute force for
  * U units over G workgroups (h of them weighted wa, the rest wb), plus the divider at its range
@@ -264,6 +271,13 @@ int exl3_gemm_trellis_silu_in(const void* gate, const void* up, int64_t ldx, con
  * smaller or NULL workspace the tail is not split: the same results to the tolerance, less
  * balance.  No reference counterpart (the reference prefill has no split). */
 size_t exl3_gemm_trellis_workspace_size(int m, int k, const int* widths, int groups);
+
+/* The largest workspace exl3_gemm_trellis_workspace_size returns for any shape (a plan splits at
+ * most two thirds of one wave of tiles into two pieces, or fewer tiles into at most one wave of
+ * pieces): one workspace of this size serves every prefill call, so a caller that reserves it on a
+ * stream at load time never needs another before graph capture there.  No reference counterpart.
+ * Callers: exl3rocm's prefill workspace. */
+size_t exl3_gemm_trellis_workspace_bound(void);
 
 /* Dispatcher by row count: m <= 32 -> fused GEMV, else the prefill GEMM.  Returns the route
  * tag (1 = GEMV, 2 = prefill GEMM) or a negative error.

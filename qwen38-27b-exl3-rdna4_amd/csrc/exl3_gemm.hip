@@ -754,7 +754,8 @@ PcPlan pc_plan(int M, int K, const int* widths, int groups)
 // One GEMM launch over `groups` groups sharing M and K: group i reads xh[i] and writes widths[i]
 // columns at y[i] (rows ldy apart).  Operands too large for 32-bit raw-buffer offsets take the
 // 128 x 128 kernel, one launch per group.  Without a workspace of the plan's size the tail is not
-// split (same results, less balance).
+// split: less balance, and the tail tiles' fp32 sums run in another order (whole K instead of piece
+// partials added in piece order), so their outputs can differ from a split launch's in the last place.
 template <int BITS, int CB>
 int launch_trellis_gemm(const uint16_t* const* xh, int64_t ldx, const void* const* trellis, uint16_t* const* y,
                         int64_t ldy, const uint16_t* const* svh, const int* widths, int groups, int M, int K,
@@ -881,6 +882,13 @@ size_t exl3_gemm_trellis_workspace_size(int m, int k, const int* widths, int gro
     for (int i = 0; i < groups; ++i)
         if (widths[i] < 128 || widths[i] % 128) return 0;
     return pc_plan(m, k, widths, groups).ws_bytes;
+}
+
+size_t exl3_gemm_trellis_workspace_bound(void)
+{
+    // pieces of one plan: full >= 1 or 2 tail <= CUs: tail * min(CUs / tail, .) <= CUs; the
+    // two-piece form: 2 tail with 3 tail <= 2 CUs
+    return PC_COUNTER_BYTES + (size_t) std::max(PC_CUS, 2 * (2 * PC_CUS / 3)) * PC_PIECE_BYTES;
 }
 
 int exl3_gemm_trellis_grouped(const void* x, int64_t ldx, const void* const* trellis, void* y, int64_t ldy,

@@ -478,6 +478,8 @@ size_t exl3_gemv_workspace_size_widths(int m, int k, const int* widths, int grou
 
 int exl3_gemv_prerot_rows(void) { return prerot_rows(); }
 
+int exl3_gemv_silu_prerot_rows(void) { return silu_prerot_rows(); }
+
 int exl3_gemv_split_check(int U, int G, int h, int wa, int wb)
 {
     if (U < 1 || G < 1 || h < 0 || h > G || wa < 1 || wb < 1) return -1;

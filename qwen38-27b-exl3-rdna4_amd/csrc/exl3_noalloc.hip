@@ -44,7 +44,13 @@ void* scratch_of_current_device(hipStream_t stream)
     std::lock_guard<std::mutex> lock(g_mu);
     if (g_scratch[dev]) return g_scratch[dev];
     void* ptr = nullptr;
-    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    // The first call may come while `stream` captures a graph in the global mode, which refuses
+    // runtime calls outside the capture: this thread relaxes it for the lookup (no stream work),
+    // then restores it.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) return nullptr;
+    const hipError_t found = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess || found != hipSuccess || !ptr) return nullptr;
     // a fill kernel rather than hipMemsetAsync: the first call may be under graph capture
     constexpr int words = EXL3_GEMV_COUNTER_BYTES / 4;
     hipLaunchKernelGGL(clear_words_kernel, dim3(words / 256 / 16), dim3(256), 0, stream, (uint32_t*) ptr, words);

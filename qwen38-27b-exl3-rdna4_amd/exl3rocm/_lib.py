@@ -15,7 +15,7 @@ OK, DECLINED, EINVAL, ELAUNCH, EWORKSPACE = 0, 1, -1, -2, -3
 MAX_GROUPS = 4
 GEMV_MAX_ROWS = 32
 NOALLOC_SCRATCH_BYTES = 17039360
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _p, _i, _i64, _sz, _f = C.c_void_p, C.c_int, C.c_int64, C.c_size_t, C.c_float
 _pp = C.POINTER(C.c_void_p)
@@ -42,6 +42,7 @@ SIGNATURES = {
     "exl3_gemv_workspace_size_widths": (_sz, [_i, _i, _ip, _i]),
     "exl3_gemv_split_check": (_i, [_i, _i, _i, _i, _i]),
     "exl3_gemv_prerot_rows": (_i, []),
+    "exl3_gemv_silu_prerot_rows": (_i, []),
     "exl3_gemv_silu_mul": (_i, [_p, _i64, _pp, _p, _i64, _pp, _p, _pp, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "exl3_silu_mul": (_i, [_p, _p, _i64, _p, _i64, _i, _i, _p]),
     "exl3_gemv_silu_in": (_i, [_p, _p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
@@ -52,6 +53,7 @@ SIGNATURES = {
     "exl3_gemm_trellis_grouped": (_i, [_p, _i64, _pp, _p, _i64, _pp, _p, _pp, _ip, _i, _i, _i, _i, _i, _i, _p, _sz,
                                        _p]),
     "exl3_gemm_trellis_workspace_size": (_sz, [_i, _i, _ip, _i]),
+    "exl3_gemm_trellis_workspace_bound": (_sz, []),
     "exl3_gemm": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "exl3_gemv_mr_approx": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _p, _i, _i, _i, _i, _i, _p, _sz, _p]),
     "exl3_gemv_mr_noalloc": (_i, [_p, _i64, _p, _p, _i64, _p, _p, _i, _i, _i, _i, _i, _i, _p]),

@@ -69,11 +69,24 @@ def workspace(device: torch.device, nbytes: int, stream: Optional[int] = None, r
 
 
 _pf_workspaces: dict = {}
+_pf_bound = None
+
+
+def prefill_workspace_bound() -> int:
+    """Bytes of a prefill split workspace that serves every shape (the library's bound, ~43 MB)."""
+    global _pf_bound
+    if _pf_bound is None:
+        _pf_bound = int(L.lib().exl3_gemm_trellis_workspace_bound())
+    return _pf_bound
 
 
 def prefill_workspace(device: torch.device, nbytes: int, stream: Optional[int] = None) -> Optional[torch.Tensor]:
-    """Grow-only zeroed workspace of the prefill GEMM's split tail for the current (or given) stream.
-    During graph capture a missing or short one is not allocated: the launch then runs unsplit."""
+    """Zeroed workspace of the prefill GEMM's split tail for the current (or given) stream.  A
+    stream's first call outside graph capture allocates the bound every shape fits in
+    (exl3_gemm_trellis_workspace_bound), so a later capture on that stream splits exactly as
+    eager calls do.  A stream that captures before any eager prefill call has none: its launches
+    run unsplit, and the tail tiles' outputs can differ from the eager split's in the last place
+    (another fp32 summation order)."""
     if nbytes <= 0:
         return None
     device = torch.device(device)
@@ -84,9 +97,14 @@ def prefill_workspace(device: torch.device, nbytes: int, stream: Optional[int] =
     if buf is None or buf.numel() < nbytes:
         if torch.cuda.is_current_stream_capturing():
             return buf
-        buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        buf = torch.zeros(max(nbytes, prefill_workspace_bound()), dtype=torch.uint8, device=device)
         _pf_workspaces[key] = buf
     return buf
+
+
+def reserve_prefill_workspace(device: torch.device, stream: Optional[int] = None) -> None:
+    """Allocate the current (or given) stream's prefill workspace now (load time)."""
+    prefill_workspace(device, prefill_workspace_bound(), stream)
 
 
 def gemv_workspace_bytes(m: int, k: int, n: int, K: int, groups: int = 1) -> int:
@@ -186,14 +204,14 @@ def exl3_gemv(A, B, C, suh, A_had, svh, mcg: bool, mul1: bool) -> int:
 _prerot = None
 
 
-def _rot_scratch(A_had, device, groups: int, m: int, k: int, any_rows: bool = False):
+def _rot_scratch(A_had, device, groups: int, m: int, k: int, silu: bool = False):
     """The A_had scratch for the multi-row GEMV (groups * m * k fp16): the caller's when it is large
     enough, else a fresh one; none below the library's pre-rotation row count (the kernel rotates
-    in LDS there) unless any_rows (the SiLU-input form, whose own row count the library applies)."""
+    in LDS there: exl3_gemv_prerot_rows, or exl3_gemv_silu_prerot_rows for the SiLU-input form)."""
     global _prerot
     if _prerot is None:
-        _prerot = int(L.lib().exl3_gemv_prerot_rows())
-    if m <= 1 or (m < _prerot and not any_rows):
+        _prerot = (int(L.lib().exl3_gemv_prerot_rows()), int(L.lib().exl3_gemv_silu_prerot_rows()))
+    if m <= 1 or m < _prerot[1 if silu else 0]:
         return None
     if A_had is not None and A_had.dtype == torch.float16 and A_had.is_contiguous() and A_had.numel() >= groups * m * k:
         return A_had
@@ -330,7 +348,7 @@ def exl3_gemv_silu_in(gate, up, B, C, suh, A_had, svh, K: int, mcg: bool, mul1: 
     _need(B.shape[-1] == 16 * K, "exl3_gemv_silu_in: trellis last dim must be 16*K")
     ld_in = g2.stride(0) if m > 1 else k
     ws = workspace(gate.device, gemv_workspace_bytes(m, k, n, K))
-    xr = _rot_scratch(A_had, gate.device, 1, m, k, any_rows=True)
+    xr = _rot_scratch(A_had, gate.device, 1, m, k, silu=True)
     return L.check(L.lib().exl3_gemv_silu_in(g2.data_ptr(), u2.data_ptr(), ld_in, B.data_ptr(), C.data_ptr(),
                                              _ldy(C, n), suh.data_ptr(), xr.data_ptr() if xr is not None else None,
                                              svh.data_ptr(), m, k, n, K, *_cb_flags(mcg, mul1), ws.data_ptr(),

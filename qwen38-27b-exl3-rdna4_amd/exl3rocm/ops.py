@@ -156,6 +156,8 @@ def exl3_linear_groups(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[t
     x2, k = _prep(x)
     M = x2.shape[0]
     ng = len(trellis)
+    if M == 0:                                        # every route: an empty batch launches nothing
+        return x2.new_empty((*x.shape[:-1], sum(widths)), dtype=torch.float16)
     if M <= MR_MAX and GEMV_APPROX and mul1:
         # the approximate route runs each group as its own launch
         y = torch.empty((M, sum(widths)), dtype=torch.float16, device=x.device)
@@ -169,8 +171,6 @@ def exl3_linear_groups(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[t
         E.exl3_mgemm(x2.view(1, 1, k), ptrs_trellis, y, ptrs_suh, None, ptrs_svh, K[0], mcg, mul1)
         return y.view(*x.shape[:-1], ng * widths[0])
     y = torch.empty((M, sum(widths)), dtype=torch.float16, device=x.device)
-    if M == 0:
-        return y.view(*x.shape[:-1], 0 if not widths else sum(widths))
     if M <= MR_MAX:
         # runs of consecutive groups with equal K share one launch, each group written straight into
         # its row-strided column slice: equal widths (gate/up, k/v) through the reference's grouped

@@ -137,3 +137,22 @@ def test_gemv_split_fast_division_matches_brute_force():
         assert L.exl3_gemv_split_check(*c) == 0, c
     assert L.exl3_gemv_split_check(0, 1, 0, 1, 1) == -1
     assert L.exl3_gemv_split_check(2 ** 22, 512, 256, 64, 64) == -1      # beyond the 32-bit domain
+
+
+def test_prefill_workspace_bound_covers_every_plan():
+    """exl3_gemm_trellis_workspace_bound >= the workspace of every plan, and some plan needs all of
+    it (170 tiles in two unequal pieces each): tile counts 1 .. 3 waves at one and two row tiles."""
+    L = _lib.lib()
+    bound = L.exl3_gemm_trellis_workspace_bound()
+    worst = 0
+    for m in (33, 300):
+        for k in (1024, 5120):
+            for nt in range(1, 3 * 256 + 1):
+                w = (ctypes.c_int * 1)(128 * nt)
+                worst = max(worst, L.exl3_gemm_trellis_workspace_size(m, k, w, 1))
+    assert 0 < worst == bound, (worst, bound)
+
+
+def test_silu_prerot_rows_query():
+    assert _lib.lib().exl3_gemv_silu_prerot_rows() == int(os.environ.get("EXL3_GEMV_SILU_PREROT_M", "4"))
+    assert _lib.lib().exl3_gemv_prerot_rows() == int(os.environ.get("EXL3_GEMV_PREROT_M", "8"))

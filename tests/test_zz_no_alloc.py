@@ -2,10 +2,14 @@
 
 GPU: it gives exl3_gemv_mr's output bitwise (the same kernels; the workspace is the library's
 per-GPU device array), on two calls in a row, the second with a smaller input, and under graph
-capture with no workspace reserved anywhere.  CPU: a shape whose workspace exceeds the array
-is rejected before any launch.
+capture with no workspace reserved anywhere, also when the first call of a fresh process is the
+captured one (the set-up's symbol lookup and counter-clearing kernel then land in the graph).
+CPU: a shape whose workspace exceeds the array is rejected before any launch.
 """
 import ctypes
+import os
+import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -86,3 +90,55 @@ def test_noalloc_graph_capture_replays():
         assert torch.equal(y.view(torch.int16), eager.view(torch.int16))
         E.exl3_gemv_mr_noalloc(X2, T2, y2, SU2, SV2, 2, False, True)     # other shape, same array
         torch.cuda.synchronize()
+
+
+# Run in a child process so that the library's first exl3_gemv_mr_noalloc call on the device is the
+# captured one, whatever ran before in the test process.
+CAPTURE_FIRST = r"""
+import sys
+sys.path[:0] = PATHS
+import numpy as np, torch
+from exl3rocm import kernels as E, synth
+dev = "cuda:0"
+tr, su, sv = synth.layer("noalloc", "first", 5120, 5120, 4)
+x = synth.activations(synth.key_of("noalloc", "first", "x"), 4, 5120)
+X, T, SU, SV = (torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in (x, tr.view(np.int16), su, sv))
+y = torch.full((4, 5120), float("nan"), dtype=torch.float16, device=dev)
+s = torch.cuda.Stream()
+s.wait_stream(torch.cuda.current_stream())
+torch.cuda.synchronize()
+print("capturing the first noalloc call", flush=True)
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=s):
+    assert E.exl3_gemv_mr_noalloc(X, T, y, SU, SV, 4, False, True) == 0
+replays = []
+for _ in range(3):
+    y.fill_(float("nan"))
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    replays.append(y.clone())
+eager = torch.empty_like(y)
+assert E.exl3_gemv_mr_noalloc(X, T, eager, SU, SV, 4, False, True) == 0
+want = torch.empty_like(y)
+assert E.exl3_gemv_mr(X, T, want, SU, None, SV, 4, False, True) == 0
+torch.cuda.synchronize()
+assert torch.equal(eager.view(torch.int16), want.view(torch.int16)), "eager noalloc != exl3_gemv_mr"
+for i, r in enumerate(replays):
+    assert torch.equal(r.view(torch.int16), eager.view(torch.int16)), f"replay {i} != eager"
+print("noalloc capture-first ok", flush=True)
+"""
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU")
+def test_noalloc_first_call_captured_in_a_fresh_process():
+    """A child process whose first exl3_gemv_mr_noalloc call is inside torch.cuda.graph: three
+    replays each equal a later eager call bitwise, and that equals exl3_gemv_mr."""
+    here = os.path.dirname(os.path.abspath(__file__))
+    paths = [os.path.join(os.path.dirname(here), "qwen38-27b-exl3-rdna4_amd"), here]
+    script = CAPTURE_FIRST.replace("PATHS", repr(paths))
+    print("child: noalloc first call under capture", flush=True)
+    r = subprocess.run([sys.executable, "-c", script], capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    assert "noalloc capture-first ok" in r.stdout, r.stdout[-2000:]
