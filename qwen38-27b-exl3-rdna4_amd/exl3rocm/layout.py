@@ -4,8 +4,9 @@ headers alone (tensor data is never read here).
 A trellis tensor is (k / 16, n / 16, 16 K) 16-bit words, so its header shape gives the module's
 input width k, output width n and bitrate K.  Checkpoint tensor names and vLLM module prefixes
 spell the same module differently ("model.language_model.layers.3..." against
-"model.layers.3..."); both are reduced to one key.  Same behaviour as the reference's
-`_norm_key` / `_read_checkpoint_layout` (vllm_plugin/exl3rocm/plugin.py:48-79).
+"model.layers.3..."); both reduce to one key.  The keys and maps are the reference's
+(`_norm_key` / `_read_checkpoint_layout`, vllm_plugin/exl3rocm/plugin.py:48-79): the checkpoint
+format and vLLM's module naming fix them.
 """
 from __future__ import annotations
 
@@ -27,17 +28,21 @@ FUSED = {
 QKV_IDS = {"q": 0, "k": 1, "v": 2}
 
 
-def norm_key(k: str) -> str:
-    """The key of a module name: decoder layers from "layers.<i>" on, the MTP head and the vision
-    tower under "mtp." / "visual.", and any other module by its last name component."""
-    parts = k.split(".")
-    if "visual" in parts:
-        return "visual." + ".".join(parts[parts.index("visual") + 1:])
-    if "mtp" in parts:
-        return "mtp." + ".".join(parts[parts.index("mtp") + 1:])
-    m = re.search(r"(layers\.\d+\..*)$", k)
-    if m:
-        return m.group(1)
+# sub-trees whose modules are keyed from their own root ("<anchor>.<rest>"), checked in this order
+SUBTREE_ROOTS = ("visual", "mtp")
+
+
+def norm_key(name: str) -> str:
+    """The key of a module name: inside the vision tower or the MTP head, the path below that
+    root prefixed with the root's name; inside the decoder stack, the path from "layers.<i>" on;
+    anything else (lm_head, embeddings) by its last component."""
+    parts = name.split(".")
+    for root in SUBTREE_ROOTS:
+        if root in parts:
+            return ".".join([root] + parts[parts.index(root) + 1:])
+    for i in range(len(parts) - 2):
+        if parts[i] == "layers" and parts[i + 1].isdigit():
+            return ".".join(parts[i:])
     return parts[-1]
 
 
@@ -51,34 +56,44 @@ def read_header(path: str) -> dict:
         return json.loads(fh.read(n))
 
 
+def _tensor_entries(model_dir: str):
+    """(name, header entry) of every tensor in the directory's *.safetensors files, files in name order."""
+    for path in sorted(glob.glob(os.path.join(model_dir, "*.safetensors"))):
+        yield from ((name, v) for name, v in read_header(path).items() if name != "__metadata__")
+
+
+def trellis_dims(shape) -> tuple:
+    """(K, k, n) of a trellis tensor of shape (k / 16, n / 16, 16 K)."""
+    kt, nt, words = shape[0], shape[1], shape[-1]
+    return words // 16, kt * 16, nt * 16
+
+
 def read_checkpoint_layout(model_dir: str):
     """Three maps over all *.safetensors files of the directory: module key -> (K, k, n) of each
     module that has a trellis, and tensor name -> dtype string / shape for every tensor."""
-    out, dtypes, shapes = {}, {}, {}
-    for f in sorted(glob.glob(os.path.join(model_dir, "*.safetensors"))):
-        for name, v in read_header(f).items():
-            if name == "__metadata__":
-                continue
-            dtypes[name] = v["dtype"]
-            shapes[name] = tuple(v["shape"])
-            if name.endswith(".trellis"):
-                s = v["shape"]
-                out[norm_key(name[: -len(".trellis")])] = (s[-1] // 16, s[0] * 16, s[1] * 16)
-    return out, dtypes, shapes
+    modules, dtypes, shapes = {}, {}, {}
+    suffix = ".trellis"
+    for name, entry in _tensor_entries(model_dir):
+        dtypes[name], shapes[name] = entry["dtype"], tuple(entry["shape"])
+        if name.endswith(suffix):
+            modules[norm_key(name[:-len(suffix)])] = trellis_dims(entry["shape"])
+    return modules, dtypes, shapes
 
 
 def groups_for(modules: dict, prefix: str, vision_qkv_bf16: bool = False):
     """The checkpoint modules behind vLLM module `prefix` (its FUSED members in output order, or
-    itself) as [(key, K, k, n)]; None when none of them is EXL3, an error when only some are
-    (the reference's Exl3Config._groups_for, plugin.py:133-147)."""
+    the module itself) as [(key, K, k, n)]; None when none of them is EXL3, an error when only
+    some are (the reference's Exl3Config._groups_for, plugin.py:133-147).  vision_qkv_bf16: the
+    vision tower's attention q/k/v stays unquantized."""
     key = norm_key(prefix)
-    if key.endswith(".attn.qkv") and key.startswith("visual.") and vision_qkv_bf16:
+    if vision_qkv_bf16 and key.startswith("visual.") and key.endswith(".attn.qkv"):
         return None
-    base, _, leaf = key.rpartition(".")
-    members = [f"{base}.{p}" if base else p for p in FUSED.get(leaf, [leaf])]
-    found = [modules.get(m) for m in members]
-    if all(f is None for f in found):
+    parent, _, leaf = key.rpartition(".")
+    names = [".".join(filter(None, (parent, member))) for member in FUSED.get(leaf, [leaf])]
+    dims = {nm: modules[nm] for nm in names if nm in modules}
+    if not dims:
         return None
-    if not all(f is not None for f in found):
-        raise AssertionError(f"exl3rocm: partially quantized fused module {prefix}")
-    return [(m, *f) for m, f in zip(members, found)]
+    if len(dims) != len(names):
+        absent = [nm for nm in names if nm not in dims]
+        raise AssertionError(f"exl3rocm: fused module {prefix}: {absent} have no trellis, the rest do")
+    return [(nm, *dims[nm]) for nm in names]

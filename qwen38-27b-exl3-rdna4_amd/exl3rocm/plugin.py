@@ -83,16 +83,35 @@ class Exl3FormatError(ValueError):
     inconsistent bitrate)."""
 
 
-def check_codebook_scalar(kind: str, value: int) -> bool:
-    """True when `value` (as an unsigned or signed 32-bit integer) is the multiplier the kernels
-    implement for codebook `kind`."""
-    return (int(value) & 0xFFFFFFFF) == CODEBOOK_MULTIPLIERS[kind]
+class Exl3LoadError(AssertionError):
+    """A checkpoint tensor that does not fit the layer it is loaded into (shape, shard id, a
+    missing tensor, partitions that do not tile the groups).  An AssertionError, the kind vLLM's
+    loaders and the reference plugin raise for these, but raised explicitly: it survives
+    `python -O`."""
 
 
-def require_codebook_scalar(kind: str, value: int, where: str = "") -> int:
+def _as_u32(value) -> int:
+    """A multiplier as stored: an integer (signed or unsigned 32-bit, e.g. an int32 tensor's
+    item()) or a string in any base int() reads with base 0 ("0x83DCD12D", "2212286765").  How
+    a real checkpoint stores it is not fixed by any reference fixture, so every such form is read."""
+    if isinstance(value, str):
+        try:
+            value = int(value.strip(), 0)
+        except ValueError as e:
+            raise Exl3FormatError(f"exl3rocm: codebook multiplier {value!r} is not an integer") from e
+    return int(value) & 0xFFFFFFFF
+
+
+def check_codebook_scalar(kind: str, value) -> bool:
+    """True when `value` (a signed or unsigned 32-bit integer, or its text) is the multiplier the
+    kernels implement for codebook `kind`."""
+    return _as_u32(value) == CODEBOOK_MULTIPLIERS[kind]
+
+
+def require_codebook_scalar(kind: str, value, where: str = "") -> int:
     """The scalar as an unsigned 32-bit multiplier; raises Exl3FormatError when it is not the
     kernels' (the reference only checks that the scalar is present, plugin.py:334-335)."""
-    v = int(value) & 0xFFFFFFFF
+    v = _as_u32(value)
     if v != CODEBOOK_MULTIPLIERS[kind]:
         raise Exl3FormatError(f"exl3rocm: {where or kind} multiplier {v:#010x} is not the {kind} codebook's "
                               f"{CODEBOOK_MULTIPLIERS[kind]:#010x}; the kernels cannot decode these weights")
@@ -186,26 +205,35 @@ def _partition_groups(parts: list, widths: list) -> list:
         starts.append(off)
         off += p
     tiled = off == ends[-1] and all(e in set(starts) | {off} for e in ends)
-    assert tiled, f"exl3rocm: partitions {parts} do not tile groups {widths}"
+    if not tiled:
+        raise Exl3LoadError(f"exl3rocm: output partitions {parts} do not tile the checkpoint groups {widths}")
     return [bisect.bisect_right(ends, s) - 1 for s in starts]
 
 
-def _shard_group(layer, shard_id) -> int:
-    """The group a checkpoint tensor loads into, from vLLM's shard id: None (unfused module),
-    "q" / "k" / "v", a partition index, or a tuple of partition indices (all in one group)."""
-    groups = layer.exl3_part_to_group
-    if shard_id is None:
-        assert len(layer.exl3_n) == 1, "exl3rocm: unsharded load into fused module"
-        return 0
+def _shard_partitions(shard_id) -> tuple:
+    """vLLM's shard id as the output partitions it names: "q" / "k" / "v", one partition index,
+    or a tuple of them (a checkpoint tensor covering several partitions)."""
     if isinstance(shard_id, str):
-        idx = [QKV_IDS[shard_id]]
-    elif isinstance(shard_id, int):
-        idx = [shard_id]
-    else:
-        idx = list(shard_id)
-    found = {groups[i] for i in idx}
-    assert len(found) == 1, f"exl3rocm: shard {shard_id} spans groups {found}"
-    return next(iter(found))
+        return (QKV_IDS[shard_id],)
+    if isinstance(shard_id, int):
+        return (shard_id,)
+    return tuple(shard_id)
+
+
+def _shard_group(layer, shard_id) -> int:
+    """The group a checkpoint tensor fills.  Without a shard id the module must have a single
+    group; otherwise every partition the id names must map to the same group."""
+    if shard_id is None:
+        if len(layer.exl3_n) != 1:
+            raise Exl3LoadError(f"exl3rocm: a tensor with no shard id cannot choose among "
+                                f"{len(layer.exl3_n)} groups of a fused module")
+        return 0
+    parts = _shard_partitions(shard_id)
+    targets = sorted({layer.exl3_part_to_group[p] for p in parts})
+    if len(targets) != 1:
+        raise Exl3LoadError(f"exl3rocm: shard id {shard_id!r} names partitions {list(parts)} of groups "
+                            f"{targets}; a checkpoint tensor fills exactly one group")
+    return targets[0]
 
 
 class _Router:
@@ -226,12 +254,15 @@ class _Router:
                 raise Exl3FormatError(f"exl3rocm: {self.kind} scalar {v:#010x} differs from the checkpoint's "
                                       f"quantization_config {self.expected:#010x}")
             seen = getattr(layer, f"exl3_{self.kind}")
-            assert seen is None or seen == v, f"exl3rocm: {self.kind} differs across groups"
+            if seen is not None and seen != v:
+                raise Exl3LoadError(f"exl3rocm: group {g} names {self.kind} {v:#010x}, an earlier group "
+                                    f"{seen:#010x}")
             setattr(layer, f"exl3_{self.kind}", v)
         else:
             dst = getattr(layer, f"exl3_{self.kind}_{g}")
-            assert tuple(w.shape) == tuple(dst.shape), \
-                f"exl3rocm: {self.kind} shape {tuple(w.shape)} vs {tuple(dst.shape)} (group {g})"
+            if tuple(w.shape) != tuple(dst.shape):
+                raise Exl3LoadError(f"exl3rocm: group {g} holds a {self.kind} of shape {tuple(dst.shape)}; "
+                                    f"the checkpoint tensor is {tuple(w.shape)}")
             dst.copy_(w)
         layer.exl3_loaded.add((self.kind, g))
 
@@ -254,7 +285,8 @@ class Exl3LinearMethod(LinearMethodBase):
         Ks = [g[1] for g in self.groups]
         widths = [g[3] for g in self.groups]
         for key, gk in zip(keys, (g[2] for g in self.groups)):
-            assert gk == k, f"exl3rocm: {key} k={gk} vs layer k={k}"
+            if gk != k:
+                raise Exl3LoadError(f"exl3rocm: checkpoint tensor {key} has {gk} inputs, the layer {k}")
         layer.exl3_part_to_group = _partition_groups(list(output_partition_sizes), widths)
         layer.exl3_K, layer.exl3_n = Ks, widths
         for i, (K, n) in enumerate(zip(Ks, widths)):
@@ -282,7 +314,8 @@ class Exl3LinearMethod(LinearMethodBase):
     def process_weights_after_loading(self, layer):
         ng = len(layer.exl3_n)
         missing = sorted({(kind, g) for kind in TENSOR_KINDS for g in range(ng)} - layer.exl3_loaded)
-        assert not missing, f"exl3rocm: missing tensors {missing}"
+        if missing:
+            raise Exl3LoadError(f"exl3rocm: never loaded, as (kind, group): {missing} (missing tensors)")
         layer.exl3_is_mul1 = layer.exl3_mul1 is not None
         layer.exl3_is_mcg = layer.exl3_mcg is not None
         dev = layer.exl3_trellis_0.device
@@ -292,6 +325,9 @@ class Exl3LinearMethod(LinearMethodBase):
             k = layer.exl3_trellis_0.shape[0] * 16
             for K, n in zip(layer.exl3_K, layer.exl3_n):
                 ops.reserve_workspace(dev, k, n, K, groups=min(ng, 4))
+            # the prefill's split workspace: one size serves every shape (each further stream
+            # allocates it on its first eager prefill call)
+            ops.E.reserve_prefill_workspace(dev)
             if ops.PREFILL_ROUTE == "recon":
                 ops.reserve_weight_buffer(dev, k * min(max(layer.exl3_n), ops.RECON_SLICE_N))
         # equal-K, equal-width groups (gate/up) take the pointer-table launch at M == 1

@@ -285,3 +285,19 @@ def test_approx_route_setting():
     for bad in ("1", "7", "int4", "affin"):
         with pytest.raises(ValueError):
             ops.approx_mode(bad)
+
+
+@pytest.mark.parametrize("mode", ["", "affine", "int8"])
+def test_empty_batch_launches_nothing_on_every_route(monkeypatch, mode):
+    """A zero-row input returns an empty [0, sum(widths)] output before any route is chosen: the
+    approximate GEMV (which declines m = 0) is never reached.  No launch happens, so CPU tensors
+    show it without a GPU."""
+    monkeypatch.setattr(ops, "GEMV_APPROX", mode)
+    x = torch.zeros(0, 256, dtype=torch.float16)
+    tr = [torch.zeros(16, 8, 64, dtype=torch.int16) for _ in range(2)]
+    s = [torch.ones(256, dtype=torch.float16)] * 2
+    v = [torch.ones(128, dtype=torch.float16)] * 2
+    y = torch.ops.exl3rocm.linear_groups(x, tr, s, v, [4, 4], False, True)
+    assert tuple(y.shape) == (0, 256) and y.dtype == torch.float16
+    y3 = torch.ops.exl3rocm.linear_groups(x.view(1, 0, 256), tr, s, v, [4, 4], False, True)
+    assert tuple(y3.shape) == (1, 0, 256)
