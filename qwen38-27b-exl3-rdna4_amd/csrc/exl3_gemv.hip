@@ -480,6 +480,29 @@ int exl3_gemv_prerot_rows(void) { return prerot_rows(); }
 
 int exl3_gemv_silu_prerot_rows(void) { return silu_prerot_rows(); }
 
+#ifdef EXL3_TIMELINE
+// Tracing build only (include/exl3_mi355x_timeline.h): the GEMV's per-workgroup phase stamps.
+int exl3_timeline_shape(int* max_wgs, int* phases)
+{
+    if (max_wgs) *max_wgs = TL_MAX_WGS;
+    if (phases) *phases = TL_PHASES;
+    return EXL3_OK;
+}
+
+int exl3_timeline_clear(void)
+{
+    static const unsigned long long zeros[TL_MAX_WGS * TL_PHASES] = {};
+    return hipMemcpyToSymbol(HIP_SYMBOL(exl3_tl), zeros, sizeof(zeros)) == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
+}
+
+int exl3_timeline_read(void* host, size_t bytes)
+{
+    if (!host || bytes > sizeof(unsigned long long) * TL_MAX_WGS * TL_PHASES) return EXL3_EINVAL;
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(exl3_tl), bytes, 0, hipMemcpyDeviceToHost) == hipSuccess ? EXL3_OK
+                                                                                                         : EXL3_ELAUNCH;
+}
+#endif
+
 int exl3_gemv_split_check(int U, int G, int h, int wa, int wb)
 {
     if (U < 1 || G < 1 || h < 0 || h > G || wa < 1 || wb < 1) return -1;

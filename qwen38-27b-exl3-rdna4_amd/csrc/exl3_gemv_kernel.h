@@ -108,6 +108,39 @@ constexpr int LDS_BUDGET = 64 * 1024;           // per workgroup: 2 workgroups p
 constexpr int RING = 4;
 constexpr int WAVES_PER_SIMD = 2;
 
+// Phase timeline (tracing builds only: -DEXL3_TIMELINE, libexl3_mi355x_timeline.so).  Thread 0 of
+// every workgroup writes the 100 MHz s_memrealtime counter at each phase boundary into
+// exl3_tl[workgroup][phase] (a vector store; phases a workgroup does not reach keep their last
+// value, so a reader clears the array first); exl3_timeline_read copies it out.  The product build
+// compiles EXL3_TL to nothing.
+enum { TL_ENTRY = 0, TL_ISSUED, TL_LOOP, TL_LOOP_END, TL_STORED, TL_COUNTED, TL_SUMMED, TL_END, TL_HWID, TL_PHASES };
+constexpr int TL_MAX_WGS = 4096;
+#ifdef EXL3_TIMELINE
+__device__ unsigned long long exl3_tl[TL_MAX_WGS * TL_PHASES];
+#define EXL3_TL(k)                                                                                        \
+    do {                                                                                                  \
+        __builtin_amdgcn_sched_barrier(0);                                                                \
+        if (threadIdx.x == 0 && blockIdx.x < TL_MAX_WGS)                                                  \
+            exl3_tl[blockIdx.x * TL_PHASES + (k)] = __builtin_amdgcn_s_memrealtime();                     \
+        __builtin_amdgcn_sched_barrier(0);                                                                \
+    } while (0)
+#else
+#define EXL3_TL(k) ((void) 0)
+#endif
+// the workgroup's placement, stamped at entry in the tracing build: HW_ID (CU, SH, SE in its low
+// 16 bits) and XCC_ID in the high word
+#ifdef EXL3_TIMELINE
+#define EXL3_TL_HWID()                                                                                    \
+    do {                                                                                                  \
+        if (threadIdx.x == 0 && blockIdx.x < TL_MAX_WGS)                                                  \
+            exl3_tl[blockIdx.x * TL_PHASES + TL_HWID] =                                                   \
+                (unsigned long long) __builtin_amdgcn_s_getreg((31 << 11) | 4) |                          \
+                ((unsigned long long) __builtin_amdgcn_s_getreg((15 << 11) | 20) << 32);                  \
+    } while (0)
+#else
+#define EXL3_TL_HWID() ((void) 0)
+#endif
+
 // s_waitcnt vmcnt(0) (gfx9 encoding: expcnt / lgkmcnt left at their maxima), fenced against
 // compiler reordering: every vector-memory store of this wave has completed.
 __device__ __forceinline__ void wait_stores_complete()
@@ -183,6 +216,20 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
 {
     constexpr bool GATED = FORM == FORM_GATED;
     extern __shared__ __align__(16) uint16_t smem[];
+    EXL3_TL(TL_ENTRY);
+    EXL3_TL_HWID();
+    {
+        // Request every 64-byte line of the argument struct at once: the argument reads that
+        // depend on earlier ones (the group's fields after the group index, then the input
+        // pointers) hit the scalar cache instead of each costing a memory round trip before the
+        // first trellis request.
+        const uint32_t __attribute__((address_space(4)))* kp =
+            (const uint32_t __attribute__((address_space(4)))*) __builtin_amdgcn_kernarg_segment_ptr();
+        uint32_t touch = 0;
+#pragma unroll
+        for (int l = 0; l < (int) ((sizeof(GemvArgs) + 63) / 64); ++l) touch += kp[l * 16];
+        asm volatile("" ::"s"(touch));
+    }
     __shared__ int s_last[256];
     __shared__ int s_list[256];
     __shared__ int s_nred;
@@ -348,26 +395,28 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // a single row of at most 4 jobs: one job per wave, two columns a lane (had128_x2, a fourth
     // of the 16-lane transform's latency)
     const bool wide = MT_ == 0 && nfirst <= 4;
+    // The loads are unconditional: a job past nfirst reads job 0's (in-bounds) input, and its
+    // results are never stored (the 16 lanes of a job exchange data only among themselves).  A
+    // load under a condition would merge with the zero-initialised register after the branch, and
+    // that copy would wait for the load before the trellis requests below could issue.
     if (wide) {
-        if (wave < nfirst) {
-            const int u = ulo + wave;
-            const int col = (u - (u / UPB) * UPB) * 128 + 2 * lane;
-            px.x = *reinterpret_cast<gc_u32*>(gx + col);
-            if (silu_in) pu.x = *reinterpret_cast<gc_u32*>(gxu + col);
-            ps.x = *reinterpret_cast<gc_u32*>(gsuh + col);
-        }
+        const int u = ulo + (wave < nfirst ? wave : 0);
+        const int col = (u - (u / UPB) * UPB) * 128 + 2 * lane;
+        px.x = *reinterpret_cast<gc_u32*>(gx + col);
+        if (silu_in) pu.x = *reinterpret_cast<gc_u32*>(gxu + col);
+        ps.x = *reinterpret_cast<gc_u32*>(gsuh + col);
     } else {
         const int i = threadIdx.x >> 4;
-        if (i < nfirst) {
+        {
             int m, col;
-            job_src(ulo, i, m, col);
+            job_src(ulo, i < nfirst ? i : 0, m, col);
             px = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * ldx + col);
             if (silu_in) pu = *reinterpret_cast<gc_u32x4*>(gxu + (int64_t) m * ldx + col);
             if (!pre) ps = *reinterpret_cast<gc_u32x4*>(gsuh + col);
         }
-        if (i + 16 < nfirst) {
+        if (nfirst > 16) {
             int m, col;
-            job_src(ulo, i + 16, m, col);
+            job_src(ulo, i + 16 < nfirst ? i + 16 : 0, m, col);
             px2 = *reinterpret_cast<gc_u32x4*>(gx + (int64_t) m * ldx + col);
             if (silu_in) pu2 = *reinterpret_cast<gc_u32x4*>(gxu + (int64_t) m * ldx + col);
             if (!pre) ps2 = *reinterpret_cast<gc_u32x4*>(gsuh + col);
@@ -399,6 +448,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
         if (i & 1) advance_load();
     };
     static_for(std::make_integer_sequence<int, RING / 2>{}, fill);
+    EXL3_TL(TL_ISSUED);
     // rotated input of units [c0, c1) -> LDS; with have_first the lane's first two 16-lane jobs use
     // (x0, s0, u0) and (x1, s1, u1) (u: the up rows of a gated-MLP input)
     auto rotate_chunk = [&](int c0, int c1, u32x4 x0, u32x4 s0, u32x4 x1, u32x4 s1, u32x4 u0, u32x4 u1,
@@ -633,6 +683,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // In the loop the second-dispatched workgroup of a CU runs at the higher priority (and takes
     // the larger unit share, weights 2 : 3): it starts later, and at equal priority the arbiter
     // favours the older wave, so the younger one's loop ended last (timeline probe).
+    EXL3_TL(TL_LOOP);
     if (older) __builtin_amdgcn_s_setprio(0);
     else __builtin_amdgcn_s_setprio(1);
     // Full ring turns run without per-step conditions (a conditional step would make the compiler
@@ -652,6 +703,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             if (s0 + decltype(I)::value < S) sub_step(I, u0, false);
         });
     }
+    EXL3_TL(TL_LOOP_END);
     __builtin_amdgcn_s_setprio(2);
     write_partial(cb_cur);
 
@@ -659,6 +711,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // The partials are device-scope (write-through) stores: once complete (vmcnt(0)) they are
     // visible to device-scope loads from any XCD, so no cache-wide release is needed.
     wait_stores_complete();
+    EXL3_TL(TL_STORED);
     __syncthreads();
     const int nblk = cb_cur - seg0_cb + 1;
     // completed blocks (gated: block pairs, 2M rows each: gate, then up) reduced side by side
@@ -706,6 +759,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
         }
         __syncthreads();
         const int nred = __builtin_amdgcn_readfirstlane(s_nred);
+        EXL3_TL(TL_COUNTED);
         for (int r0 = 0; r0 < nred; r0 += RB) {
             const int rb = min(RB, nred - r0);
             // svh of the first output-transform pass, requested before the partial loads so that its
@@ -944,6 +998,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                     if (has_b) lds_c[lb] = f16_bits((f16) sb);
                 }
             }
+            EXL3_TL(TL_SUMMED);
             if ((int) threadIdx.x < rb)                        // ready for the next call (stream order)
                 __hip_atomic_store(&counters[(seg0_cb + b0 + s_list[r0 + threadIdx.x]) * CNT_STRIDE], 0u, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
@@ -1028,6 +1083,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             __syncthreads();                                   // lds_c free for the next blocks
         }
     }
+    EXL3_TL(TL_END);
 }
 
 // LDS: chunk_units x (m + 1) input rows, then the C rows of the blocks reduced side by side (the
