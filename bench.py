@@ -70,21 +70,29 @@ class LayerSet:
         g = [self.w["gate"], self.w["up"]]
         self.gu_ptrs = [torch.tensor([x[i].data_ptr() for x in g], dtype=torch.int64, device=dev) for i in range(3)]
 
-    def step(self, x5120, x17408):
-        t = self.t
-        ops = t.ops.exl3rocm
+    def launch(self, name, x5120, x17408):
+        """One of the step's four GEMV launches, as the plugin makes it: "qkv" (one grouped-widths
+        launch), "o", "gate_up" (the grouped pointer-table launch) or "down"."""
+        ops = self.t.ops.exl3rocm
         w, b, mc, m1 = self.w, self.bits, self.mcg, self.mul1
-        qkv = ops.linear_groups(x5120, [w["q"][0], w["k"][0], w["v"][0]], [w["q"][1], w["k"][1], w["v"][1]],
-                                [w["q"][2], w["k"][2], w["v"][2]], [b, b, b], mc, m1)
-        o = ops.linear(x5120, *w["o"], b, mc, m1)
-        gu = ops.linear_groups(x5120, [w["gate"][0], w["up"][0]], [w["gate"][1], w["up"][1]],
-                               [w["gate"][2], w["up"][2]], [b, b], mc, m1, *self.gu_ptrs)
-        d = ops.linear(x17408, *w["down"], b, mc, m1)
-        return qkv, o, gu, d
+        if name == "qkv":
+            return ops.linear_groups(x5120, [w["q"][0], w["k"][0], w["v"][0]], [w["q"][1], w["k"][1], w["v"][1]],
+                                     [w["q"][2], w["k"][2], w["v"][2]], [b, b, b], mc, m1)
+        if name == "gate_up":
+            return ops.linear_groups(x5120, [w["gate"][0], w["up"][0]], [w["gate"][1], w["up"][1]],
+                                     [w["gate"][2], w["up"][2]], [b, b], mc, m1, *self.gu_ptrs)
+        return ops.linear(x17408 if name == "down" else x5120, *w[name], b, mc, m1)
+
+    def step(self, x5120, x17408):
+        return tuple(self.launch(name, x5120, x17408) for name in STEP_LAUNCHES)
+
+
+# the step's GEMV launches: q/k/v grouped (mixed widths), o, gate/up grouped (pointer tables), down
+STEP_LAUNCHES = ("qkv", "o", "gate_up", "down")
 
 
 def launches_per_step():
-    return 1 + 1 + 1 + 1      # q/k/v grouped (mixed widths) + o + gate/up grouped + down
+    return len(STEP_LAUNCHES)
 
 
 def build_layers(torch, bits, copies, mul1=True, tag="config1"):
@@ -125,6 +133,38 @@ def capture_steps(torch, sets, x5120, x17408, steps):
     rest = graph_of(0, steps % block) if steps % block else None
     torch.cuda.synchronize()
     return {"singles": singles, "block": block, "full": full, "rest": rest}
+
+
+def device_copy_gbs(torch, nbytes=1 << 30, reps=30):
+    """What HBM delivers: a 1 GiB torch copy_ (read + write bytes counted, 4x the 256 MB cache),
+    median of `reps` HIP-event-timed copies after 5 untimed (the reference's roofline probe,
+    bench/bench_layer.py:43-60, at a size past this GPU's cache); and a read-only sweep (a sum over
+    the same 1 GiB, median of `reps`).  Returns (copy GB/s, read GB/s)."""
+    src = torch.ones(nbytes // 2, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dst.copy_(src)
+        e1.record()
+        e1.synchronize()
+        ts.append(e0.elapsed_time(e1) * 1e3)
+    # read only (the GEMV's traffic is almost all reads): a sum over the same 1 GiB
+    tr = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        src.sum(dtype=torch.float32)
+        e1.record()
+        e1.synchronize()
+        tr.append(e0.elapsed_time(e1) * 1e3)
+    del src, dst
+    torch.cuda.empty_cache()
+    return round(2.0 * nbytes / float(np.median(ts)) / 1e3, 1), round(nbytes / float(np.median(tr)) / 1e3, 1)
 
 
 def time_graphs(torch, graphs, steps, warmup):
@@ -179,6 +219,84 @@ def per_shape_gemv(torch, sets, x5120, x17408, reps=64):
         out[name] = {"k": k, "n": n, "us": round(us, 3), "gbs": round(b / us / 1e3, 1),
                      "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
     return out
+
+
+# The reference checkpoint's GEMV shapes with their calls per decode token (the reference's
+# scoreboard, vllm_plugin/tests/gemv_bench.py:18-28): (name, k, n, bits, calls per token)
+CKPT_CASES = [
+    ("gate|up K3", 5120, 17408, 3, 70), ("gate|up K2", 5120, 17408, 2, 56), ("gate|up K1", 5120, 17408, 1, 2),
+    ("down K3", 17408, 5120, 3, 64),
+    ("gdn qkv K4", 5120, 10240, 4, 12), ("gdn qkv K2", 5120, 10240, 2, 35),
+    ("gdn z K4", 5120, 6144, 4, 48), ("gdn out K4", 6144, 5120, 4, 48),
+    ("attn q K2", 5120, 12288, 2, 11), ("attn q K4", 5120, 12288, 4, 4),
+    ("attn kv K5", 5120, 1024, 5, 18), ("attn kv K6", 5120, 1024, 6, 8), ("attn kv K4", 5120, 1024, 4, 6),
+    ("attn o K3", 6144, 5120, 3, 4), ("attn o K5", 6144, 5120, 5, 4),
+    ("lm_head K4", 5120, 248320, 4, 1),
+]
+CKPT_PREFILL = [("gdn qkv", 5120, 10240, 4), ("gdn out / attn o", 6144, 5120, 4), ("lm_head", 5120, 248320, 4)]
+
+
+def _device_layer(torch, k, n, bits, g):
+    T = torch.randint(0, 65536, (k // 16, n // 16, 16 * bits), device="cuda", dtype=torch.int32, generator=g).to(torch.int16)
+    su = (torch.randn(k, device="cuda", generator=g).sign() * torch.exp(0.25 * torch.randn(k, device="cuda", generator=g))).half()
+    sv = (torch.randn(n, device="cuda", generator=g).sign() * torch.exp(0.25 * torch.randn(n, device="cuda", generator=g))).half()
+    return T, su, sv
+
+
+def checkpoint_shapes(torch, reps=32, m_prefill=2048):
+    """The reference checkpoint's own shapes: every M = 1 case of the reference's GEMV scoreboard
+    (device-generated weights, enough copies for >= 1 GiB so they stream from HBM; mean of a graph
+    of `reps` launches over the copies, HIP events), its per-token total weighted by calls per
+    decode token, and the prefill at M = 2048 on its three shapes outside configuration 1."""
+    g = torch.Generator(device="cuda").manual_seed(20261202)
+    s = torch.cuda.Stream()
+    gemv, total_us = {}, 0.0
+    for name, k, n, bits, calls in CKPT_CASES:
+        copies = max(2, (1 << 30) // (k * n * bits // 8) + 1)
+        ws = [_device_layer(torch, k, n, bits, g) for _ in range(copies)]
+        x = torch.randn(1, k, device="cuda", dtype=torch.float16, generator=g)
+        y = torch.empty(1, n, dtype=torch.float16, device="cuda")
+        with torch.cuda.stream(s):
+            for w in ws:
+                torch.ops.exl3rocm.linear(x, *w, bits, False, True)
+        s.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            for r in range(reps):
+                y = torch.ops.exl3rocm.linear(x, *ws[r % copies], bits, False, True)
+        with torch.cuda.stream(s):
+            graph.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            for _ in range(3):
+                graph.replay()
+            e1.record(s)
+        s.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (3 * reps)
+        b = algo_bytes(1, k, n, bits)
+        gemv[name] = {"k": k, "n": n, "bits": bits, "calls_per_token": calls, "us": round(us, 2),
+                      "gbs": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+        total_us += us * calls
+        del graph, ws
+        torch.cuda.empty_cache()
+    prefill = {}
+    for name, k, n, bits in CKPT_PREFILL:
+        w = _device_layer(torch, k, n, bits, g)
+        x = torch.randn(m_prefill, k, device="cuda", dtype=torch.float16, generator=g)
+        torch.ops.exl3rocm.linear(x, *w, bits, False, True)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(4):
+            torch.ops.exl3rocm.linear(x, *w, bits, False, True)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / 4
+        prefill[name] = {"m": m_prefill, "k": k, "n": n, "bits": bits, "us": round(us, 1),
+                         "tflops": round(2 * m_prefill * k * n / us / 1e6, 1)}
+        del w, x
+        torch.cuda.empty_cache()
+    return {"gemv_m1": gemv, "gemv_us_per_token_weighted": round(total_us, 1), "prefill": prefill}
 
 
 def approx_m1(torch, sets, x5120, x17408, reps=64):
@@ -294,28 +412,33 @@ def gated_mlp(torch, sets, x5120, ms=(1, 8), reps=32):
     return out
 
 
-def cpu_baseline(base, bits, budget_s=8.0):
+def cpu_baseline(base, bits, budget_s=8.0, reps=5):
     """The C oracle restatement on the host cores: the configuration-1 layer's 7 faithful GEMVs at
-    M = 1 repeated for `budget_s` on every thread of this process's CPU share (the headline
-    baseline), plus bounded side samples: one thread, decode only (reconstruct), configuration 0
-    (4096 x 4096 mcg), configuration 2 (gate shape at 2 / 3 / 5 / 6 / 8 bpw) and a configuration-4
-    subsample (q at M = 64).  Every figure is GB/s of the same algorithmic bytes as the GPU's."""
+    M = 1 on every thread of this process's CPU share (the affinity mask, or OMP_NUM_THREADS where
+    set), repeated until `budget_s` and at least `reps` times (the headline baseline), plus bounded
+    side samples: one thread (q shape), decode only (reconstruct), configuration 0 (4096 x 4096
+    mcg), configuration 2 (gate shape at 2 / 3 / 5 / 6 / 8 bpw) and a configuration-4 subsample (q
+    at M = 64).  Every figure is the median over at least `reps` timed repetitions (after one
+    untimed), in GB/s of the same algorithmic bytes as the GPU's."""
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     import cpu  # noqa: E402  (oracle: test infrastructure, used here only as the baseline)
     from exl3rocm import synth
     affinity = len(os.sched_getaffinity(0))
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, affinity)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or affinity
     x = {k: synth.activations(synth.key_of("cpu", k), 1, k) for k in (HIDDEN, INTER)}
     layer_bytes = sum(algo_bytes(1, k, n, bits) for _, k, n in LAYER)
 
-    def timed(fn, nbytes, budget, min_reps=1):
-        t0 = time.perf_counter()
-        reps = 0
-        while reps < min_reps or time.perf_counter() - t0 < budget:
+    def timed(fn, nbytes, budget=0.0):
+        fn()                                           # untimed: first touch, thread pool start
+        times = []
+        t_end = time.perf_counter() + budget
+        while len(times) < reps or time.perf_counter() < t_end:
+            t0 = time.perf_counter()
             fn()
-            reps += 1
-        dt = time.perf_counter() - t0
-        return {"gbs": round(reps * nbytes / dt / 1e9, 4), "us_per_call": round(dt / reps * 1e6, 1), "reps": reps}
+            times.append(time.perf_counter() - t0)
+        med = float(np.median(times))
+        return {"gbs": round(nbytes / med / 1e9, 4), "us_per_call": round(med * 1e6, 1), "reps": len(times),
+                "stat": "median"}
 
     def layer(th):
         for name, k, n in LAYER:
@@ -324,25 +447,26 @@ def cpu_baseline(base, bits, budget_s=8.0):
 
     head = timed(lambda: layer(threads), layer_bytes, budget_s)
     side = {"threads": threads, "affinity_cores": affinity}
-    gate_tr, gate_su, gate_sv = base["gate"]
-    side["config1_gate_1thread"] = timed(lambda: cpu.linear(x[HIDDEN], gate_tr, bits, gate_su, gate_sv, 2, threads=1),
-                                         algo_bytes(1, HIDDEN, INTER, bits), 2.0)
-    gate_bytes = HIDDEN * INTER * bits // 8
-    side["decode_only_gate"] = timed(lambda: cpu.reconstruct(gate_tr, bits, 2, threads=threads), gate_bytes, 2.0)
+    q_tr, q_su, q_sv = base["q"]
+    side["config1_q_1thread"] = timed(lambda: cpu.linear(x[HIDDEN], q_tr, bits, q_su, q_sv, 2, threads=1),
+                                      algo_bytes(1, HIDDEN, HIDDEN, bits))
+    gate_tr = base["gate"][0]
+    side["decode_only_gate"] = timed(lambda: cpu.reconstruct(gate_tr, bits, 2, threads=threads),
+                                     HIDDEN * INTER * bits // 8)
     tr0, su0, sv0 = synth.layer("cpu-config0", 0, 4096, 4096, 4)
     x0 = synth.activations(synth.key_of("cpu-config0", "x"), 1, 4096)
     side["config0_mcg_4096"] = timed(lambda: cpu.linear(x0, tr0, 4, su0, sv0, 1, threads=threads),
-                                     algo_bytes(1, 4096, 4096, 4), 2.0)
+                                     algo_bytes(1, 4096, 4096, 4))
     sweep = {}
     for b in (2, 3, 5, 6, 8):
         trb, sub, svb = synth.layer("cpu-config2", b, HIDDEN, INTER, b)
         sweep[f"{b}bpw"] = timed(lambda: cpu.linear(x[HIDDEN], trb, b, sub, svb, 2, threads=threads),
-                                 algo_bytes(1, HIDDEN, INTER, b), 0.0)
+                                 algo_bytes(1, HIDDEN, INTER, b))
     side["config2_gate_sweep"] = sweep
     x64 = synth.activations(synth.key_of("cpu-config4", "x"), 64, HIDDEN)
     trq, suq, svq = base["q"]
     side["config4_q_m64"] = timed(lambda: cpu.linear(x64, trq, bits, suq, svq, 2, threads=threads),
-                                  algo_bytes(64, HIDDEN, HIDDEN, bits), 0.0)
+                                  algo_bytes(64, HIDDEN, HIDDEN, bits))
     side["config4_q_m64"]["tflops"] = round(2 * 64 * HIDDEN * HIDDEN / (side["config4_q_m64"]["us_per_call"] * 1e6), 6)
     model = ""
     try:
@@ -352,9 +476,9 @@ def cpu_baseline(base, bits, budget_s=8.0):
         pass
     side["cpu_model"] = model
     return {"value": head["gbs"], "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{head['reps']} x the 7 linears of one configuration-1 layer at M=1, 4 bpw mul1 "
-                      f"(C oracle restatement, OpenMP {threads} threads of {affinity} in the affinity mask, "
-                      f"{head['reps'] * head['us_per_call'] / 1e6:.1f} s); cpu: {model}",
+            "sample": f"median of {head['reps']} repetitions of the 7 linears of one configuration-1 layer at M=1, "
+                      f"4 bpw mul1 (C oracle restatement, OpenMP {threads} threads of {affinity} in the affinity "
+                      f"mask, {head['reps'] * head['us_per_call'] / 1e6:.1f} s); cpu: {model}",
             "side": side}
 
 
@@ -532,6 +656,88 @@ def traffic_probe(torch, bits=4, copies=8):
     return 0
 
 
+TL_NAMES = ("entry", "issued", "loop", "loop_end", "stored", "counted", "summed", "end")
+
+
+def timeline(torch, sets, x5120, x17408, reps=16):
+    """--timeline (the tracing library, libexl3_mi355x_timeline.so): per-workgroup phase stamps
+    (include/exl3_mi355x_timeline.h) of each configuration-1 GEMV launch.  A graph of `reps`
+    launches of one kind over the weight copies is replayed twice; the stamps are those of its last
+    launch (steady state, weights from HBM).  Times in us from the first workgroup's entry: the
+    median and the last workgroup per phase, the critical (last-ending) workgroup's own phases, and
+    the launch's mean duration from HIP events on the replay stream."""
+    import ctypes
+    from exl3rocm import _lib
+    L = _lib.lib()
+    if not hasattr(L, "exl3_timeline_read"):
+        raise SystemExit("bench.py --timeline needs the tracing library (build_ext.py --timeline)")
+    ip = ctypes.POINTER(ctypes.c_int)
+    L.exl3_timeline_shape.argtypes = [ip, ip]
+    L.exl3_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    mw, ph = ctypes.c_int(), ctypes.c_int()
+    L.exl3_timeline_shape(ctypes.byref(mw), ctypes.byref(ph))
+    buf = np.zeros(mw.value * ph.value, dtype=np.uint64)
+    s = torch.cuda.Stream()
+    out = {}
+    for name in STEP_LAUNCHES:
+        with torch.cuda.stream(s):
+            for ls in sets:
+                ls.launch(name, x5120, x17408)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for r in range(reps):
+                sets[r % len(sets)].launch(name, x5120, x17408)
+        assert L.exl3_timeline_clear() == 0
+        with torch.cuda.stream(s):
+            g.replay()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            g.replay()
+            e1.record(s)
+        s.synchronize()
+        assert L.exl3_timeline_read(buf.ctypes.data, buf.nbytes) == 0
+        raw = buf.reshape(mw.value, ph.value)
+        live = raw[:, 0] != 0                                # workgroups of this launch (all run)
+        hw = raw[live, 8]
+        t = raw[live, :8].astype(np.int64)
+        us = (t - t[:, :1].min()) * 10 / 1e3                 # 100 MHz ticks -> us from the first entry
+        reducer = t[:, 6] >= t[:, 0]                         # reduced in this launch (not a stale stamp)
+        # per CU (XCC, SE, SH, CU): when its last loop ended; first-dispatched (older) workgroups
+        cu = ((hw >> np.uint64(32)) * np.uint64(1 << 16) + ((hw >> np.uint64(8)) & np.uint64(0xFF))).astype(np.int64)
+        cu_end = np.array([us[cu == c, 3].max() for c in np.unique(cu)])
+        xcc = (hw >> np.uint64(32)).astype(np.int64)
+        older = np.arange(len(t)) < min(256, len(t))
+        crit = int(np.argmax(us[:, 7]))
+        row = {"wgs": int(len(t)), "launch_us": round(e0.elapsed_time(e1) * 1e3 / reps, 2)}
+        for i, nm in enumerate(TL_NAMES):
+            col = us[reducer, i] if nm == "summed" else us[:, i]
+            row[nm] = {"p50": round(float(np.median(col)), 2), "max": round(float(col.max()), 2)}
+        row["loop_us"] = {"p50": round(float(np.median(us[:, 3] - us[:, 2])), 2),
+                          "max": round(float((us[:, 3] - us[:, 2]).max()), 2)}
+        row["critical_wg"] = {nm: round(float(us[crit, i]), 2) for i, nm in enumerate(TL_NAMES)
+                              if nm != "summed" or reducer[crit]}
+        row["cus"] = int(len(cu_end))
+        row["cu_loop_end"] = {q: round(float(np.percentile(cu_end, p)), 2) for q, p in
+                              (("min", 0), ("p10", 10), ("p50", 50), ("p90", 90), ("max", 100))}
+        row["loop_end_older_younger_p50"] = [round(float(np.median(us[older, 3])), 2),
+                                             round(float(np.median(us[~older, 3])), 2)]
+        row["xcc_loop_end_p50"] = [round(float(np.median(us[xcc == x, 3])), 2) for x in np.unique(xcc)]
+        out[name] = row
+        del g
+    print("| launch | WGs | launch us | " + " | ".join(f"{nm} p50 / max" for nm in TL_NAMES) + " | loop us p50 / max |")
+    print("|---|---|---|" + "---|" * (len(TL_NAMES) + 1))
+    for name, r in out.items():
+        cells = " | ".join(f"{r[nm]['p50']:.2f} / {r[nm]['max']:.2f}" for nm in TL_NAMES)
+        print(f"| {name} | {r['wgs']} | {r['launch_us']} | {cells} | {r['loop_us']['p50']:.2f} / {r['loop_us']['max']:.2f} |")
+    for name, r in out.items():
+        print(f"critical workgroup of {name}: " + ", ".join(f"{k} {v:.2f}" for k, v in r["critical_wg"].items()))
+        print(f"  {name}: loop end per CU ({r['cus']} CUs) {r['cu_loop_end']}; older / younger workgroups "
+              f"p50 {r['loop_end_older_younger_p50']}; per XCC p50 {r['xcc_loop_end_p50']}")
+    print(json.dumps({"timeline": out}), flush=True)
+    return 0
+
+
 def measured_traffic():
     """HBM bytes per GEMV launch of the configuration-1 step, from the committed rocprofv3 --pmc
     summary (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter on a copy of known size);
@@ -558,6 +764,9 @@ def main() -> int:
     ap.add_argument("--config3-only", action="store_true",
                     help="only the configuration-3 section (the GEMV at small M, the prefill GEMM split and "
                          "unsplit at M = 4-256; what its kernel-trace profile reads); prints its dict")
+    ap.add_argument("--timeline", action="store_true",
+                    help="only the per-workgroup phase timeline of each configuration-1 GEMV launch (loads the "
+                         "tracing library exl3rocm/libexl3_mi355x_timeline.so: build_ext.py --timeline)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the configuration-4 prefill chunk (what the prefill PMC passes read); prints its dict")
     args = ap.parse_args()
@@ -569,6 +778,9 @@ def main() -> int:
               "(see DESIGN.md for how the path would shard)", file=sys.stderr)
         return 2
 
+    if args.timeline:
+        os.environ["EXL3_MI355X_LIB"] = os.path.join(REPO, "qwen38-27b-exl3-rdna4_amd", "exl3rocm",
+                                                     "libexl3_mi355x_timeline.so")
     import torch
     from exl3rocm import _lib, ops  # noqa: F401
     _lib.lib()
@@ -578,6 +790,12 @@ def main() -> int:
     if args.prefill_only:
         print(json.dumps(prefill_chunk(torch)), flush=True)
         return 0
+    if args.timeline:
+        _, sets = build_layers(torch, bits, args.copies)
+        from exl3rocm import synth
+        x5120 = torch.from_numpy(synth.activations(synth.key_of("config1", "x", HIDDEN), 1, HIDDEN)).cuda()
+        x17408 = torch.from_numpy(synth.activations(synth.key_of("config1", "x", INTER), 1, INTER)).cuda()
+        return timeline(torch, sets, x5120, x17408)
     if args.config3_only:
         _, sets = build_layers(torch, bits, args.copies)
         print(json.dumps(small_batch(torch, sets)), flush=True)
@@ -603,6 +821,12 @@ def main() -> int:
                 "traffic_source": "profiles/gemv_traffic_config1.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE)",
                 "kernel": "gemv_kernel<4,2,0,0> (every M=1 launch of the step)",
                 "bytes_per_launch": step_bytes / lps, "mean_launch_us": round(avg_launch_us, 3)}
+    copy_gbs, read_gbs = device_copy_gbs(torch)
+    roofline["achievable_gbs"] = copy_gbs
+    roofline["frac_of_achievable"] = round(achieved / copy_gbs, 4)
+    roofline["achievable_source"] = "device copy of 1 GiB (torch copy_, read + write bytes), median of 30, HIP events"
+    roofline["achievable_read_gbs"] = read_gbs
+    roofline["frac_of_achievable_read"] = round(achieved / read_gbs, 4)
     weights = sum(k * n for _, k, n in LAYER)
     valu_floor_us = weights * VALU_OPS_PER_WEIGHT_4BPW / VALU_LANE_OPS_PER_S * 1e6
     roofline["valu_decode_roof"] = {
@@ -613,6 +837,14 @@ def main() -> int:
     extra = {"launches_per_step": lps, "step_bytes": step_bytes, "wall_s": round(wall, 3)}
     log("per-shape GEMV timing")
     extra["per_shape_m1"] = per_shape_gemv(torch, sets, x5120, x17408)
+    # the same step graphs again, now that the GPU has run decode work for a while: 400 steps after
+    # 40 warmup steps (a decode loop's clock; the timed region above follows ~1 s of idle set-up)
+    n_s = args.steps if graphs["rest"] is not None else max(1, 400 // graphs["block"]) * graphs["block"]
+    el_s, _ = time_graphs(torch, graphs, n_s, 40)
+    extra["headline_steady"] = {"steps": n_s, "warmup": 40, "gbs": round(n_s * step_bytes / el_s / 1e9, 1),
+                                "us_per_step": round(el_s * 1e6 / n_s, 2)}
+    log("reference checkpoint shapes (GEMV scoreboard, prefill)")
+    extra["checkpoint_shapes"] = checkpoint_shapes(torch)
     log("approximate mul1 GEMV (opt-in affine / int8 routes)")
     extra["approx_m1"] = approx_m1(torch, sets, x5120, x17408)
     log("gated MLP (gate/up, SiLU-and-mul, down) three ways")

@@ -149,7 +149,11 @@ def exl3_linear_groups(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[t
     own K / suh / svh; the concatenation happens inside this opaque op (reference ops.py:106-175).
 
     ptrs_* = int64 device tensors of per-group data pointers, given when all groups share K and
-    width: at M == 1 one grouped launch over the pointer tables computes every group."""
+    width (the reference's M == 1 exl3_mgemm route).  They are accepted and not read: the grouped
+    launch takes the same pointers as kernel arguments instead (exl3_gemv_mr_grouped, the same
+    kernel, split and output bitwise as exl3_mgemm over the tables), which saves every workgroup a
+    dependent load of its table entries before its first trellis request (~1.3 us of a 5120 ->
+    2 x 17408 launch)."""
     widths = [s.shape[0] for s in svh]
     if len(trellis) == 1:
         return exl3_linear(x, trellis[0], suh[0], svh[0], K[0], mcg, mul1)
@@ -166,10 +170,6 @@ def exl3_linear_groups(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[t
             _linear_into(x2, trellis[g], suh[g], svh[g], K[g], mcg, mul1, y[:, n0:n0 + widths[g]])
             n0 += widths[g]
         return y.view(*x.shape[:-1], n0)
-    if M == 1 and ptrs_trellis is not None and ng <= _lib.MAX_GROUPS:
-        y = torch.empty((ng, 1, widths[0]), dtype=torch.float16, device=x.device)
-        E.exl3_mgemm(x2.view(1, 1, k), ptrs_trellis, y, ptrs_suh, None, ptrs_svh, K[0], mcg, mul1)
-        return y.view(*x.shape[:-1], ng * widths[0])
     y = torch.empty((M, sum(widths)), dtype=torch.float16, device=x.device)
     if M <= MR_MAX:
         # runs of consecutive groups with equal K share one launch, each group written straight into
