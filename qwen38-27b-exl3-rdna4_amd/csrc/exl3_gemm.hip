@@ -678,9 +678,15 @@ __global__ void __launch_bounds__(PC::THREADS) gemm_pc_kernel(PcArgs a)
     // (had128_mfma16: the values of exl3_had_r_128_f32 with post), 16-byte stores ----------------
     const uint16_t* ct = reinterpret_cast<const uint16_t*>(lds);
     const int jr = t & 15, gq = (t >> 4) & 3;
+    // svh as device-scope (sc1) raw-buffer loads: a split tile's last piece reaches here after its
+    // counter atomic, and every load after a counter atomic carries sc1 (checked on the built code)
     u32x4 sv[4];
+    const __amdgpu_buffer_rsrc_t svs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(gg.svh), 0, 0x7FFFFFFF,
+                                                                         RAW_BUFFER_FLAGS);
 #pragma unroll
-    for (int p = 0; p < 4; ++p) sv[p] = *reinterpret_cast<gc_u32x4*>(as_global(gg.svh) + col0 + 32 * p + 8 * gq);
+    for (int p = 0; p < 4; ++p)
+        sv[p] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(svs, (uint32_t) ((col0 + 32 * p + 8 * gq) * 2),
+                                                                                0, SC1));
     // the tile's rows as one raw buffer from row row0 (offsets below 256 * ldy * 2 bytes); the
     // stores write through L2 (device scope), so the end-of-kernel writeback finds no dirty output
     const __amdgpu_buffer_rsrc_t ysrc = __builtin_amdgcn_make_buffer_rsrc(gg.y + (int64_t) row0 * a.ldy, 0, 0x7FFFFFFF,

@@ -284,7 +284,19 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     const __amdgpu_buffer_rsrc_t trsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(trel), 0, (int) (uint32_t) trel_bytes, RAW_BUFFER_FLAGS);
     gc_u16* const gsuh = as_global(suh);
-    gc_u16* const gsvh = as_global(svh);
+    // svh is read only after the completion counters, as device-scope (sc1) raw-buffer loads like
+    // the partial sums around it: every load after a counter atomic then carries sc1, which a check
+    // of the built code can require without telling the two apart
+    auto sc1_rsrc = [](const uint16_t* p) __attribute__((always_inline)) {
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p), 0, 0x7FFFFFFF, RAW_BUFFER_FLAGS);
+    };
+    auto sv32 = [](__amdgpu_buffer_rsrc_t r, int e) __attribute__((always_inline)) {
+        return (uint32_t) __builtin_amdgcn_raw_buffer_load_b32(r, (uint32_t) (2 * e), 0, SC1);
+    };
+    auto sv128 = [](__amdgpu_buffer_rsrc_t r, int e) __attribute__((always_inline)) {
+        return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t) (2 * e), 0, SC1));
+    };
+    const __amdgpu_buffer_rsrc_t svsrc = sc1_rsrc(svh);
     // the input rows: x (rotated here, per workgroup) or the group's pre-rotated rows
     const bool pre = MT_ != 0 && a.xr != nullptr;
     gc_u16* const gx = as_global(pre ? a.xr + (int64_t) grp * M * a.k : a.x);
@@ -772,21 +784,21 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                     // single row: pair r goes to wave r, two columns a lane
                     if (wave < rb) {
                         const int cb = seg0_cb + b0 + s_list[r0 + wave];
-                        sv_first.x = *reinterpret_cast<gc_u32*>(as_global(a.g[0].svh) + cb * 128 + 2 * lane);
-                        sv_first_u.x = *reinterpret_cast<gc_u32*>(as_global(a.g[1].svh) + cb * 128 + 2 * lane);
+                        sv_first.x = sv32(sc1_rsrc(a.g[0].svh), cb * 128 + 2 * lane);
+                        sv_first_u.x = sv32(sc1_rsrc(a.g[1].svh), cb * 128 + 2 * lane);
                     }
                 } else if (gated) {
                     if (rr < rb * M) {
                         const int cb = seg0_cb + b0 + s_list[r0 + rr / M];
-                        sv_first = *reinterpret_cast<gc_u32x4*>(as_global(a.g[0].svh) + cb * 128 + 8 * l16);
-                        sv_first_u = *reinterpret_cast<gc_u32x4*>(as_global(a.g[1].svh) + cb * 128 + 8 * l16);
+                        sv_first = sv128(sc1_rsrc(a.g[0].svh), cb * 128 + 8 * l16);
+                        sv_first_u = sv128(sc1_rsrc(a.g[1].svh), cb * 128 + 8 * l16);
                     }
                 } else if (MT_ == 0) {
                     // single row: block r of the pair goes to wave r, two columns a lane
                     if (wave < rb)
-                        sv_first.x = *reinterpret_cast<gc_u32*>(gsvh + (seg0_cb + b0 + s_list[r0 + wave]) * 128 + 2 * lane);
+                        sv_first.x = sv32(svsrc, (seg0_cb + b0 + s_list[r0 + wave]) * 128 + 2 * lane);
                 } else if (rr < rb * M) {
-                    sv_first = *reinterpret_cast<gc_u32x4*>(gsvh + (seg0_cb + b0 + s_list[r0 + rr / M]) * 128 + 8 * l16);
+                    sv_first = sv128(svsrc, (seg0_cb + b0 + s_list[r0 + rr / M]) * 128 + 8 * l16);
                 }
             }
             // contributor wf holds block cb in its segment cb - first_cb(wf); every later
@@ -794,6 +806,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
             // RED_BATCH and each sum runs in contributor order; the gated form sums two elements at
             // a time with both elements' loads in flight together (its passes hold twice the rows).
             const int total = rb * RM * 128;
+            // both groups' partial-slot geometry as scalars: a per-element choice between two
+            // argument fields would otherwise become a vector load from a per-lane argument address
+            const int ms0 = __builtin_amdgcn_readfirstlane(a.g[0].max_seg);
+            const int ms1 = __builtin_amdgcn_readfirstlane(a.g[1].max_seg);
+            const float* const pg0 = a.part + uniform_i64(a.g[0].part_off);
+            const float* const pg1 = a.part + uniform_i64(a.g[1].part_off);
             // element e of the pass: contributor 0's partial, contributor 1's (the rest follow
             // cstride floats apart), the contributor count and the element's LDS slot
             auto elem = [&](int e, const float*& p0, const float*& p1, int64_t& cstride, int& nc, int& lofs)
@@ -804,8 +822,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 // the group whose partials hold element el: this workgroup's, or gate / up rows
                 const bool up = gated && el >= M * 128;
                 if (up) el -= M * 128;
-                const int max_seg = !gated ? gg.max_seg : up ? a.g[1].max_seg : a.g[0].max_seg;
-                const float* pr = !gated ? part_grp : a.part + (up ? a.g[1].part_off : a.g[0].part_off);
+                const int max_seg = !gated ? gg.max_seg : up ? ms1 : ms0;
+                const float* pr = !gated ? part_grp : up ? pg1 : pg0;
                 const int wf = s_own[up ? 3 : 0][bi], seg_f = s_own[up ? 5 : 2][bi];
                 nc = s_own[up ? 4 : 1][bi];
                 cstride = (int64_t) max_seg * M * 128;
@@ -1030,8 +1048,8 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                     if (live) {
                         cg = *reinterpret_cast<const u32x4*>(lds_c + (r * RM + m) * A_ROW + 8 * l16);
                         cu = *reinterpret_cast<const u32x4*>(lds_c + (r * RM + M + m) * A_ROW + 8 * l16);
-                        svg = rr0 == 0 ? sv_first : *reinterpret_cast<gc_u32x4*>(as_global(a.g[0].svh) + cb * 128 + 8 * l16);
-                        svu = rr0 == 0 ? sv_first_u : *reinterpret_cast<gc_u32x4*>(as_global(a.g[1].svh) + cb * 128 + 8 * l16);
+                        svg = rr0 == 0 ? sv_first : sv128(sc1_rsrc(a.g[0].svh), cb * 128 + 8 * l16);
+                        svu = rr0 == 0 ? sv_first_u : sv128(sc1_rsrc(a.g[1].svh), cb * 128 + 8 * l16);
                     }
                     const u32x4 rg = had128_x8<double>(cg, u32x4{0u, 0u, 0u, 0u}, false, svg, true, r_scale<double>());
                     const u32x4 ru = had128_x8<double>(cu, u32x4{0u, 0u, 0u, 0u}, false, svu, true, r_scale<double>());
@@ -1074,7 +1092,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 u32x4 c = {0u, 0u, 0u, 0u}, sv = c;
                 if (live) {
                     c = *reinterpret_cast<const u32x4*>(lds_c + rr * A_ROW + 8 * l16);
-                    sv = rr0 == 0 ? sv_first : *reinterpret_cast<gc_u32x4*>(gsvh + cb * 128 + 8 * l16);
+                    sv = rr0 == 0 ? sv_first : sv128(svsrc, cb * 128 + 8 * l16);
                 }
                 const u32x4 res = had128_x8<double>(c, u32x4{0u, 0u, 0u, 0u}, false, sv, true, r_scale<double>());
                 if (live)
