@@ -575,13 +575,17 @@ def prefill_chunk(torch, layers=64, m=2048, bits=4, iters=2):
             "frac_mfma_fp16": round(tf / MFMA_FP16_PEAK_TFLOPS, 4), "flops_per_chunk": flops}
 
 
-def small_batch(torch, sets, ms=(1, 4, 8, 16, 32), gemm_ms=(4, 8, 16, 32, 33, 64, 128, 256), reps=32):
-    """Configuration 3: gate (5120 -> 17408) and down (17408 -> 5120) at M in {1, 4, 8, 16, 32}
-    through the op (the fused GEMV), heavy-tail activations; and the prefill GEMM (the route for
-    M > 32) at M from 4 to 256, for the GEMV -> GEMM crossover: the smallest M at which the GEMM is
-    faster than the GEMV, or "none below 33" (the op routes M <= 32 to the GEMV).  Mean duration
-    per call from a graph of `reps` calls over the weight copies (HIP events on the replay stream)."""
-    from exl3rocm import kernels as E, synth
+def small_batch(torch, sets, ms=(1, 2, 4, 8, 12, 16, 17, 20, 24, 28, 32, 33, 36, 40, 44, 48, 49, 56, 64, 65, 128, 256),
+                reps=32):
+    """Configuration 3: gate (5120 -> 17408), down (17408 -> 5120) and the grouped gate/up launch
+    (5120 -> 2 x 17408) at M from 1 to 256, heavy-tail activations.  Per M: the op (its route: the
+    fused GEMV up to the measured crossover b of the launch's shape, the prefill GEMM above), the
+    GEMV (<= 64 rows) and the prefill GEMM called directly, and the GEMM without a workspace (its
+    tiles unsplit, the plan's comparison) at M in {4, ..., 256}.  Also b, the step at the route
+    boundary op(b + 1) / op(b) - 1, the op's worst ratio to the faster route over M <= 64, and the
+    smallest M at which the GEMM beats the GEMV.  Mean duration per call from a graph of `reps`
+    calls over the weight copies (HIP events on the replay stream)."""
+    from exl3rocm import kernels as E, ops, synth, _lib
     res = {}
     s = torch.cuda.Stream()
 
@@ -605,29 +609,50 @@ def small_batch(torch, sets, ms=(1, 4, 8, 16, 32), gemm_ms=(4, 8, 16, 32, 33, 64
         del g
         return round(e0.elapsed_time(e1) * 1e3 / (3 * reps), 2)
 
-    for name in ("gate", "down"):
-        k = INTER if name == "down" else HIDDEN
+    for name, k, names in (("gate", HIDDEN, ("gate",)), ("down", INTER, ("down",)), ("gate_up", HIDDEN, ("gate", "up"))):
         n = HIDDEN if name == "down" else INTER
-        row = {}
+        ng = len(names)
+        b = ops.gemv_max_rows(k, ng * n)
+        m_all = sorted(set(ms) | {b, b + 1})
         xs = {m: torch.from_numpy(synth.activations(synth.key_of("cfg3", k, m), m, k, heavy_tail=True)).cuda()
-              for m in sorted(set(ms) | set(gemm_ms))}
-        for m in ms:
+              for m in m_all}
+        W = lambda ls, i: [ls.w[nm][i] for nm in names]
+        op_us, gemv_us, gemm_us, unsplit = {}, {}, {}, {}
+        for m in m_all:
             x = xs[m]
-            row[f"m{m}_us"] = graph_us(lambda ls, x=x: torch.ops.exl3rocm.linear(x, *ls.w[name], ls.bits, ls.mcg, ls.mul1))
-        gemm, unsplit = {}, {}
-        for m in gemm_ms:
-            x = xs[m]
-            y = torch.empty(m, n, dtype=torch.float16, device="cuda")
-            xh = torch.empty(m, k, dtype=torch.float16, device="cuda")
-            gemm[f"m{m}_us"] = graph_us(lambda ls, x=x, y=y, xh=xh: E.exl3_gemm_trellis_grouped(
-                x, [ls.w[name][0]], y, [ls.w[name][1]], xh, [ls.w[name][2]], ls.bits, ls.mcg, ls.mul1))
-            # the same GEMM without a workspace: its tiles unsplit (the plan's comparison)
-            unsplit[f"m{m}_us"] = graph_us(lambda ls, x=x, y=y, xh=xh: E.exl3_gemm_trellis(
-                x, ls.w[name][0], y, ls.w[name][1], xh, ls.w[name][2], ls.bits, ls.mcg, ls.mul1))
-        row["prefill_gemm"] = gemm
-        row["prefill_gemm_unsplit"] = unsplit
-        cross = [m for m in ms if m in gemm_ms and gemm[f"m{m}_us"] < row[f"m{m}_us"]]
-        row["gemm_faster_from_m"] = min(cross) if cross else "none below 33"
+            y = torch.empty(m, ng * n, dtype=torch.float16, device="cuda")
+            xh = torch.empty(ng, m, k, dtype=torch.float16, device="cuda")
+            ah = torch.empty(ng * m * k, dtype=torch.float16, device="cuda")
+            if ng == 1:
+                op_us[m] = graph_us(lambda ls, x=x: torch.ops.exl3rocm.linear(x, *ls.w[name], ls.bits, ls.mcg, ls.mul1))
+            else:
+                op_us[m] = graph_us(lambda ls, x=x: torch.ops.exl3rocm.linear_groups(
+                    x, W(ls, 0), W(ls, 1), W(ls, 2), [ls.bits] * ng, ls.mcg, ls.mul1))
+            if 1 < m <= _lib.GEMV_MAX_ROWS and ng == 1:
+                gemv_us[m] = graph_us(lambda ls, x=x, y=y, ah=ah: E.exl3_gemv_mr(
+                    x, ls.w[name][0], y, ls.w[name][1], ah, ls.w[name][2], ls.bits, ls.mcg, ls.mul1))
+            elif 1 < m <= _lib.GEMV_MAX_ROWS:
+                gemv_us[m] = graph_us(lambda ls, x=x, y=y, ah=ah: E.exl3_gemv_mr_grouped(
+                    x, W(ls, 0), y, W(ls, 1), ah, W(ls, 2), ls.bits, ls.mcg, ls.mul1, ng))
+            if m > 1:
+                gemm_us[m] = graph_us(lambda ls, x=x, y=y, xh=xh: E.exl3_gemm_trellis_grouped(
+                    x, W(ls, 0), y, W(ls, 1), xh, W(ls, 2), ls.bits, ls.mcg, ls.mul1))
+            if ng == 1 and m in (4, 8, 16, 32, 64, 128, 256):
+                unsplit[m] = graph_us(lambda ls, x=x, y=y, xh=xh: E.exl3_gemm_trellis(
+                    x, ls.w[name][0], y, ls.w[name][1], xh[0], ls.w[name][2], ls.bits, ls.mcg, ls.mul1))
+        cross = [m for m in gemv_us if gemm_us[m] < gemv_us[m]]
+        worst = max(op_us[m] / min(gemv_us[m], gemm_us[m]) for m in gemv_us)
+        row = {"launch": f"{k} -> {' + '.join([str(n)] * ng)}", "route_boundary": b,
+               "boundary_step": round(op_us[b + 1] / op_us[b] - 1, 4),
+               "boundary_note": "GEMV at b rows, GEMM at b + 1" if b < _lib.GEMV_MAX_ROWS else
+                                f"b = the GEMV's {_lib.GEMV_MAX_ROWS}-row maximum: the GEMM at b + 1 is the only route",
+               "op_over_faster_route_max": round(worst, 4),
+               "gemm_faster_from_m": min(cross) if cross else f"none up to {max(gemv_us)}",
+               "op_us": {f"m{m}": v for m, v in op_us.items()},
+               "gemv_us": {f"m{m}": v for m, v in gemv_us.items()},
+               "prefill_gemm_us": {f"m{m}": v for m, v in gemm_us.items()}}
+        if unsplit:
+            row["prefill_gemm_unsplit_us"] = {f"m{m}": v for m, v in unsplit.items()}
         res[name] = row
     return res
 

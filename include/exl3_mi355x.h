@@ -39,7 +39,8 @@ extern "C" {
 #define EXL3_ABI_VERSION 3       /* 2: exl3_gemv_f32, exl3_gemm_trellis_silu_in; 3: exl3_gemv_silu_prerot_rows,
                                     exl3_gemm_trellis_workspace_bound */
 #define EXL3_MAX_GROUPS 4       /* groups per grouped launch (reference EXL3_GEMV_MRG_MAX) */
-#define EXL3_GEMV_MAX_ROWS 32   /* rows handled by the fused GEMV */
+#define EXL3_GEMV_MAX_ROWS 64   /* rows the plain fused GEMV takes (exl3_gemv_mr and its grouped forms) */
+#define EXL3_GEMV_FUSED_MAX_ROWS 32 /* rows of the fused-epilogue forms (SiLU input, gated, approximate) */
 #define EXL3_GEMV_COUNTER_BYTES 262144 /* workspace head reserved for completion counters (one per 128-byte line) */
 #define EXL3_NOALLOC_SCRATCH_BYTES 17039360 /* 16.25 MiB: exl3_gemv_mr_noalloc's per-GPU device array */
 
@@ -95,7 +96,8 @@ size_t exl3_gemv_workspace_size(int m, int k, int n, int K, int groups);
 /* Eligibility of the fused multi-row GEMV.
  * Replaces `exl3_gemv_mr_supported(m, k, n, K, mcg, mul1)`
  * (reference vllm_plugin/patches/exl3-fork/0002-gemv-multirow.patch:334-338).  Unlike the
- * reference (mul1 only), every codebook is supported; 1 <= m <= 32, k and n multiples of 128. */
+ * reference (mul1 only), every codebook is supported; 1 <= m <= EXL3_GEMV_MAX_ROWS (64), k and n multiples
+ * of 128. */
 int exl3_gemv_mr_supported(int m, int k, int n, int K, int mcg, int mul1);
 
 /* M == 1 EXL3 linear, y = fp16(H(fp16(H(x*suh)) . W) * svh) with fused input and output
@@ -116,7 +118,7 @@ int exl3_gemv_f32(const void* x, int64_t ldx, const void* trellis, void* y, int6
                   const void* svh, int m, int k, int n, int K, int mcg, int mul1, void* workspace, size_t ws_bytes,
                   void* stream);
 
-/* 1 <= m <= 32 EXL3 linear, output rows with stride ldy.
+/* 1 <= m <= EXL3_GEMV_MAX_ROWS (64) EXL3 linear, output rows with stride ldy.
  * A_had: optional fp16 scratch of m * k elements (groups * m * k for the grouped forms).  When
  * given and m >= 8 (EXL3_GEMV_PREROT_M), the input is rotated once per group into it,
  * A_had = fp16(Had128(fp16(x * suh))) as in the reference, and the GEMV reads those rows; otherwise

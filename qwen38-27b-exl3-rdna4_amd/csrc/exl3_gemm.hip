@@ -940,7 +940,7 @@ int exl3_gemm(const void* x, int64_t ldx, const void* trellis, void* y, int64_t 
               void* stream)
 {
     if (m <= 0) return m == 0 ? 1 : EXL3_EINVAL;
-    if (m <= EXL3_GEMV_MAX_ROWS) {
+    if (m <= EXL3_GEMV_FUSED_MAX_ROWS) {
         const int rc = exl3_gemv_mr(x, ldx, trellis, y, ldy, suh, A_had, svh, m, k, n, K, mcg, mul1, workspace,
                                     ws_bytes, stream);
         return rc == EXL3_OK ? 1 : (rc > 0 ? EXL3_EINVAL : rc);

@@ -360,6 +360,8 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
                 const void* x_up = nullptr, bool f32out = false)
 {
     if (f32out && (m != 1 || gated || tabs || approx || x_up)) return EXL3_EINVAL;
+    // the fused-epilogue forms take up to EXL3_GEMV_FUSED_MAX_ROWS rows (16-row tiles 1 and 2 only)
+    if ((gated || x_up || approx) && m > EXL3_GEMV_FUSED_MAX_ROWS) return EXL3_DECLINED;
     if (x_up && (gated || tabs || approx || (((uintptr_t) x_up) & 15))) return EXL3_EINVAL;
     if (approx && (gated || approx > 2)) return EXL3_EINVAL;
     if (gated && (groups != 2 || tabs || widths[0] != widths[1] || ldy < widths[0])) return EXL3_EINVAL;

@@ -202,7 +202,7 @@ struct Split {
 
 // Two workgroups (8 waves) per CU are resident at once: up to 256 registers per lane, enough for
 // a ring deep enough that one wave alone keeps its SIMD busy.
-// MT: 16-row MFMA tiles of the input rows (0: exactly one row, a compile-time M).  FORM:
+// MT: 16-row MFMA tiles of the input rows (0: exactly one row, a compile-time M; 1 to 4).  FORM:
 //   FORM_PLAIN   the EXL3 linear of each group;
 //   FORM_GATED   groups 0 (gate) and 1 (up) of equal width; the workgroup completing a block of
 //                both writes fp16(fp16(silu(gate)) * up) to g[0].y instead of the two outputs;
@@ -1121,11 +1121,18 @@ int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t stream)
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 
+// 16-row MFMA tiles of the rows: one exact row, <= 16, <= 32, and for the plain faithful forms (the
+// only ones the host lets past EXL3_GEMV_FUSED_MAX_ROWS) <= 48 and <= 64
 template <int BITS, int CB, int FORM>
 int launch_gemv_m(const GemvArgs& a, int wgs, hipStream_t s)
 {
-    return a.M == 1 ? launch_gemv_t<BITS, CB, 0, FORM>(a, wgs, s)
-         : a.M <= 16 ? launch_gemv_t<BITS, CB, 1, FORM>(a, wgs, s) : launch_gemv_t<BITS, CB, 2, FORM>(a, wgs, s);
+    if (a.M == 1) return launch_gemv_t<BITS, CB, 0, FORM>(a, wgs, s);
+    if (a.M <= 16) return launch_gemv_t<BITS, CB, 1, FORM>(a, wgs, s);
+    if constexpr (FORM == FORM_PLAIN && CB <= 2) {
+        if (a.M > 48) return launch_gemv_t<BITS, CB, 4, FORM>(a, wgs, s);
+        if (a.M > 32) return launch_gemv_t<BITS, CB, 3, FORM>(a, wgs, s);
+    }
+    return launch_gemv_t<BITS, CB, 2, FORM>(a, wgs, s);
 }
 
 template <int BITS, int FORM>

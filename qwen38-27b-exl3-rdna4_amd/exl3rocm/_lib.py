@@ -13,7 +13,8 @@ LIB_PATH = os.environ.get("EXL3_MI355X_LIB", os.path.join(HERE, "libexl3_mi355x.
 
 OK, DECLINED, EINVAL, ELAUNCH, EWORKSPACE = 0, 1, -1, -2, -3
 MAX_GROUPS = 4
-GEMV_MAX_ROWS = 32
+GEMV_MAX_ROWS = 64
+GEMV_FUSED_MAX_ROWS = 32
 NOALLOC_SCRATCH_BYTES = 17039360
 ABI_VERSION = 3
 

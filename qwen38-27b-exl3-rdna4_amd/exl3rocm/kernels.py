@@ -463,8 +463,8 @@ def exl3_gemm(A, B, C, suh, A_had, svh, force_shape_idx: int = -1, mcg: bool = F
     x2, m, k = _rows(A)
     n = svh.shape[0]
     K = _bits_of(B)
-    ws = workspace(A.device, gemv_workspace_bytes(min(max(m, 1), L.GEMV_MAX_ROWS), k, n, K)) \
-        if m <= L.GEMV_MAX_ROWS else None
+    ws = workspace(A.device, gemv_workspace_bytes(min(max(m, 1), L.GEMV_FUSED_MAX_ROWS), k, n, K)) \
+        if m <= L.GEMV_FUSED_MAX_ROWS else None
     return L.check(L.lib().exl3_gemm(x2.data_ptr(), x2.stride(0) if m > 1 else k, B.data_ptr(), C.data_ptr(),
                                      _ldy(C, n), suh.data_ptr(), A_had.data_ptr(), svh.data_ptr(), m, k, n, K,
                                      *_cb_flags(mcg, mul1), ws.data_ptr() if ws is not None else None,

@@ -4,13 +4,14 @@ each call as one node.  Same op names, schemas and routing contract as the refer
 ops (vllm_plugin/exl3rocm/ops.py:65-180); kernels come from libexl3_mi355x.so.
 
 One call computes one checkpoint tensor ("group"): y = had(had(x * suh) @ W_inner) * svh.
-Routing by rows M:
-  M <= EXL3_MR_MAX (32)  -> fused GEMV (input Hadamard, trellis decode + MFMA dot, split-K
+Routing by rows M, per launch (gemv_rows: the measured GEMV / GEMM crossover of the launch's shape,
+or EXL3_MR_MAX rows for every shape when set):
+  M <= the crossover     -> fused GEMV (input Hadamard, trellis decode + MFMA dot, split-K
                             reduction and output Hadamard in one launch); every row is bitwise
                             equal to the M == 1 call of that row; EXL3_GEMV_APPROX=affine|int8
                             selects the opt-in approximate mul1 forms (unrounded weights, or
                             int8 activations as the reference's EXL3_ROCM_GFX1201_INT8 path)
-  M  > EXL3_MR_MAX       -> input Hadamard pass, then the prefill GEMM (trellis decoded into LDS,
+  otherwise              -> input Hadamard pass, then the prefill GEMM (trellis decoded into LDS,
                             fp16 MFMA, fp32 accumulate, output Hadamard and svh in its epilogue);
                             a fused module's groups share one GEMM launch; EXL3_PREFILL=recon takes
                             the reference's reconstruct + hgemm route instead
@@ -25,11 +26,54 @@ import torch
 from . import _lib
 from . import kernels as E
 
-MR_MAX = min(int(os.environ.get("EXL3_MR_MAX", str(_lib.GEMV_MAX_ROWS))), _lib.GEMV_MAX_ROWS)
+def _env_rows(name: str) -> Optional[int]:
+    v = os.environ.get(name)
+    return None if v is None or not v.strip() else min(int(v), _lib.GEMV_MAX_ROWS)
+
+
+# EXL3_MR_MAX (the reference's knob) fixes the GEMV / prefill boundary for every launch; unset, each
+# launch takes the measured crossover of its shape from GEMV_CROSSOVER (shapes outside it: DEFAULT_MR)
+MR_MAX: Optional[int] = _env_rows("EXL3_MR_MAX")
+DEFAULT_MR = 32
+# Largest row count at which the fused GEMV beats the prefill GEMM, by (k, output columns of the
+# launch: all its groups).  Measured on MI355X for the launches a Qwen3.5-27B checkpoint makes (q/k/v
+# and gate/up grouped as linear_groups groups them, and lm_head): both routes at every M from 2 to
+# 48 (to 64 where the GEMV still led at 48), graphs of 24 launches over 8 weight copies, 4 bpw, and
+# 2 / 3 bpw where a checkpoint holds them (the boundary moved by <= 6 rows).  Each entry is the
+# boundary b that minimises the summed time over M with no step above 5 % from the GEMV at b rows
+# to the GEMM at b + 1.  The GEMM's cost is flat within each 16-row MFMA tile and the GEMV's grows
+# ~0.75 us a row (its split-K reduction), so the GEMM wins early where its 128-column tiles fill
+# the chip (5120 - 7168 columns: b = 8) and late where they do not (2 x 17408 columns: at 64 rows
+# the GEMV takes 100.5 us, the GEMM 102.6; lm_head: 484 against 553, the GEMV's row limit).
+GEMV_CROSSOVER = {
+    (5120, 1024): 24, (5120, 2048): 21, (5120, 5120): 8, (5120, 6144): 8, (5120, 7168): 8,
+    (5120, 10240): 20, (5120, 12288): 30, (5120, 14336): 17, (5120, 16384): 28, (5120, 17408): 40,
+    (5120, 34816): 64, (5120, 248320): 64, (6144, 5120): 25, (17408, 5120): 30,
+}
+
+
+def gemv_max_rows(k: int, width: int) -> int:
+    """Most rows a launch of k inputs and `width` output columns takes on the fused GEMV."""
+    if MR_MAX is not None:
+        return MR_MAX
+    return min(GEMV_CROSSOVER.get((k, width), DEFAULT_MR), _lib.GEMV_MAX_ROWS)
+
+
+def gemv_rows(m: int, k: int, width: int) -> bool:
+    """Route of an m-row launch: the fused GEMV (True; every row bitwise equal to its m = 1 call)
+    or the prefill GEMM."""
+    return m <= gemv_max_rows(k, width)
+
+
+def fused_rows(m: int, k: int, width: int) -> bool:
+    """The GEMV route for the fused-epilogue forms (SiLU input, gated, approximate): <= 32 rows."""
+    return m <= min(gemv_max_rows(k, width), _lib.GEMV_FUSED_MAX_ROWS)
+
+
 # widest non-lm_head layer (17408): the shared reconstruction buffer of the `recon` prefill route
 RECON_SLICE_N = int(os.environ.get("EXL3_RECON_SLICE_N", "17408"))
 PREFILL_ROUTE = os.environ.get("EXL3_PREFILL", "fused")
-# linear_silu_mul at M <= MR_MAX: "unfused" (grouped GEMV + elementwise kernel) or "fused" (one
+# linear_silu_mul on the GEMV route: "unfused" (grouped GEMV + elementwise kernel) or "fused" (one
 # gated GEMV launch)
 GATED_ROUTE = os.environ.get("EXL3_GATED", "unfused")
 def approx_mode(value: Optional[str]) -> str:
@@ -46,7 +90,7 @@ def approx_mode(value: Optional[str]) -> str:
     return v
 
 
-# opt-in approximate mul1 GEMV for M <= MR_MAX
+# opt-in approximate mul1 GEMV, in place of the faithful one where fused_rows holds
 GEMV_APPROX = approx_mode(os.environ.get("EXL3_GEMV_APPROX"))
 
 _wbuf: dict = {}
@@ -71,10 +115,13 @@ def _weight_buffer(device, numel):
     return _wbuf[torch.device(device)][:numel]
 
 
-def reserve_workspace(device, k: int, n: int, K: int, groups: int = 1, m: int = MR_MAX):
-    """Reserve the GEMV workspace for up to m rows (load time): the current stream gets it now, and
+def reserve_workspace(device, k: int, n: int, K: int, groups: int = 1, m: Optional[int] = None):
+    """Reserve the GEMV workspace for up to m rows (load time; default: the most rows gemv_rows
+    sends to the GEMV for a module of groups x n columns): the current stream gets it now, and
     every other stream gets at least this much on its first eager call (so a later graph capture on
     that stream never allocates)."""
+    if m is None:
+        m = gemv_max_rows(k, n * groups)
     if m < 1:
         return
     E.workspace(torch.device(device), E.gemv_workspace_bytes(min(m, _lib.GEMV_MAX_ROWS), k, n, K, groups),
@@ -91,15 +138,18 @@ def _prep(x: torch.Tensor):
     return x2, k
 
 
-def _linear_into(x2, trellis, suh, svh, K, mcg, mul1, y):
-    """One group into y ([M, n] view, unit column stride, any row stride)."""
+def _linear_into(x2, trellis, suh, svh, K, mcg, mul1, y, gemv: Optional[bool] = None):
+    """One group into y ([M, n] view, unit column stride, any row stride); gemv: the route chosen
+    by the caller for the launch this group belongs to (None: by this group's own shape)."""
     M, k = x2.shape
     n = svh.shape[0]
-    if M <= MR_MAX and GEMV_APPROX and mul1:
+    if gemv is None:
+        gemv = gemv_rows(M, k, n)
+    if gemv and GEMV_APPROX and mul1 and M <= _lib.GEMV_FUSED_MAX_ROWS:
         rc = E.exl3_gemv_mr_approx(x2, trellis, y, suh, None, svh, K, GEMV_APPROX)
         if rc != 0:
             raise RuntimeError(f"exl3rocm: approximate GEMV declined shape m={M} k={k} n={n} K={K}")
-    elif M <= MR_MAX:
+    elif gemv:
         rc = E.exl3_gemv_mr(x2, trellis, y, suh, None, svh, K, mcg, mul1)
         if rc != 0:
             raise RuntimeError(f"exl3rocm: GEMV declined shape m={M} k={k} n={n} K={K}")
@@ -162,51 +212,37 @@ def exl3_linear_groups(x: torch.Tensor, trellis: list[torch.Tensor], suh: list[t
     ng = len(trellis)
     if M == 0:                                        # every route: an empty batch launches nothing
         return x2.new_empty((*x.shape[:-1], sum(widths)), dtype=torch.float16)
-    if M <= MR_MAX and GEMV_APPROX and mul1:
-        # the approximate route runs each group as its own launch
-        y = torch.empty((M, sum(widths)), dtype=torch.float16, device=x.device)
-        n0 = 0
-        for g in range(ng):
-            _linear_into(x2, trellis[g], suh[g], svh[g], K[g], mcg, mul1, y[:, n0:n0 + widths[g]])
-            n0 += widths[g]
-        return y.view(*x.shape[:-1], n0)
     y = torch.empty((M, sum(widths)), dtype=torch.float16, device=x.device)
-    if M <= MR_MAX:
-        # runs of consecutive groups with equal K share one launch, each group written straight into
-        # its row-strided column slice: equal widths (gate/up, k/v) through the reference's grouped
-        # entry point, mixed widths (q/k/v) through the widths form
-        i, n0 = 0, 0
-        while i < ng:
-            j = i + 1
-            while j < ng and j - i < _lib.MAX_GROUPS and K[j] == K[i]:
-                j += 1
-            if j - i > 1 and all(w == widths[i] for w in widths[i:j]):
-                E.exl3_gemv_mr_grouped(x2, list(trellis[i:j]), y[:, n0:], list(suh[i:j]), None, list(svh[i:j]),
-                                       K[i], mcg, mul1, j - i)
-            elif j - i > 1:
-                E.exl3_gemv_mr_grouped_widths(x2, list(trellis[i:j]), y[:, n0:], list(suh[i:j]), list(svh[i:j]),
-                                              K[i], mcg, mul1)
-            else:
-                _linear_into(x2, trellis[i], suh[i], svh[i], K[i], mcg, mul1, y[:, n0:n0 + widths[i]])
-            n0 += sum(widths[i:j])
-            i = j
-        return y.view(*x.shape[:-1], n0)
-    # prefill: runs of consecutive groups with equal K share one GEMM launch (each group its own
-    # rotated input); the recon route keeps the reference's one-group-at-a-time path
+    # runs of consecutive groups with equal K share one launch, each group written straight into
+    # its row-strided column slice; each run takes the route of its own shape
     i, n0 = 0, 0
     while i < ng:
         j = i + 1
         while j < ng and j - i < _lib.MAX_GROUPS and K[j] == K[i]:
             j += 1
-        if j - i > 1 and PREFILL_ROUTE != "recon":
+        w = sum(widths[i:j])
+        gemv = gemv_rows(M, k, w)
+        if j == i + 1 or (gemv and GEMV_APPROX and mul1 and M <= _lib.GEMV_FUSED_MAX_ROWS) or \
+                (not gemv and PREFILL_ROUTE == "recon"):
+            # one group, the approximate GEMV or the recon prefill: each group its own launch
+            c = n0
+            for g in range(i, j):
+                _linear_into(x2, trellis[g], suh[g], svh[g], K[g], mcg, mul1, y[:, c:c + widths[g]], gemv)
+                c += widths[g]
+        elif gemv and all(wd == widths[i] for wd in widths[i:j]):
+            # equal widths (gate/up, k/v): the reference's grouped entry point
+            E.exl3_gemv_mr_grouped(x2, list(trellis[i:j]), y[:, n0:], list(suh[i:j]), None, list(svh[i:j]),
+                                   K[i], mcg, mul1, j - i)
+        elif gemv:
+            # mixed widths (q/k/v)
+            E.exl3_gemv_mr_grouped_widths(x2, list(trellis[i:j]), y[:, n0:], list(suh[i:j]), list(svh[i:j]),
+                                          K[i], mcg, mul1)
+        else:
+            # one grouped prefill GEMM launch, each group its own rotated input
             xh = torch.empty((j - i, M, k), dtype=torch.float16, device=x.device)
             E.exl3_gemm_trellis_grouped(x2, list(trellis[i:j]), y[:, n0:], list(suh[i:j]), xh, list(svh[i:j]),
                                         K[i], mcg, mul1)
-        else:
-            for g in range(i, j):
-                _linear_into(x2, trellis[g], suh[g], svh[g], K[g], mcg, mul1, y[:, n0 + sum(widths[i:g]):
-                                                                               n0 + sum(widths[i:g + 1])])
-        n0 += sum(widths[i:j])
+        n0 += w
         i = j
     return y.view(*x.shape[:-1], n0)
 
@@ -225,7 +261,7 @@ def exl3_linear_silu_mul(x: torch.Tensor, trellis: list[torch.Tensor], suh: list
     a separate SiluAndMul (the fusion is proposed in reference docs/EFFICIENCY_INVESTIGATION.md:36-66).
 
     Routes: linear_groups, then an elementwise SiLU-and-mul kernel (the default: measured faster
-    on MI355X); or, with EXL3_GATED=fused and M <= EXL3_MR_MAX, equal K and width, one GEMV launch
+    on MI355X); or, with EXL3_GATED=fused on the GEMV route (<= 32 rows), equal K and width, one GEMV launch
     whose workgroup completing a 128-column block of both groups applies the activation.  Both
     routes give bitwise the same result."""
     if not (len(trellis) == 2 and len(suh) == 2 and len(svh) == 2 and len(K) == 2):
@@ -238,7 +274,7 @@ def exl3_linear_silu_mul(x: torch.Tensor, trellis: list[torch.Tensor], suh: list
     act = torch.empty((M, n), dtype=torch.float16, device=x.device)
     if M == 0:
         return act.view(*x.shape[:-1], n)
-    if GATED_ROUTE == "fused" and M <= MR_MAX and K[0] == K[1]:
+    if GATED_ROUTE == "fused" and K[0] == K[1] and fused_rows(M, k, 2 * n):
         E.exl3_gemv_silu_mul(x2, list(trellis), act, list(suh), list(svh), K[0], mcg, mul1)
     else:
         gu = exl3_linear_groups(x2, trellis, suh, svh, K, mcg, mul1)
@@ -259,8 +295,8 @@ def exl3_silu_mul_linear(gu: torch.Tensor, trellis: torch.Tensor, suh: torch.Ten
     counterpart in the reference plugin, whose MLP runs a separate SiluAndMul before the down
     linear (the fusion is proposed in reference docs/EFFICIENCY_INVESTIGATION.md:36-66).
 
-    At M <= EXL3_MR_MAX one GEMV launch forms act from gate and up as its input rows load; above
-    it the prefill's input transform forms act as it loads the rows (one transform launch and one
+    On the GEMV route (<= 32 rows) one GEMV launch forms act from gate and up as its input rows
+    load; on the prefill route the prefill's input transform forms act as it loads the rows (one transform launch and one
     GEMM launch, no act in memory); on the approximate GEMV routes and the recon prefill route the
     elementwise kernel writes act and linear runs on it.  Every route equals silu_mul followed by
     linear, bitwise."""
@@ -274,11 +310,11 @@ def exl3_silu_mul_linear(gu: torch.Tensor, trellis: torch.Tensor, suh: torch.Ten
     y = torch.empty((M, n), dtype=torch.float16, device=gu.device)
     if M == 0:
         return y.view(*gu.shape[:-1], n)
-    if M <= MR_MAX and not (GEMV_APPROX and mul1):
+    if fused_rows(M, k, n) and not (GEMV_APPROX and mul1):
         rc = E.exl3_gemv_silu_in(g2[:, :k], g2[:, k:], trellis, y, suh, None, svh, K, mcg, mul1)
         if rc != 0:
             raise RuntimeError(f"exl3rocm: GEMV declined shape m={M} k={k} n={n} K={K}")
-    elif M > MR_MAX and PREFILL_ROUTE != "recon":
+    elif not gemv_rows(M, k, n) and PREFILL_ROUTE != "recon":
         xh = torch.empty((M, k), dtype=torch.float16, device=gu.device)
         E.exl3_gemm_trellis_silu_in(g2[:, :k], g2[:, k:], trellis, y, suh, xh, svh, K, mcg, mul1)
     else:

@@ -54,7 +54,8 @@ def test_workspace_sizes():
     ws16 = L.exl3_gemv_workspace_size(16, 5120, 5120, 4, 1)
     ws2g = L.exl3_gemv_workspace_size(1, 5120, 5120, 4, 2)
     assert ws1 >= 65536 + 512 * 2 * 128 * 4 and ws16 > ws1 and ws2g >= ws1
-    assert L.exl3_gemv_workspace_size(33, 5120, 5120, 4, 1) == 0        # beyond the GEMV row limit
+    assert L.exl3_gemv_workspace_size(64, 5120, 5120, 4, 1) > 0          # the 64-row plain GEMV
+    assert L.exl3_gemv_workspace_size(65, 5120, 5120, 4, 1) == 0        # beyond the GEMV row limit
     assert L.exl3_gemv_workspace_size(1, 5000, 5120, 4, 1) == 0         # k not a multiple of 128
 
 
@@ -77,7 +78,8 @@ def test_mr_supported_predicate():
     L = _lib.lib()
     assert L.exl3_gemv_mr_supported(1, 5120, 5120, 4, 0, 1) == 1
     assert L.exl3_gemv_mr_supported(32, 5120, 1024, 8, 1, 0) == 1
-    assert L.exl3_gemv_mr_supported(33, 5120, 1024, 8, 1, 0) == 0
+    assert L.exl3_gemv_mr_supported(64, 5120, 1024, 8, 1, 0) == 1
+    assert L.exl3_gemv_mr_supported(65, 5120, 1024, 8, 1, 0) == 0
     assert L.exl3_gemv_mr_supported(4, 5120, 1000, 4, 0, 1) == 0
     assert L.exl3_gemv_mr_supported(4, 5120, 1024, 9, 0, 1) == 0
 
@@ -96,7 +98,7 @@ def test_invalid_arguments_return_before_any_launch():
                            None) == _lib.DECLINED
     assert L.exl3_gemv_f32(dummy, 128, dummy, None, 128, dummy, None, dummy, 1, 128, 128, 4, 0, 1, dummy, 1 << 20,
                            None) == _lib.EINVAL
-    assert L.exl3_gemv_mr(dummy, 128, dummy, dummy, 128, dummy, None, dummy, 40, 128, 128, 4, 0, 1, dummy, 1 << 20,
+    assert L.exl3_gemv_mr(dummy, 128, dummy, dummy, 128, dummy, None, dummy, 65, 128, 128, 4, 0, 1, dummy, 1 << 20,
                           None) == _lib.DECLINED
     assert L.exl3_gemv_mr(dummy, 128, dummy, dummy, 128, dummy, None, dummy, 1, 128, 128, 4, 0, 1, dummy, 0,
                           None) == _lib.EWORKSPACE

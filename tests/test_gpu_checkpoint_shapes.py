@@ -32,7 +32,7 @@ import pytest
 import torch
 
 import cpu
-from exl3rocm import _lib, kernels as E, synth
+from exl3rocm import _lib, kernels as E, ops, synth
 from test_gpu_parity import DEV, assert_close, to_dev
 
 pytestmark = [pytest.mark.gpu,
@@ -83,7 +83,8 @@ def assert_m1(got, ref, svh, what):
 
 
 @pytest.mark.parametrize("k,n,bits", CKPT_GEMV)
-def test_checkpoint_gemv_rows_and_oracle(k, n, bits):
+def test_checkpoint_gemv_rows_and_oracle(k, n, bits, monkeypatch):
+    monkeypatch.setattr(ops, "MR_MAX", 32)             # the GEMV route up to 32 rows on every shape
     tr, su, sv = synth.layer("ckpt", f"{k}x{n}x{bits}", k, n, bits)
     x = synth.activations(synth.key_of("ckpt", f"{k}x{n}x{bits}", "x"), 32, k)
     X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)

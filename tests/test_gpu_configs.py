@@ -147,9 +147,10 @@ def test_small_m_prefill_splits_every_tile(name, m, k, n):
 
 # ---------------------------------------------------------------------------------- config 3
 @pytest.mark.parametrize("k,n", [(5120, 17408), (17408, 5120)])
-def test_config3_heavy_tail_m16_m32(k, n):
-    """M = 16 and 32 (pre-rotated input) with heavy-tail x at 4 bpw: oracle, and every row ==
-    its M = 1 call bitwise."""
+def test_config3_heavy_tail_m16_m32(k, n, monkeypatch):
+    """M = 16 and 32 (pre-rotated input) with heavy-tail x at 4 bpw on the GEMV route: oracle, and
+    every row == its M = 1 call bitwise."""
+    monkeypatch.setattr(ops, "MR_MAX", 32)
     bits = 4
     tr, su, sv = synth.layer("cfg3", f"{k}x{n}", k, n, bits)
     x = synth.activations(synth.key_of("cfg3", f"{k}x{n}", "x"), 32, k, heavy_tail=True)
@@ -299,3 +300,79 @@ def test_layer_loaded_from_a_checkpoint_file_vs_oracle(tmp_path):
     torch.cuda.synchronize()
     assert_close(y1.cpu().numpy(), ref[:1], "file M=1", strict=True)
     assert_close(y40.cpu().numpy(), ref, "file M=40")
+
+
+# ---------------------------------------------------------------------------------------------- 64 rows
+@pytest.mark.parametrize("k,n,bits,cb", [(5120, 17408, 4, 2), (17408, 5120, 3, 2), (2048, 1024, 5, 1)])
+def test_gemv_64_rows_bitwise_rows_and_oracle(k, n, bits, cb):
+    """The plain GEMV's third and fourth 16-row tiles (33 to 64 rows): every row of an m-row call
+    is bitwise equal to its M = 1 call, and the rows match the oracle."""
+    tr, su, sv = synth.layer("rows48", f"{k}x{n}x{bits}", k, n, bits)
+    x = synth.activations(synth.key_of("rows48", f"{k}x{n}x{bits}", "x"), 64, k, heavy_tail=True)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    print(f"64-row GEMV k={k} n={n} bits={bits} cb={cb}", flush=True)
+    rows1 = torch.empty(64, n, dtype=torch.float16, device=DEV)
+    for r in range(64):
+        assert E.exl3_gemv_mr(X[r:r + 1], T, rows1[r:r + 1], SU, None, SV, bits, cb == 1, cb == 2) == 0
+    for m in (33, 40, 47, 48, 49, 57, 63, 64):
+        assert E.exl3_gemv_mr_supported(m, k, n, bits, cb == 1, cb == 2)
+        ym = torch.full((m, n), float("nan"), dtype=torch.float16, device=DEV)
+        assert E.exl3_gemv_mr(X[:m], T, ym, SU, None, SV, bits, cb == 1, cb == 2) == 0
+        assert torch.equal(ym.view(torch.int16), rows1[:m].view(torch.int16)), m
+    torch.cuda.synchronize()
+    assert_close(rows1.cpu().numpy(), cpu.linear(x, tr, bits, su, sv, cb), (k, n, bits, cb))
+    assert not E.exl3_gemv_mr_supported(65, k, n, bits, cb == 1, cb == 2)
+
+
+def test_fused_forms_decline_above_32_rows():
+    """The fused-epilogue GEMV forms take at most 32 rows: 33 declines without writing."""
+    k, n, bits = 1024, 512, 4
+    tr, su, sv = synth.layer("fused33", 0, k, n, bits)
+    X, T, SU, SV = to_dev(synth.activations(synth.key_of("fused33", "x"), 33, k), tr.view(np.int16), su, sv)
+    y = torch.full((33, n), 7.0, dtype=torch.float16, device=DEV)
+    assert E.exl3_gemv_mr_approx(X, T, y, SU, None, SV, bits, "affine") == 1
+    gu = torch.randn(33, 2 * k, device=DEV, dtype=torch.float16)
+    assert E.exl3_gemv_silu_in(gu[:, :k], gu[:, k:], T, y, SU, None, SV, bits, False, True) == 1
+    torch.cuda.synchronize()
+    assert bool((y == 7.0).all())
+
+
+# ---------------------------------------------------------------------------------- route boundary
+ROUTE_CASES = [(6144, (5120,), 4), (5120, (17408,), 4), (5120, (17408, 17408), 4), (5120, (5120, 1024, 1024), 4)]
+
+
+@pytest.mark.parametrize("k,widths,bits", ROUTE_CASES)
+def test_routing_follows_the_measured_crossover(k, widths, bits):
+    """linear / linear_groups at the measured crossover b of the launch's shape and at b + 1: the
+    (grouped) GEMV launch at b rows and the grouped prefill GEMM at b + 1, bitwise; the first and
+    last rows of both against the oracle."""
+    b = ops.gemv_max_rows(k, sum(widths))
+    assert ops.MR_MAX is None and b == ops.GEMV_CROSSOVER[(k, sum(widths))]
+    g = len(widths)
+    tag = f"route{k}x{'-'.join(map(str, widths))}"
+    mats = [synth.layer(tag, i, k, n, bits) for i, n in enumerate(widths)]
+    x = synth.activations(synth.key_of(tag, "x"), b + 1, k)
+    X = to_dev(x)[0]
+    Ts = [to_dev(t.view(np.int16))[0] for t, _, _ in mats]
+    SUs = [to_dev(s)[0] for _, s, _ in mats]
+    SVs = [to_dev(s)[0] for _, _, s in mats]
+    print(f"route boundary k={k} widths={widths} b={b}", flush=True)
+    for m, gemv in ((b, True), (b + 1, False)):
+        Xm = X[:m].contiguous()
+        got = (torch.ops.exl3rocm.linear(Xm, Ts[0], SUs[0], SVs[0], bits, False, True) if g == 1 else
+               torch.ops.exl3rocm.linear_groups(Xm, Ts, SUs, SVs, [bits] * g, False, True))
+        want = torch.empty_like(got)
+        if not gemv:
+            xh = torch.empty(g, m, k, dtype=torch.float16, device=DEV)
+            E.exl3_gemm_trellis_grouped(Xm, Ts, want, SUs, xh, SVs, bits, False, True)
+        elif g == 1:
+            assert E.exl3_gemv_mr(Xm, Ts[0], want, SUs[0], None, SVs[0], bits, False, True) == 0
+        elif len(set(widths)) == 1:
+            assert E.exl3_gemv_mr_grouped(Xm, Ts, want, SUs, None, SVs, bits, False, True, g) == 0
+        else:
+            assert E.exl3_gemv_mr_grouped_widths(Xm, Ts, want, SUs, SVs, bits, False, True) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), (m, gemv)
+        rows = [0, m - 1]
+        ref = np.concatenate([cpu.linear(x[rows], t, bits, s, v, 2) for t, s, v in mats], axis=1)
+        assert_close(got[rows].cpu().numpy(), ref, (k, widths, m))

@@ -236,7 +236,8 @@ def test_gemv_heavy_tail_parity():
 
 
 @pytest.mark.parametrize("k,n,bits", [(5120, 5120, 4), (17408, 5120, 3), (5120, 1024, 5)])
-def test_rows_bitwise_equal_to_m1(k, n, bits):
+def test_rows_bitwise_equal_to_m1(k, n, bits, monkeypatch):
+    monkeypatch.setattr(ops, "MR_MAX", 32)             # the GEMV route up to 32 rows on every shape
     x, tr, su, sv = layer(k, n, bits, m=32)
     X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
     rows1 = torch.cat([torch.ops.exl3rocm.linear(X[r:r + 1], T, SU, SV, bits, False, True) for r in range(32)])

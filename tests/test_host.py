@@ -301,3 +301,59 @@ def test_empty_batch_launches_nothing_on_every_route(monkeypatch, mode):
     assert tuple(y.shape) == (0, 256) and y.dtype == torch.float16
     y3 = torch.ops.exl3rocm.linear_groups(x.view(1, 0, 256), tr, s, v, [4, 4], False, True)
     assert tuple(y3.shape) == (1, 0, 256)
+
+
+# ---------------------------------------------------------------------------------- GEMV / GEMM route
+def test_route_boundary_table_and_override(monkeypatch):
+    """Each launch shape in the measured table routes its own boundary b to the GEMV and b + 1 to
+    the prefill GEMM; the fused-epilogue forms stop at 32 rows; shapes outside the table take
+    DEFAULT_MR; EXL3_MR_MAX fixes one boundary for every shape, capped at the GEMV's 48 rows."""
+    from exl3rocm import _lib
+    monkeypatch.setattr(ops, "MR_MAX", None)
+    for (k, w), b in ops.GEMV_CROSSOVER.items():
+        assert 1 <= b <= _lib.GEMV_MAX_ROWS
+        assert ops.gemv_rows(b, k, w) and not ops.gemv_rows(b + 1, k, w)
+        assert ops.fused_rows(min(b, 32), k, w) and not ops.fused_rows(33, k, w)
+    assert ops.gemv_max_rows(512, 512) == ops.DEFAULT_MR
+    monkeypatch.setattr(ops, "MR_MAX", 16)
+    assert ops.gemv_max_rows(5120, 34816) == 16 and ops.gemv_max_rows(512, 512) == 16
+    monkeypatch.setenv("EXL3_MR_MAX", "64")
+    assert ops._env_rows("EXL3_MR_MAX") == _lib.GEMV_MAX_ROWS
+    monkeypatch.setenv("EXL3_MR_MAX", " ")
+    assert ops._env_rows("EXL3_MR_MAX") is None
+
+
+class _Launches:
+    """Stands in for the kernels module: records each launch linear_groups makes (no GPU)."""
+
+    def __init__(self):
+        self.calls = []
+
+    def __getattr__(self, name):
+        def launch(*args, **kw):
+            svh = args[5] if name.startswith("exl3_gemm_trellis") else \
+                args[4] if name == "exl3_gemv_mr_grouped_widths" else args[5]
+            self.calls.append((name, [int(s.shape[0]) for s in svh] if isinstance(svh, list) else [int(svh.shape[0])]))
+            return 0
+        return launch
+
+
+@pytest.mark.parametrize("m,expect", [
+    (20, [("exl3_gemv_mr", [12288]), ("exl3_gemv_mr_grouped", [1024, 1024])]),
+    (25, [("exl3_gemv_mr", [12288]), ("exl3_gemm_trellis_grouped", [1024, 1024])]),
+    (31, [("exl3_gemm_trellis_grouped", [12288]), ("exl3_gemm_trellis_grouped", [1024, 1024])]),
+])
+def test_linear_groups_routes_each_run_by_its_shape(monkeypatch, m, expect):
+    """A checkpoint's q (2 bpw, 5120 -> 12288) and k / v (5 bpw, 1024 each): two runs of equal K,
+    each routed by its own launch shape (crossovers 30 and 21 rows)."""
+    rec = _Launches()
+    monkeypatch.setattr(ops, "E", rec)
+    monkeypatch.setattr(ops, "MR_MAX", None)
+    monkeypatch.setattr(ops, "GEMV_APPROX", "")
+    x = torch.zeros(m, 5120, dtype=torch.float16)
+    tr = [torch.zeros(320, n // 16, 16 * K, dtype=torch.int16) for n, K in ((12288, 2), (1024, 5), (1024, 5))]
+    su = [torch.ones(5120, dtype=torch.float16)] * 3
+    sv = [torch.ones(n, dtype=torch.float16) for n in (12288, 1024, 1024)]
+    y = torch.ops.exl3rocm.linear_groups(x, tr, su, sv, [2, 5, 5], False, True)
+    assert tuple(y.shape) == (m, 14336)
+    assert rec.calls == expect

@@ -30,8 +30,8 @@ def test_noalloc_rejects_oversize_and_ineligible_shapes_without_a_gpu():
     assert L.exl3_gemv_workspace_size(32, 256, 21888, 4, 1) > _lib.NOALLOC_SCRATCH_BYTES
     assert L.exl3_gemv_mr_noalloc(p[0], 256, p[1], p[2], 21888, p[3], p[4], 32, 256, 21888, 4, 0, 1, None) \
         == _lib.EWORKSPACE
-    assert L.exl3_gemv_mr_noalloc(p[0], 256, p[1], p[2], 128, p[3], p[4], 33, 256, 128, 4, 0, 1, None) \
-        == _lib.DECLINED                                   # m > 32: the GEMV's own status
+    assert L.exl3_gemv_mr_noalloc(p[0], 256, p[1], p[2], 128, p[3], p[4], _lib.GEMV_MAX_ROWS + 1, 256, 128, 4, 0, 1,
+                                  None) == _lib.DECLINED    # m > 64: the GEMV's own status, before any launch
     assert L.exl3_gemv_mr_noalloc(None, 256, p[1], p[2], 128, p[3], p[4], 1, 256, 128, 4, 0, 1, None) == _lib.EINVAL
     assert L.exl3_gemv_workspace_size(32, 17408, 5120, 4, 1) <= _lib.NOALLOC_SCRATCH_BYTES
     assert L.exl3_gemv_workspace_size(32, 5120, 17408, 8, 1) <= _lib.NOALLOC_SCRATCH_BYTES
