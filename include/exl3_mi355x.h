@@ -37,7 +37,7 @@ extern "C" {
 #endif
 
 #define EXL3_ABI_VERSION 3       /* 2: exl3_gemv_f32, exl3_gemm_trellis_silu_in; 3: exl3_gemv_silu_prerot_rows,
-                                    exl3_gemm_trellis_workspace_bound */
+                                    exl3_gemm_trellis_workspace_bound, the plain GEMV up to 64 rows */
 #define EXL3_MAX_GROUPS 4       /* groups per grouped launch (reference EXL3_GEMV_MRG_MAX) */
 #define EXL3_GEMV_MAX_ROWS 64   /* rows the plain fused GEMV takes (exl3_gemv_mr and its grouped forms) */
 #define EXL3_GEMV_FUSED_MAX_ROWS 32 /* rows of the fused-epilogue forms (SiLU input, gated, approximate) */

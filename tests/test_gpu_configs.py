@@ -201,13 +201,16 @@ def test_mixed_bitrate_qkv_module_vs_oracle():
 # ---------------------------------------------------------------------------------- boundary
 def test_exl3_gemm_dispatcher_routes_and_matches_the_ops():
     """The reference's row dispatcher (exl3_gemm -> route tag) through the C ABI: m <= 32 takes the
-    fused GEMV (tag 1), larger m the prefill GEMM (tag 2); outputs equal the op's bitwise."""
+    fused GEMV (tag 1), larger m the prefill GEMM (tag 2), although the plain GEMV itself takes up
+    to 64 rows; outputs equal the op's bitwise (this shape is outside the op's crossover table, so
+    the op's boundary is 32 too)."""
     k, n, bits = 2048, 1024, 4
     tr, su, sv = synth.layer("disp", 0, k, n, bits)
     x = synth.activations(synth.key_of("disp", "x"), 40, k)
     X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
     for m, tag in ((1, 1), (8, 1), (32, 1), (40, 2)):
-        assert E.exl3_gemv_mr_supported(m, k, n, bits, False, True) == (m <= 32)
+        assert E.exl3_gemv_mr_supported(m, k, n, bits, False, True) == (m <= _lib.GEMV_MAX_ROWS)
+        assert ops.gemv_rows(m, k, n) == (m <= 32)
         C = torch.empty(m, n, dtype=torch.float16, device=DEV)
         A_had = torch.empty(m, k, dtype=torch.float16, device=DEV)
         assert E.exl3_gemm(X[:m].contiguous(), T, C, SU, A_had, SV, -1, False, True, 0) == tag
