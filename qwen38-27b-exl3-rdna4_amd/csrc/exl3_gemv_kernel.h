@@ -880,8 +880,12 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                         if (e < total) lds_c[(e >> 7) * A_ROW + (e & 127)] = f16_bits((f16) sum[j]);
                     }
                 }
-            } else if (!GATED && MT_ != 0 && M > 1) {
-                if (rb == 2) {
+            } else if (!GATED && MT_ == 1 && M > 1 && rb == 2) {
+                // up to 16 rows, two blocks side by side up to 8: 4-byte loads, a thread keeping 4
+                // elements x 8 contributors in flight.  (The 16-byte form below in this
+                // instantiation too took 8 and 16 rows 1-3 us faster but 2 and 4 rows 1-1.9 us
+                // slower: its registers changed the whole kernel's allocation.)
+                {
                     // two blocks side by side (M <= 8): a thread keeps 4 elements x 8 contributors of
                     // loads in flight, each element summing its block's contributors in order (one
                     // round trip for both blocks: -1.5 to -2 us at M = 2 / 4 on gate; the one-block
@@ -928,7 +932,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                             if (e < total) lds_c[(e >> 7) * A_ROW + (e & 127)] = f16_bits((f16) sum[j]);
                         }
                     }
-                } else {
+                }
+            } else if (!GATED && MT_ == 1 && M > 1) {
+                {
                     // one block per pass (rb == 1): every element shares the block's contributors, so a
                     // thread keeps 4 elements x 8 contributors of loads in flight (sums in contributor order)
                     const int bi = s_list[r0];
@@ -960,6 +966,67 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                         for (int j = 0; j < 4; ++j) {
                             const int e = e0 + 256 * j;
                             if (e < total) lds_c[(e >> 7) * A_ROW + (e & 127)] = f16_bits((f16) sum[j]);
+                        }
+                    }
+                }
+            } else if (!GATED && MT_ != 0 && M > 1) {
+                // 17 to 64 rows (one block per pass): partials as 16-byte device-scope loads, a
+                // thread summing 4 consecutive elements of one row per load, each element over its
+                // block's contributors in order (the order of every other form), J x 8 loads in
+                // flight per thread.  Scalar 4-byte loads carried 4 x fewer elements per round trip:
+                // at 32 rows the reduction was the critical workgroup's longest phase (down 8 us, at
+                // 64 rows 35 us); with these loads down takes 41.1 against 48.9 us at 32 rows, 67.3
+                // against 83.3 at 64
+                constexpr int J = 4;
+                const int half = M * 128;
+                const int bi0 = s_list[r0], bi1 = s_list[r0 + (rb == 2 ? 1 : 0)];
+                const uint32_t cs4 = (uint32_t) gg.max_seg * (uint32_t) M * 512u;   // bytes between slots
+                const uint32_t f00 = (uint32_t) ((s_own[0][bi0] * gg.max_seg + s_own[2][bi0]) * M) * 512u;
+                const uint32_t f01 = (uint32_t) (s_own[0][bi0] + 1) * cs4;
+                const uint32_t f10 = (uint32_t) ((s_own[0][bi1] * gg.max_seg + s_own[2][bi1]) * M) * 512u;
+                const uint32_t f11 = (uint32_t) (s_own[0][bi1] + 1) * cs4;
+                const int nc0 = s_own[1][bi0], nc1 = rb == 2 ? s_own[1][bi1] : 0;
+                const int ncmax = nc0 > nc1 ? nc0 : nc1;
+                const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(part_grp), 0, 0x7FFFFFFF,
+                                                                                     RAW_BUFFER_FLAGS);
+                for (int e0 = 4 * (int) threadIdx.x; e0 < total; e0 += 1024 * J) {
+                    f32x4 sum[J];
+#pragma unroll
+                    for (int j = 0; j < J; ++j) sum[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int c0 = 0; c0 < ncmax; c0 += 8) {
+                        f32x4 v[J][8];
+#pragma unroll
+                        for (int j = 0; j < J; ++j) {
+                            const int e = e0 + 1024 * j;
+                            const bool second = e >= half;
+                            const int el = second ? e - half : e;
+                            const int nc = e < total ? (second ? nc1 : nc0) : 0;
+#pragma unroll
+                            for (int cc = 0; cc < 8; ++cc) {
+                                const int c = c0 + cc;
+                                const uint32_t off = (c == 0 ? (second ? f10 : f00) : (second ? f11 : f01) + (uint32_t) (c - 1) * cs4) +
+                                                     (uint32_t) el * 4u;
+                                v[j][cc] = c < nc ? __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(prs, off, 0, SC1))
+                                                  : f32x4{0.f, 0.f, 0.f, 0.f};
+                            }
+                        }
+#pragma unroll
+                        for (int j = 0; j < J; ++j) {
+                            const int e = e0 + 1024 * j;
+                            const int nc = e < total ? (e >= half ? nc1 : nc0) : 0;
+#pragma unroll
+                            for (int cc = 0; cc < 8; ++cc)
+                                if (c0 + cc < nc) sum[j] += v[j][cc];
+                        }
+                    }
+#pragma unroll
+                    for (int j = 0; j < J; ++j) {
+                        const int e = e0 + 1024 * j;
+                        if (e < total) {
+                            // the 4 elements share a row (rows are 128 wide): one 8-byte LDS store
+                            const uint32_t lo = f16_bits((f16) sum[j][0]) | (f16_bits((f16) sum[j][1]) << 16);
+                            const uint32_t hi = f16_bits((f16) sum[j][2]) | (f16_bits((f16) sum[j][3]) << 16);
+                            *reinterpret_cast<u32x2*>(&lds_c[(e >> 7) * A_ROW + (e & 127)]) = u32x2{lo, hi};
                         }
                     }
                 }

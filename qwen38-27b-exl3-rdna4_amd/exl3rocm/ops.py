@@ -38,17 +38,16 @@ DEFAULT_MR = 32
 # Largest row count at which the fused GEMV beats the prefill GEMM, by (k, output columns of the
 # launch: all its groups).  Measured on MI355X for the launches a Qwen3.5-27B checkpoint makes (q/k/v
 # and gate/up grouped as linear_groups groups them, and lm_head): both routes at every M from 2 to
-# 48 (to 64 where the GEMV still led at 48), graphs of 24 launches over 8 weight copies, 4 bpw, and
-# 2 / 3 bpw where a checkpoint holds them (the boundary moved by <= 6 rows).  Each entry is the
-# boundary b that minimises the summed time over M with no step above 5 % from the GEMV at b rows
-# to the GEMM at b + 1.  The GEMM's cost is flat within each 16-row MFMA tile and the GEMV's grows
-# ~0.75 us a row (its split-K reduction), so the GEMM wins early where its 128-column tiles fill
-# the chip (5120 - 7168 columns: b = 8) and late where they do not (2 x 17408 columns: at 64 rows
-# the GEMV takes 100.5 us, the GEMM 102.6; lm_head: 484 against 553, the GEMV's row limit).
+# 64, graphs of 24 launches over 8 weight copies, 4 bpw, and 2 / 3 bpw where a checkpoint holds them
+# (the boundary moved by <= 4 rows).  Each entry is a boundary b within 1 % of the least summed time
+# over M with no step above 5 % from the GEMV at b rows to the GEMM at b + 1.  The GEMM's cost is
+# flat within each 16-row MFMA tile; the GEMV's grows with every row and 16-row tile, so the GEMM
+# wins early where its 128-column tiles fill the chip (5120 - 7168 columns: b = 8) and late where
+# they do not (2 x 17408 columns and lm_head: the GEMV to its 64-row limit).
 GEMV_CROSSOVER = {
-    (5120, 1024): 24, (5120, 2048): 21, (5120, 5120): 8, (5120, 6144): 8, (5120, 7168): 8,
-    (5120, 10240): 20, (5120, 12288): 30, (5120, 14336): 17, (5120, 16384): 28, (5120, 17408): 40,
-    (5120, 34816): 64, (5120, 248320): 64, (6144, 5120): 25, (17408, 5120): 30,
+    (5120, 1024): 64, (5120, 2048): 33, (5120, 5120): 8, (5120, 6144): 8, (5120, 7168): 8,
+    (5120, 10240): 31, (5120, 12288): 33, (5120, 14336): 18, (5120, 16384): 33, (5120, 17408): 46,
+    (5120, 34816): 64, (5120, 248320): 64, (6144, 5120): 32, (17408, 5120): 35,
 }
 
 

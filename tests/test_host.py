@@ -345,10 +345,11 @@ class _Launches:
 ])
 def test_linear_groups_routes_each_run_by_its_shape(monkeypatch, m, expect):
     """A checkpoint's q (2 bpw, 5120 -> 12288) and k / v (5 bpw, 1024 each): two runs of equal K,
-    each routed by its own launch shape (crossovers 30 and 21 rows)."""
+    each routed by its own launch shape (crossovers set here to 30 and 21 rows)."""
     rec = _Launches()
     monkeypatch.setattr(ops, "E", rec)
     monkeypatch.setattr(ops, "MR_MAX", None)
+    monkeypatch.setattr(ops, "GEMV_CROSSOVER", {(5120, 12288): 30, (5120, 2048): 21})
     monkeypatch.setattr(ops, "GEMV_APPROX", "")
     x = torch.zeros(m, 5120, dtype=torch.float16)
     tr = [torch.zeros(320, n // 16, 16 * K, dtype=torch.int16) for n, K in ((12288, 2), (1024, 5), (1024, 5))]
