@@ -202,7 +202,8 @@ struct Split {
 
 // Two workgroups (8 waves) per CU are resident at once: up to 256 registers per lane, enough for
 // a ring deep enough that one wave alone keeps its SIMD busy.
-// MT: 16-row MFMA tiles of the input rows (0: exactly one row, a compile-time M; 1 to 4).  FORM:
+// MT: 16-row MFMA tiles of the input rows (0: exactly one row, a compile-time M; 1 to 4; 5: one
+// tile, like 1, with the 16-byte-load reduction of the multi-tile forms).  FORM:
 //   FORM_PLAIN   the EXL3 linear of each group;
 //   FORM_GATED   groups 0 (gate) and 1 (up) of equal width; the workgroup completing a block of
 //                both writes fp16(fp16(silu(gate)) * up) to g[0].y instead of the two outputs;
@@ -255,7 +256,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // scratch memory, and every later read of it would be a vector-memory load
     const GemvGroup gg = grp == 0 ? a.g[0] : grp == 1 ? a.g[1] : grp == 2 ? a.g[2] : a.g[3];
     const int w = older ? b - gg.o0 : gg.nold + (b - gg.y0);
-    constexpr int MT = MT_ == 0 ? 1 : MT_;
+    constexpr int MT = MT_ == 0 || MT_ == 5 ? 1 : MT_;
     // approximate mul1 routes (CB 3: affine, CB 4: int8 activations): the decoder emits 1024 + s
     // unscaled; per (unit, row) the input rotation leaves in the LDS row's padding the row's input
     // sum (affine) or its int8 scale q and integer sum (int8)
@@ -729,7 +730,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // completed blocks (gated: block pairs, 2M rows each: gate, then up) reduced side by side
     // blocks reduced side by side: two up to 8 rows (one round trip of partial loads for both;
     // measured slower from 16 rows, where one block already fills the passes)
-    const int RB = gated && M > 1 ? 1 : (M <= 8 ? 2 : 1);
+    // (MT 5, 8 to 16 rows: two blocks side by side, one pass of 16-byte loads for both: a second
+    // pass of partial loads cost 16-row launches ~5 us)
+    const int RB = gated && M > 1 ? 1 : (M <= (MT_ == 5 ? 16 : 8) ? 2 : 1);
     const int RM = gated ? 2 * M : M;
     const Split sp0{U, a.g[0].G, a.g[0].h, a.wa, a.wb, a.g[0].d_sg, a.g[0].d_u, a.d_wa, a.d_wb};
     const Split sp1{U, a.g[1].G, a.g[1].h, a.wa, a.wb, a.g[1].d_sg, a.g[1].d_u, a.d_wa, a.d_wb};
@@ -970,10 +973,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                     }
                 }
             } else if (!GATED && MT_ != 0 && M > 1) {
-                // 17 to 64 rows (one block per pass): partials as 16-byte device-scope loads, a
-                // thread summing 4 consecutive elements of one row per load, each element over its
-                // block's contributors in order (the order of every other form), J x 8 loads in
-                // flight per thread.  Scalar 4-byte loads carried 4 x fewer elements per round trip:
+                // 8 to 64 rows (two blocks side by side up to 16, else one block per pass): partials as
+                // 16-byte device-scope loads, a thread summing 4 consecutive elements of one row per
+                // load, each element over its block's contributors in order (the order of every
+                // other form), J x 8 loads in flight per thread.  Scalar 4-byte loads carried 4 x fewer elements per round trip:
                 // at 32 rows the reduction was the critical workgroup's longest phase (down 8 us, at
                 // 64 rows 35 us); with these loads down takes 41.1 against 48.9 us at 32 rows, 67.3
                 // against 83.3 at 64
@@ -1173,10 +1176,10 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
 
 // LDS: chunk_units x (m + 1) input rows, then the C rows of the blocks reduced side by side (the
 // fp32-output form: two fp32 rows of 128, the room of four fp16 rows)
-inline size_t lds_bytes(int M, int cu, bool gated, bool f32out = false)
+inline size_t lds_bytes(int M, int cu, bool gated, bool f32out = false, bool pair16 = false)
 {
     // blocks (gated: pairs) reduced side by side x rows: as RB in the kernel
-    const int c_rows = gated || f32out ? (M == 1 ? 4 : 2 * M) : (M <= 8 ? 2 * M : M);
+    const int c_rows = gated || f32out ? (M == 1 ? 4 : 2 * M) : (M <= (pair16 ? 16 : 8) ? 2 * M : M);
     return ((size_t) cu * (M + 1) + c_rows) * A_ROW * 2;
 }
 
@@ -1184,16 +1187,19 @@ template <int BITS, int CB, int MT_, int FORM>
 int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t stream)
 {
     hipLaunchKernelGGL((gemv_kernel<BITS, CB, MT_, FORM>), dim3(wgs), dim3(256),
-                       lds_bytes(a.M, a.chunk_units, FORM == FORM_GATED, FORM == FORM_F32OUT), stream, a);
+                       lds_bytes(a.M, a.chunk_units, FORM == FORM_GATED, FORM == FORM_F32OUT, MT_ == 5), stream, a);
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 
 // 16-row MFMA tiles of the rows: one exact row, <= 16, <= 32, and for the plain faithful forms (the
-// only ones the host lets past EXL3_GEMV_FUSED_MAX_ROWS) <= 48 and <= 64
+// only ones the host lets past EXL3_GEMV_FUSED_MAX_ROWS) <= 48 and <= 64; the plain form takes 8
+// to 16 rows in the one-tile instantiation with the 16-byte-load reduction (MT 5)
 template <int BITS, int CB, int FORM>
 int launch_gemv_m(const GemvArgs& a, int wgs, hipStream_t s)
 {
     if (a.M == 1) return launch_gemv_t<BITS, CB, 0, FORM>(a, wgs, s);
+    if constexpr (FORM == FORM_PLAIN && CB <= 2)
+        if (a.M >= 8 && a.M <= 16) return launch_gemv_t<BITS, CB, 5, FORM>(a, wgs, s);
     if (a.M <= 16) return launch_gemv_t<BITS, CB, 1, FORM>(a, wgs, s);
     if constexpr (FORM == FORM_PLAIN && CB <= 2) {
         if (a.M > 48) return launch_gemv_t<BITS, CB, 4, FORM>(a, wgs, s);

@@ -42,11 +42,11 @@ DEFAULT_MR = 32
 # (the boundary moved by <= 4 rows).  Each entry is a boundary b within 1 % of the least summed time
 # over M with no step above 5 % from the GEMV at b rows to the GEMM at b + 1.  The GEMM's cost is
 # flat within each 16-row MFMA tile; the GEMV's grows with every row and 16-row tile, so the GEMM
-# wins early where its 128-column tiles fill the chip (5120 - 7168 columns: b = 8) and late where
-# they do not (2 x 17408 columns and lm_head: the GEMV to its 64-row limit).
+# wins early where its 128-column tiles fill the chip (5120 - 7168 columns: b = 15 - 17) and late
+# where they do not (2 x 17408 columns and lm_head: the GEMV to its 64-row limit).
 GEMV_CROSSOVER = {
-    (5120, 1024): 64, (5120, 2048): 33, (5120, 5120): 8, (5120, 6144): 8, (5120, 7168): 8,
-    (5120, 10240): 31, (5120, 12288): 33, (5120, 14336): 18, (5120, 16384): 33, (5120, 17408): 46,
+    (5120, 1024): 64, (5120, 2048): 33, (5120, 5120): 15, (5120, 6144): 17, (5120, 7168): 15,
+    (5120, 10240): 31, (5120, 12288): 33, (5120, 14336): 17, (5120, 16384): 33, (5120, 17408): 46,
     (5120, 34816): 64, (5120, 248320): 64, (6144, 5120): 32, (17408, 5120): 35,
 }
 
