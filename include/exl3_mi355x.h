@@ -171,9 +171,12 @@ int exl3_gemv_mr_grouped_widths(const void* x, int64_t ldx, const void* const* t
  * counterpart, as exl3_gemv_workspace_size. */
 size_t exl3_gemv_workspace_size_widths(int m, int k, const int* widths, int groups);
 
-/* Rows from which the multi-row GEMV entry points rotate the input once per group into A_had
- * (EXL3_GEMV_PREROT_M, default 8); callers need not provide A_had below it.  No reference
- * counterpart.  Callers: exl3rocm's kernel wrappers. */
+/* Rows from which the multi-row GEMV entry points may rotate the input once per group into A_had;
+ * callers need not provide A_had below it.  2 by default: the library pre-rotates a launch when
+ * rows x the most units one workgroup owns >= 60 x (groups + 1) (o at 24 rows, gate and down at
+ * 9, gate/up at 7) and rotates in LDS otherwise, with the same outputs bitwise.  EXL3_GEMV_PREROT_M
+ * fixes one row count for every shape instead and is returned.  No reference counterpart.
+ * Callers: exl3rocm's kernel wrappers. */
 int exl3_gemv_prerot_rows(void);
 
 /* Rows from which exl3_gemv_silu_in forms and rotates its SiLU input once, by a separate pass into

@@ -332,15 +332,33 @@ bool shape_ok(int m, int k, int n, int K)
 
 // gs[i].y: group i's first output column (rows ldy apart); with pointer tables only gs[i].y is
 // read from gs, the table entries are the caller's contract
-// rows from which the input is rotated once per group by a separate pass into the caller's A_had
-// scratch, instead of by every workgroup for its own k-range (EXL3_GEMV_PREROT_M overrides): at
-// M = 32 the per-workgroup rotation is more VALU work than the decode; with the rows copied into
-// LDS in batches the pass pays from 8 rows (config-1 down at M = 8: 32.9 -> 30.8 us, gate even;
-// at M = 4 it costs 2 us)
+// The input is rotated either by every workgroup for its own k-range, in LDS (work ~ rows x the
+// units a workgroup owns), or once per group by a separate pass into the caller's A_had scratch
+// (a launch and one rotated copy per group: a fixed cost of 3.5-6 us that grows with the groups).
+// The pass pays from rows x max_per >= PREROT_UNIT_ROWS x (groups + 1); measured crossovers
+// (rows, max_per): gate and down 8-9 (14), o 24-28 (5), 6144 x 5120 17-20 (6); the 2-group
+// 1024-wide k/v pair 40-48 (4), gate/up ~7 (27); the 3-group q/k/v 28-40 (7).  Outputs are
+// bitwise the same either way.  EXL3_GEMV_PREROT_M, when set, fixes one row count for every shape.
+constexpr int PREROT_UNIT_ROWS = 60;
+
+int prerot_override()
+{
+    static const int v = env_int("EXL3_GEMV_PREROT_M", 0);
+    return v;
+}
+
+bool prerot(int m, int max_per, int groups)
+{
+    const int o = prerot_override();
+    if (o > 0) return m >= o;
+    return m > 1 && (int64_t) m * max_per >= (int64_t) PREROT_UNIT_ROWS * (groups + 1);
+}
+
+// the fewest rows at which any shape may be pre-rotated: callers pass A_had from there on
 int prerot_rows()
 {
-    static const int v = env_int("EXL3_GEMV_PREROT_M", 8);
-    return v;
+    const int o = prerot_override();
+    return o > 0 ? o : 2;
 }
 
 // The same for a SiLU input (EXL3_GEMV_SILU_PREROT_M overrides): there the pass takes the place
@@ -391,7 +409,7 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
     a.x = (const uint16_t*) x;
     a.ldx = ldx;
     a.x_up = (const uint16_t*) x_up;
-    if (xr && !tabs && m > 1 && m >= (x_up ? silu_prerot_rows() : prerot_rows())) {
+    if (xr && !tabs && m > 1 && (x_up ? m >= silu_prerot_rows() : prerot(m, p.max_per, groups))) {
         if (((uintptr_t) xr) & 15) return EXL3_EINVAL;
         // every group's rotated rows in one launch
         void* outs[EXL3_MAX_GROUPS];

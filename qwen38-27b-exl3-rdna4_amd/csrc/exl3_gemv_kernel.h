@@ -730,7 +730,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // completed blocks (gated: block pairs, 2M rows each: gate, then up) reduced side by side
     // blocks reduced side by side: two up to 8 rows (one round trip of partial loads for both;
     // measured slower from 16 rows, where one block already fills the passes)
-    // (MT 5, 8 to 16 rows: two blocks side by side, one pass of 16-byte loads for both: a second
+    // (MT 5, up to 16 rows: two blocks side by side, one pass of 16-byte loads for both: a second
     // pass of partial loads cost 16-row launches ~5 us)
     const int RB = gated && M > 1 ? 1 : (M <= (MT_ == 5 ? 16 : 8) ? 2 : 1);
     const int RM = gated ? 2 * M : M;
@@ -973,7 +973,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                     }
                 }
             } else if (!GATED && MT_ != 0 && M > 1) {
-                // 8 to 64 rows (two blocks side by side up to 16, else one block per pass): partials as
+                // MT 5 and 17 to 64 rows (two blocks side by side up to 16, else one block per pass): partials as
                 // 16-byte device-scope loads, a thread summing 4 consecutive elements of one row per
                 // load, each element over its block's contributors in order (the order of every
                 // other form), J x 8 loads in flight per thread.  Scalar 4-byte loads carried 4 x fewer elements per round trip:
@@ -1192,14 +1192,17 @@ int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t stream)
 }
 
 // 16-row MFMA tiles of the rows: one exact row, <= 16, <= 32, and for the plain faithful forms (the
-// only ones the host lets past EXL3_GEMV_FUSED_MAX_ROWS) <= 48 and <= 64; the plain form takes 8
-// to 16 rows in the one-tile instantiation with the 16-byte-load reduction (MT 5)
+// only ones the host lets past EXL3_GEMV_FUSED_MAX_ROWS) <= 48 and <= 64; the plain form takes up
+// to 16 rows in the one-tile instantiation with the 16-byte-load reduction (MT 5) from 5 rows when
+// the grid holds two workgroups on every CU (gate, down, o, q/k/v at 5-7 rows: 1.5-3.6 us faster
+// than MT 1), from 9 on a smaller grid (the 320-workgroup 1024-wide k/v pair: MT 1 2.4 us faster
+// at 5-8 rows); below 5 rows MT 1 is as fast or faster on every shape
 template <int BITS, int CB, int FORM>
 int launch_gemv_m(const GemvArgs& a, int wgs, hipStream_t s)
 {
     if (a.M == 1) return launch_gemv_t<BITS, CB, 0, FORM>(a, wgs, s);
     if constexpr (FORM == FORM_PLAIN && CB <= 2)
-        if (a.M >= 8 && a.M <= 16) return launch_gemv_t<BITS, CB, 5, FORM>(a, wgs, s);
+        if (a.M >= (wgs >= 256 * WAVES_PER_SIMD ? 5 : 9) && a.M <= 16) return launch_gemv_t<BITS, CB, 5, FORM>(a, wgs, s);
     if (a.M <= 16) return launch_gemv_t<BITS, CB, 1, FORM>(a, wgs, s);
     if constexpr (FORM == FORM_PLAIN && CB <= 2) {
         if (a.M > 48) return launch_gemv_t<BITS, CB, 4, FORM>(a, wgs, s);

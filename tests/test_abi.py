@@ -157,4 +157,4 @@ def test_prefill_workspace_bound_covers_every_plan():
 
 def test_silu_prerot_rows_query():
     assert _lib.lib().exl3_gemv_silu_prerot_rows() == int(os.environ.get("EXL3_GEMV_SILU_PREROT_M", "4"))
-    assert _lib.lib().exl3_gemv_prerot_rows() == int(os.environ.get("EXL3_GEMV_PREROT_M", "8"))
+    assert _lib.lib().exl3_gemv_prerot_rows() == int(os.environ.get("EXL3_GEMV_PREROT_M", "2"))

@@ -126,7 +126,8 @@ def test_reconstruct_full_size_bitexact(k, n, bits, cb):
 def test_had_r_128_f32_vs_exact():
     """The float32 transform (the prefill's values) against the exact float64 one: equal in all
     but a few elements, and those within one fp16 unit in the last place.  The GEMV's pre-rotated
-    input rows (A_had from m >= 8) are the exact transform's, bitwise."""
+    input rows are the exact transform's, bitwise (5120 -> 256 at 64 rows: 4 units per workgroup,
+    64 x 4 >= 120, so the library takes the pre-rotation pass)."""
     rng = np.random.default_rng(5)
     x = (rng.standard_normal((64, 5120)) * 2).astype(np.float16)
     su = synth.scales(2, 5120)
@@ -139,11 +140,11 @@ def test_had_r_128_f32_vs_exact():
     assert np.abs(e - f).max() <= 1 and (e != f).mean() < 0.01
     tr, _, sv = synth.layer("hadf32", 0, 5120, 256, 4)
     T, SV = to_dev(tr.view(np.int16), sv)
-    A_had = torch.empty(16, 5120, dtype=torch.float16, device=DEV)
-    y = torch.empty(16, 256, dtype=torch.float16, device=DEV)
-    assert E.exl3_gemv_mr(X[:16], T, y, SU, A_had, SV, 4, False, True) == 0
+    A_had = torch.zeros(64, 5120, dtype=torch.float16, device=DEV)
+    y = torch.empty(64, 256, dtype=torch.float16, device=DEV)
+    assert E.exl3_gemv_mr(X, T, y, SU, A_had, SV, 4, False, True) == 0
     torch.cuda.synchronize()
-    assert torch.equal(A_had.view(torch.int16), ex[:16].view(torch.int16))
+    assert torch.equal(A_had.view(torch.int16), ex.view(torch.int16))
 
 
 @pytest.mark.parametrize("rows,cols", [(1, 128), (37, 384), (16, 5120), (300, 1024)])
@@ -241,11 +242,44 @@ def test_rows_bitwise_equal_to_m1(k, n, bits, monkeypatch):
     x, tr, su, sv = layer(k, n, bits, m=32)
     X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
     rows1 = torch.cat([torch.ops.exl3rocm.linear(X[r:r + 1], T, SU, SV, bits, False, True) for r in range(32)])
-    for m in (2, 3, 4, 8, 12, 16, 17, 24, 32):
+    for m in (2, 3, 4, 5, 7, 8, 9, 12, 16, 17, 24, 32):
         ym = torch.ops.exl3rocm.linear(X[:m], T, SU, SV, bits, False, True)
         assert torch.equal(ym.view(torch.int16), rows1[:m].view(torch.int16)), m
     torch.cuda.synchronize()
     assert_close(rows1.cpu().numpy(), cpu.linear(x, tr, bits, su, sv, 2), (k, n, bits))
+
+
+@pytest.mark.parametrize("k,n,m,pre", [(5120, 256, 16, False), (5120, 256, 64, True), (5120, 5120, 20, False),
+                                       (5120, 5120, 24, True), (5120, 17408, 8, False), (5120, 17408, 9, True)])
+def test_prerotation_rule_and_lds_rotation_bitwise(k, n, m, pre):
+    """Through the C ABI: the library rotates the input by a separate pass into A_had exactly when
+    rows x the most units one workgroup owns >= 60 x (groups + 1) (5120 -> 256: 4 units, from 30
+    rows; 5120 x 5120: 5, from 24; 5120 -> 17408: 14, from 9), else in LDS leaving A_had as it
+    was; the outputs of the two are bitwise equal, and equal to A_had = NULL (always in LDS)."""
+    import os
+    if os.environ.get("EXL3_GEMV_PREROT_M"):
+        pytest.skip("EXL3_GEMV_PREROT_M fixes the row count for every shape")
+    x, tr, su, sv = layer(k, n, 4, tag="prerot", m=m)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    L = _lib.lib()
+    ws = torch.zeros(L.exl3_gemv_workspace_size(m, k, n, 4, 1), dtype=torch.uint8, device=DEV)
+    sentinel = torch.full((m, k), 7.0, dtype=torch.float16, device=DEV)
+    ah = sentinel.clone()
+    y_lds, y_ah = (torch.empty(m, n, dtype=torch.float16, device=DEV) for _ in range(2))
+    st = torch.cuda.current_stream().cuda_stream
+    for y, a in ((y_lds, None), (y_ah, ah)):
+        assert L.exl3_gemv_mr(X.data_ptr(), k, T.data_ptr(), y.data_ptr(), n, SU.data_ptr(),
+                              a.data_ptr() if a is not None else None, SV.data_ptr(), m, k, n, 4, 0, 1,
+                              ws.data_ptr(), ws.numel(), st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(y_lds.view(torch.int16), y_ah.view(torch.int16))
+    assert torch.equal(ah, sentinel) != pre
+    if pre:
+        ex = torch.empty_like(X)
+        E.had_r_128(X, ex, SU, None, 1.0)
+        torch.cuda.synchronize()
+        assert torch.equal(ah.view(torch.int16), ex.view(torch.int16))
+    assert_close(y_lds.cpu().numpy(), cpu.linear(x, tr, 4, su, sv, 2), (k, n, m))
 
 
 def test_grouped_rows_and_pointer_table_form():
