@@ -307,7 +307,7 @@ def test_empty_batch_launches_nothing_on_every_route(monkeypatch, mode):
 def test_route_boundary_table_and_override(monkeypatch):
     """Each launch shape in the measured table routes its own boundary b to the GEMV and b + 1 to
     the prefill GEMM; the fused-epilogue forms stop at 32 rows; shapes outside the table take
-    DEFAULT_MR; EXL3_MR_MAX fixes one boundary for every shape, capped at the GEMV's 48 rows."""
+    DEFAULT_MR; EXL3_MR_MAX fixes one boundary for every shape, capped at the GEMV's 64 rows."""
     from exl3rocm import _lib
     monkeypatch.setattr(ops, "MR_MAX", None)
     for (k, w), b in ops.GEMV_CROSSOVER.items():
