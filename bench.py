@@ -584,12 +584,15 @@ def small_batch(torch, sets, ms=(1, 2, 4, 8, 12, 16, 17, 20, 24, 28, 32, 33, 36,
     tiles unsplit, the plan's comparison) at M in {4, ..., 256}.  Also b, the step at the route
     boundary op(b + 1) / op(b) - 1, the op's worst ratio to the faster route over M <= 64, and the
     smallest M at which the GEMM beats the GEMV.  Mean duration per call from a graph of `reps`
-    calls over the weight copies (HIP events on the replay stream)."""
+    calls over the weight copies (HIP events on the replay stream): the median of three blocks of
+    two replays, each graph after 8 warm replays (~10 ms) and the whole section after ~0.3 s of
+    M = 1 launches: the first graph timed after a host-side pause (capture, new inputs) ran 5-12 %
+    slower than the same graph timed again, the order of the forms deciding which looked faster."""
     from exl3rocm import kernels as E, ops, synth, _lib
     res = {}
     s = torch.cuda.Stream()
 
-    def graph_us(fn):
+    def graph_us(fn, blocks=3):
         with torch.cuda.stream(s):
             for ls in sets:
                 fn(ls)
@@ -598,16 +601,23 @@ def small_batch(torch, sets, ms=(1, 2, 4, 8, 12, 16, 17, 20, 24, 28, 32, 33, 36,
         with torch.cuda.graph(g, stream=s):
             for r in range(reps):
                 fn(sets[r % len(sets)])
+        ts = []
         with torch.cuda.stream(s):
-            g.replay()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(s)
-            for _ in range(3):
+            for _ in range(8):
                 g.replay()
-            e1.record(s)
-        s.synchronize()
+            for _ in range(blocks):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(s)
+                g.replay()
+                g.replay()
+                e1.record(s)
+                s.synchronize()
+                ts.append(e0.elapsed_time(e1) * 1e3 / (2 * reps))
         del g
-        return round(e0.elapsed_time(e1) * 1e3 / (3 * reps), 2)
+        return round(sorted(ts)[len(ts) // 2], 2)
+
+    x1 = torch.from_numpy(synth.activations(synth.key_of("cfg3", HIDDEN, 1), 1, HIDDEN)).cuda()
+    graph_us(lambda ls: torch.ops.exl3rocm.linear(x1, *ls.w["gate"], ls.bits, ls.mcg, ls.mul1), blocks=240)
 
     for name, k, names in (("gate", HIDDEN, ("gate",)), ("down", INTER, ("down",)), ("gate_up", HIDDEN, ("gate", "up"))):
         n = HIDDEN if name == "down" else INTER
