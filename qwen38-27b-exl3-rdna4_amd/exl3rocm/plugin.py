@@ -355,6 +355,26 @@ class Exl3LinearMethod(LinearMethodBase):
         y = y if y.dtype == x.dtype else y.to(x.dtype)
         return y if bias is None else y + bias
 
+    def apply_silu_mul(self, layer, gate_up, bias=None):
+        """The layer's linear of act = fp16(fp16(silu(gate)) * up), gate_up = [gate | up] (the
+        [*, 2k] output of the MLP's gate/up module): what `apply(layer, act_fn(gate_up))` gives with
+        vLLM's SiluAndMul, bitwise, as one op (exl3rocm::silu_mul_linear: the GEMV or the
+        prefill's input transform forms act as it loads, so act is never written).  No counterpart
+        in the reference plugin, whose MLP runs SiluAndMul and then the down linear.  For MLP code
+        that owns both steps; the layer holds one group (a down projection).  Like `apply`, this
+        is the local product only: a row-parallel caller still reduces across ranks."""
+        from . import ops  # noqa: F401  (registers the custom ops)
+        if len(layer.exl3_n) != 1:
+            raise ValueError(f"exl3rocm: apply_silu_mul takes a layer of one group, got {len(layer.exl3_n)}")
+        k = layer.exl3_suh_0.shape[0]
+        if gate_up.shape[-1] != 2 * k:
+            raise ValueError(f"exl3rocm: apply_silu_mul takes [gate | up] of 2 x {k} columns, got {gate_up.shape[-1]}")
+        gu = gate_up if gate_up.dtype == torch.float16 else gate_up.to(torch.float16)
+        y = torch.ops.exl3rocm.silu_mul_linear(gu, layer.exl3_trellis_0, layer.exl3_suh_0, layer.exl3_svh_0,
+                                                layer.exl3_K[0], layer.exl3_is_mcg, layer.exl3_is_mul1)
+        y = y if y.dtype == gate_up.dtype else y.to(gate_up.dtype)
+        return y if bias is None else y + bias
+
     def embedding(self, layer, input_):
         raise NotImplementedError("exl3rocm: quantized input embeddings are not supported")
 

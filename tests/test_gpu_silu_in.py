@@ -206,3 +206,41 @@ def test_prefill_silu_in_graph_replays():
             again = torch.ops.exl3rocm.silu_mul_linear(GU, T, SU, SV, bits, False, True)
         torch.cuda.synchronize()
         assert same(again, eager)
+
+
+@pytest.mark.parametrize("m", [1, 5, 40])
+def test_plugin_apply_silu_mul(m):
+    """The plugin's hook for a model's MLP (in place of act_fn + down_proj): a down layer created
+    and loaded through Exl3LinearMethod; apply_silu_mul(layer, gu) == apply(layer, silu_mul(gu))
+    bitwise (fused GEMV at 1 and 5 rows, the prefill's input transform at 40), to the bar against
+    the oracle, leading shape, dtype and bias kept; a gu of the wrong width is rejected."""
+    from exl3rocm import plugin
+    k, n, bits = 1024, 768, 4
+    method = plugin.Exl3LinearMethod(plugin.Exl3Config("mul1"), [("down", bits, k, n)])
+    lay = torch.nn.Module()
+    method.create_weights(lay, k, [n], k, n, torch.float16)
+    lay.to(DEV)
+    gu, tr, su, sv = down(k, n, bits, m, tag="silu-plugin", spread=4.0)
+    lay.trellis.weight_loader(lay.trellis, torch.from_numpy(tr.view(np.int16)))
+    lay.suh.weight_loader(lay.suh, torch.from_numpy(su))
+    lay.svh.weight_loader(lay.svh, torch.from_numpy(sv))
+    lay.mul1.weight_loader(lay.mul1, torch.tensor(0x83DCD12D))
+    method.process_weights_after_loading(lay)
+    GU = to_dev(gu)[0]
+    y = method.apply_silu_mul(lay, GU.view(1, m, 2 * k))
+    assert y.shape == (1, m, n) and y.dtype == torch.float16
+    act = torch.empty(m, k, dtype=torch.float16, device=DEV)
+    E.silu_mul(GU[:, :k], GU[:, k:], act)
+    want = method.apply(lay, act)
+    assert same(y.view(m, n), want)
+    g, u = gu[:, :k].astype(np.float64), gu[:, k:].astype(np.float64)
+    with np.errstate(over="ignore"):
+        a = O.to_f16(O.to_f16(g / (1.0 + np.exp(-g))) * u)
+    ref = cpu.linear(a.astype(np.float16), tr, bits, su, sv, 2)
+    torch.cuda.synchronize()
+    assert_close(y.view(m, n).cpu().numpy(), ref, ("apply_silu_mul", m))
+    yb = method.apply_silu_mul(lay, GU.float(), bias=torch.ones(n, device=DEV))
+    assert yb.dtype == torch.float32
+    assert torch.equal(yb, want.float() + 1)
+    with pytest.raises(ValueError):
+        method.apply_silu_mul(lay, GU[:, :k])

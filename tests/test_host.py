@@ -139,6 +139,14 @@ def test_partition_mapping_and_errors():
             plugin.Exl3LinearMethod._group_of(layer, (0, 1))
 
 
+def test_apply_silu_mul_rejects_fused_modules():
+    """The MLP hook takes a down projection (one group): a gate/up module is rejected before any
+    launch."""
+    method, layer = make_layer([("gate", 4, 128, 128), ("up", 4, 128, 128)])
+    with pytest.raises(ValueError, match="one group"):
+        method.apply_silu_mul(layer, torch.zeros(1, 256, dtype=torch.float16))
+
+
 def test_missing_tensor_is_reported():
     method, layer = make_layer([("a", 4, 128, 128)])
     layer.trellis.weight_loader(layer.trellis, torch.zeros(8, 8, 64, dtype=torch.int16))
