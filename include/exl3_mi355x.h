@@ -120,7 +120,9 @@ int exl3_gemv_f32(const void* x, int64_t ldx, const void* trellis, void* y, int6
 
 /* 1 <= m <= EXL3_GEMV_MAX_ROWS (64) EXL3 linear, output rows with stride ldy.
  * A_had: optional fp16 scratch of m * k elements (groups * m * k for the grouped forms).  When
- * given and m >= 8 (EXL3_GEMV_PREROT_M), the input is rotated once per group into it,
+ * given and the launch takes the pre-rotation pass (m x the most units one workgroup owns >=
+ * 60 x (groups + 1), or m >= EXL3_GEMV_PREROT_M when that is set; exl3_gemv_prerot_rows), the input
+ * is rotated once per group into it,
  * A_had = fp16(Had128(fp16(x * suh))) as in the reference, and the GEMV reads those rows; otherwise
  * every workgroup rotates its own k-range in LDS.  Either way the output is the same, bitwise.
  * Replaces `exl3_gemv_mr(A, B, C, suh, A_had, svh, K, mcg, mul1)` (reference ops.py:85;
