@@ -1193,7 +1193,8 @@ int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t stream)
 
 // 16-row MFMA tiles of the rows: one exact row, <= 16, <= 32, and for the plain faithful forms (the
 // only ones the host lets past EXL3_GEMV_FUSED_MAX_ROWS) <= 48 and <= 64; the plain form takes up
-// to 16 rows in the one-tile instantiation with the 16-byte-load reduction (MT 5) from 5 rows when
+// to 16 rows (the SiLU-input form too) in the one-tile instantiation with the 16-byte-load
+// reduction (MT 5) from 5 rows when
 // the grid holds two workgroups on every CU (gate, down, o, q/k/v at 5-7 rows: 1.5-3.6 us faster
 // than MT 1), from 9 on a smaller grid (the 320-workgroup 1024-wide k/v pair: MT 1 2.4 us faster
 // at 5-8 rows); below 5 rows MT 1 is as fast or faster on every shape
@@ -1201,7 +1202,7 @@ template <int BITS, int CB, int FORM>
 int launch_gemv_m(const GemvArgs& a, int wgs, hipStream_t s)
 {
     if (a.M == 1) return launch_gemv_t<BITS, CB, 0, FORM>(a, wgs, s);
-    if constexpr (FORM == FORM_PLAIN && CB <= 2)
+    if constexpr ((FORM == FORM_PLAIN || FORM == FORM_SILU_IN) && CB <= 2)
         if (a.M >= (wgs >= 256 * WAVES_PER_SIMD ? 5 : 9) && a.M <= 16) return launch_gemv_t<BITS, CB, 5, FORM>(a, wgs, s);
     if (a.M <= 16) return launch_gemv_t<BITS, CB, 1, FORM>(a, wgs, s);
     if constexpr (FORM == FORM_PLAIN && CB <= 2) {

@@ -57,7 +57,8 @@ def raw_silu_in(GU, T, SU, SV, k, bits, mcg, mul1):
 
 
 @pytest.mark.parametrize("m,k,n,bits,cb", [(1, 17408, 5120, 4, 2), (2, 17408, 5120, 4, 2), (4, 17408, 5120, 4, 2),
-                                           (12, 17408, 5120, 4, 2),
+                                           (5, 17408, 5120, 4, 2), (8, 17408, 5120, 4, 2), (12, 17408, 5120, 4, 2),
+                                           (16, 17408, 5120, 4, 2), (6, 1024, 768, 4, 2), (9, 1024, 768, 4, 2),
                                            (32, 17408, 5120, 4, 2), (1, 512, 256, 3, 0), (3, 1024, 768, 2, 1),
                                            (16, 2048, 1024, 6, 2), (11, 256, 128, 8, 1)])
 def test_silu_in_matches_two_launches(m, k, n, bits, cb):
