@@ -454,6 +454,7 @@ int gemv_common(const void* x, int64_t ldx, const GemvGroup* gs, const int* widt
     a.k = k;
     a.UPB = k / 128;
     a.chunk_units = chunk_units(m, p.max_per);
+    a.max_per = p.max_per;
     a.ldy = ldy;
     a.counters = (uint32_t*) ws;
     a.part = (float*) ((char*) ws + COUNTER_BYTES);

@@ -89,6 +89,7 @@ struct GemvArgs {
     int wa, wb;                // unit-split weights of first-dispatched / second workgroups on a CU
     UDiv d_wa, d_wb;
     int chunk_units;           // units whose rotated input fits the LDS at once
+    int max_per;               // most units any workgroup owns (one LDS chunk when chunk_units == max_per)
     int64_t ldy;
     float* part;               // per group: [G][max_seg][M][128] fp32 partials
     uint32_t* counters;        // per group: [n / 128], zero between calls
@@ -202,8 +203,9 @@ struct Split {
 
 // Two workgroups (8 waves) per CU are resident at once: up to 256 registers per lane, enough for
 // a ring deep enough that one wave alone keeps its SIMD busy.
-// MT: 16-row MFMA tiles of the input rows (0: exactly one row, a compile-time M; 1 to 4; 5: one
-// tile, like 1, with the 16-byte-load reduction of the multi-tile forms).  FORM:
+// MT: 16-row MFMA tiles of the input rows (0: exactly one row, a compile-time M; 1 to 4; 5 and 6:
+// one tile, like 1, with the 16-byte-load reduction of the multi-tile forms, 6 with one quad of
+// loads in flight per contributor batch instead of four).  FORM:
 //   FORM_PLAIN   the EXL3 linear of each group;
 //   FORM_GATED   groups 0 (gate) and 1 (up) of equal width; the workgroup completing a block of
 //                both writes fp16(fp16(silu(gate)) * up) to g[0].y instead of the two outputs;
@@ -256,7 +258,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // scratch memory, and every later read of it would be a vector-memory load
     const GemvGroup gg = grp == 0 ? a.g[0] : grp == 1 ? a.g[1] : grp == 2 ? a.g[2] : a.g[3];
     const int w = older ? b - gg.o0 : gg.nold + (b - gg.y0);
-    constexpr int MT = MT_ == 0 || MT_ == 5 ? 1 : MT_;
+    constexpr int MT = MT_ == 0 || MT_ >= 5 ? 1 : MT_;
     // approximate mul1 routes (CB 3: affine, CB 4: int8 activations): the decoder emits 1024 + s
     // unscaled; per (unit, row) the input rotation leaves in the LDS row's padding the row's input
     // sum (affine) or its int8 scale q and integer sum (int8)
@@ -730,9 +732,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // completed blocks (gated: block pairs, 2M rows each: gate, then up) reduced side by side
     // blocks reduced side by side: two up to 8 rows (one round trip of partial loads for both;
     // measured slower from 16 rows, where one block already fills the passes)
-    // (MT 5, up to 16 rows: two blocks side by side, one pass of 16-byte loads for both: a second
-    // pass of partial loads cost 16-row launches ~5 us)
-    const int RB = gated && M > 1 ? 1 : (M <= (MT_ == 5 ? 16 : 8) ? 2 : 1);
+    // (MT 5 and 6, up to 16 rows: two blocks side by side, one pass (MT 5; MT 6 at up to 4 rows) of
+    // 16-byte loads for both: a second pass of partial loads cost 16-row launches ~5 us)
+    const int RB = gated && M > 1 ? 1 : (M <= (MT_ >= 5 ? 16 : 8) ? 2 : 1);
     const int RM = gated ? 2 * M : M;
     const Split sp0{U, a.g[0].G, a.g[0].h, a.wa, a.wb, a.g[0].d_sg, a.g[0].d_u, a.d_wa, a.d_wb};
     const Split sp1{U, a.g[1].G, a.g[1].h, a.wa, a.wb, a.g[1].d_sg, a.g[1].d_u, a.d_wa, a.d_wb};
@@ -973,14 +975,16 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                     }
                 }
             } else if (!GATED && MT_ != 0 && M > 1) {
-                // MT 5 and 17 to 64 rows (two blocks side by side up to 16, else one block per pass): partials as
+                // MT 5 / 6 and 17 to 64 rows (two blocks side by side up to 16, else one block per pass): partials as
                 // 16-byte device-scope loads, a thread summing 4 consecutive elements of one row per
                 // load, each element over its block's contributors in order (the order of every
                 // other form), J x 8 loads in flight per thread.  Scalar 4-byte loads carried 4 x fewer elements per round trip:
                 // at 32 rows the reduction was the critical workgroup's longest phase (down 8 us, at
                 // 64 rows 35 us); with these loads down takes 41.1 against 48.9 us at 32 rows, 67.3
-                // against 83.3 at 64
-                constexpr int J = 4;
+                // against 83.3 at 64.  MT 6 keeps one quad per thread (J = 1: the 1024 elements of two
+                // blocks of up to 4 rows in one pass, more rows in further passes): the 128 VGPRs of
+                // four quads would raise the whole kernel's allocation (MT 5: 220, MT 6: 172)
+                constexpr int J = MT_ == 6 ? 1 : 4;
                 const int half = M * 128;
                 const int bi0 = s_list[r0], bi1 = s_list[r0 + (rb == 2 ? 1 : 0)];
                 const uint32_t cs4 = (uint32_t) gg.max_seg * (uint32_t) M * 512u;   // bytes between slots
@@ -1187,23 +1191,29 @@ template <int BITS, int CB, int MT_, int FORM>
 int launch_gemv_t(const GemvArgs& a, int wgs, hipStream_t stream)
 {
     hipLaunchKernelGGL((gemv_kernel<BITS, CB, MT_, FORM>), dim3(wgs), dim3(256),
-                       lds_bytes(a.M, a.chunk_units, FORM == FORM_GATED, FORM == FORM_F32OUT, MT_ == 5), stream, a);
+                       lds_bytes(a.M, a.chunk_units, FORM == FORM_GATED, FORM == FORM_F32OUT, MT_ >= 5), stream, a);
     return hipGetLastError() == hipSuccess ? EXL3_OK : EXL3_ELAUNCH;
 }
 
 // 16-row MFMA tiles of the rows: one exact row, <= 16, <= 32, and for the plain faithful forms (the
-// only ones the host lets past EXL3_GEMV_FUSED_MAX_ROWS) <= 48 and <= 64; the plain form takes up
-// to 16 rows (the SiLU-input form too) in the one-tile instantiation with the 16-byte-load
-// reduction (MT 5) from 5 rows when
-// the grid holds two workgroups on every CU (gate, down, o, q/k/v at 5-7 rows: 1.5-3.6 us faster
-// than MT 1), from 9 on a smaller grid (the 320-workgroup 1024-wide k/v pair: MT 1 2.4 us faster
-// at 5-8 rows); below 5 rows MT 1 is as fast or faster on every shape
+// only ones the host lets past EXL3_GEMV_FUSED_MAX_ROWS) <= 48 and <= 64.  Up to 16 rows the plain
+// and SiLU-input forms take a one-tile instantiation with the 16-byte-load reduction: MT 6 (one
+// quad in flight, 172 VGPRs) when the workgroups stage their input in one LDS chunk, up to 8 rows
+// on a grid of two workgroups per CU and up to 16 on a smaller one; else MT 5 (four quads, 220
+// VGPRs) from 5 rows on the full grid and from 9 on a smaller one.  Against the 4-byte-load MT 1:
+// MT 6 0.5-2.7 us faster at 2-8 rows on every shape measured (o at 4 rows 14.1 -> 12.1 us, q/k/v at
+// 2 rows 16.0 -> 13.7), ~1 us at 9-16 rows on the 320-workgroup k/v pair; MT 5 up to 1.2 us faster
+// than MT 6 at 9-16 rows on full grids.  With two LDS chunks (gate/up at 8 rows: 27 units per
+// workgroup, 24 fit) the 172-VGPR forms lose 4 us to the chunk reload and MT 5 keeps them.
 template <int BITS, int CB, int FORM>
 int launch_gemv_m(const GemvArgs& a, int wgs, hipStream_t s)
 {
     if (a.M == 1) return launch_gemv_t<BITS, CB, 0, FORM>(a, wgs, s);
-    if constexpr ((FORM == FORM_PLAIN || FORM == FORM_SILU_IN) && CB <= 2)
-        if (a.M >= (wgs >= 256 * WAVES_PER_SIMD ? 5 : 9) && a.M <= 16) return launch_gemv_t<BITS, CB, 5, FORM>(a, wgs, s);
+    if constexpr ((FORM == FORM_PLAIN || FORM == FORM_SILU_IN) && CB <= 2) {
+        const bool full = wgs >= 256 * WAVES_PER_SIMD;
+        if (a.M <= (full ? 8 : 16) && a.chunk_units >= a.max_per) return launch_gemv_t<BITS, CB, 6, FORM>(a, wgs, s);
+        if (a.M >= (full ? 5 : 9) && a.M <= 16) return launch_gemv_t<BITS, CB, 5, FORM>(a, wgs, s);
+    }
     if (a.M <= 16) return launch_gemv_t<BITS, CB, 1, FORM>(a, wgs, s);
     if constexpr (FORM == FORM_PLAIN && CB <= 2) {
         if (a.M > 48) return launch_gemv_t<BITS, CB, 4, FORM>(a, wgs, s);
