@@ -436,26 +436,36 @@ def test_ineligible_declines_without_modifying_outputs():
 
 
 def test_graph_capture_replays_match_eager():
-    x, tr, su, sv = layer(5120, 5120, 4, m=4)
+    """Graph replays equal the eager calls bitwise, with eager work between replays, for every
+    small-M form on 5120 x 5120: 1 row (MT 0), 4 (MT 6), 12 (MT 5) through the op, and 24 rows
+    called directly with A_had (MT 2 after the pre-rotation launch, 24 x 5 units >= 120)."""
+    x, tr, su, sv = layer(5120, 5120, 4, m=24)
     X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
-    eager1 = torch.ops.exl3rocm.linear(X[:1], T, SU, SV, 4, False, True)
-    eager4 = torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True)
+    ms = (1, 4, 12)
+    eager = [torch.ops.exl3rocm.linear(X[:m], T, SU, SV, 4, False, True) for m in ms]
+    ah = torch.empty(24, 5120, dtype=torch.float16, device=DEV)
+    e24 = torch.empty(24, 5120, dtype=torch.float16, device=DEV)
+    assert E.exl3_gemv_mr(X, T, e24, SU, ah, SV, 4, False, True) == 0
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        ops.reserve_workspace(DEV, 5120, 5120, 4)       # the capture stream's own workspace
-        torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True)
+        ops.reserve_workspace(DEV, 5120, 5120, 4, m=24)  # the capture stream's own workspace
+        for m in ms:
+            torch.ops.exl3rocm.linear(X[:m], T, SU, SV, 4, False, True)
+        E.exl3_gemv_mr(X, T, torch.empty_like(e24), SU, ah, SV, 4, False, True)
     torch.cuda.current_stream().wait_stream(s)
+    y24 = torch.empty_like(e24)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=s):
-        y1 = torch.ops.exl3rocm.linear(X[:1], T, SU, SV, 4, False, True)
-        y4 = torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True)
+        ys = [torch.ops.exl3rocm.linear(X[:m], T, SU, SV, 4, False, True) for m in ms]
+        E.exl3_gemv_mr(X, T, y24, SU, ah, SV, 4, False, True)
     for _ in range(4):
         g.replay()
         torch.cuda.synchronize()
-        assert torch.equal(y1.view(torch.int16), eager1.view(torch.int16))
-        assert torch.equal(y4.view(torch.int16), eager4.view(torch.int16))
-        torch.ops.exl3rocm.linear(X, T, SU, SV, 4, False, True)     # eager work between replays
+        for m, y, e in zip(ms, ys, eager):
+            assert torch.equal(y.view(torch.int16), e.view(torch.int16)), m
+        assert torch.equal(y24.view(torch.int16), e24.view(torch.int16))
+        torch.ops.exl3rocm.linear(X[:4], T, SU, SV, 4, False, True)     # eager work between replays
         torch.cuda.synchronize()
 
 
