@@ -327,6 +327,29 @@ def test_gemv_64_rows_bitwise_rows_and_oracle(k, n, bits, cb):
     assert not E.exl3_gemv_mr_supported(65, k, n, bits, cb == 1, cb == 2)
 
 
+@pytest.mark.parametrize("k,n,bits,cb", [(2048, 1024, 2, 0), (2048, 1024, 8, 0), (5120, 5120, 6, 1), (5120, 5120, 2, 2),
+                                          (5120, 5120, 8, 2), (1024, 4096, 1, 1)])
+def test_gemv_small_rows_every_codebook(k, n, bits, cb):
+    """The one-tile forms at 2-16 rows for every codebook and the extreme bitrates: MT 6 (one quad of
+    partial loads in flight, in one pass up to 4 rows and several above) up to 8 rows on the
+    512-workgroup grid of 5120 x 5120 and up to 16 on the smaller grids of 2048 x 1024 and
+    1024 x 4096, MT 5 at 9-16 rows on the full grid: every row bitwise equal to its M = 1 call,
+    the rows against the oracle."""
+    tr, su, sv = synth.layer("rows16", f"{k}x{n}x{bits}x{cb}", k, n, bits)
+    x = synth.activations(synth.key_of("rows16", f"{k}x{n}x{bits}", "x"), 16, k, heavy_tail=True)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    print(f"small-row GEMV k={k} n={n} bits={bits} cb={cb} grid={_lib.lib().exl3_gemv_grid(k, n, 1)}", flush=True)
+    rows1 = torch.empty(16, n, dtype=torch.float16, device=DEV)
+    for r in range(16):
+        assert E.exl3_gemv_mr(X[r:r + 1], T, rows1[r:r + 1], SU, None, SV, bits, cb == 1, cb == 2) == 0
+    for m in (2, 3, 4, 5, 7, 8, 9, 13, 16):
+        ym = torch.full((m, n), float("nan"), dtype=torch.float16, device=DEV)
+        assert E.exl3_gemv_mr(X[:m], T, ym, SU, None, SV, bits, cb == 1, cb == 2) == 0
+        assert torch.equal(ym.view(torch.int16), rows1[:m].view(torch.int16)), m
+    torch.cuda.synchronize()
+    assert_close(rows1.cpu().numpy(), cpu.linear(x, tr, bits, su, sv, cb), (k, n, bits, cb))
+
+
 def test_fused_forms_decline_above_32_rows():
     """The fused-epilogue GEMV forms take at most 32 rows: 33 declines without writing."""
     k, n, bits = 1024, 512, 4
