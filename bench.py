@@ -475,7 +475,9 @@ def cpu_baseline(base, bits, budget_s=8.0, reps=5):
     except OSError:
         pass
     side["cpu_model"] = model
+    layer_weights = sum(k * n for _, k, n in LAYER)
     return {"value": head["gbs"], "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_layer": head["us_per_call"], "weights_per_s": round(layer_weights / (head["us_per_call"] * 1e-6), 1),
             "sample": f"median of {head['reps']} repetitions of the 7 linears of one configuration-1 layer at M=1, "
                       f"4 bpw mul1 (C oracle restatement, OpenMP {threads} threads of {affinity} in the affinity "
                       f"mask, {head['reps'] * head['us_per_call'] / 1e6:.1f} s); cpu: {model}",
@@ -869,7 +871,8 @@ def main() -> int:
         "lane_ops_per_s": VALU_LANE_OPS_PER_S, "floor_us_per_step": round(valu_floor_us, 2),
         "max_gbs": round(step_bytes / valu_floor_us / 1e3, 1),
         "frac_of_valu_roof": round(valu_floor_us / (ms_per_step * 1e3), 4)}
-    extra = {"launches_per_step": lps, "step_bytes": step_bytes, "wall_s": round(wall, 3)}
+    extra = {"launches_per_step": lps, "step_bytes": step_bytes, "wall_s": round(wall, 3),
+             "us_per_layer": round(ms_per_step * 1e3, 3), "weights_per_s": round(weights / (ms_per_step * 1e-3), 1)}
     log("per-shape GEMV timing")
     extra["per_shape_m1"] = per_shape_gemv(torch, sets, x5120, x17408)
     # the same step graphs again, now that the GPU has run decode work for a while: 400 steps after
