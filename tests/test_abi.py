@@ -158,3 +158,21 @@ def test_prefill_workspace_bound_covers_every_plan():
 def test_silu_prerot_rows_query():
     assert _lib.lib().exl3_gemv_silu_prerot_rows() == int(os.environ.get("EXL3_GEMV_SILU_PREROT_M", "4"))
     assert _lib.lib().exl3_gemv_prerot_rows() == int(os.environ.get("EXL3_GEMV_PREROT_M", "2"))
+
+
+@pytest.mark.parametrize("env,want", [(None, 2), ("5", 5), ("65", 65)])
+def test_prerot_override_in_a_fresh_process(env, want):
+    """EXL3_GEMV_PREROT_M is read once per process: unset, exl3_gemv_prerot_rows() is 2 (the fewest
+    rows at which the per-launch rule may pre-rotate); set, it is that row count (every launch from
+    it, none below).  Checked in a fresh interpreter (no GPU call)."""
+    import subprocess
+    import sys
+    e = dict(os.environ)
+    e.pop("EXL3_GEMV_PREROT_M", None)
+    if env is not None:
+        e["EXL3_GEMV_PREROT_M"] = env
+    code = ("import sys; sys.path.insert(0, %r); from exl3rocm import _lib; "
+            "print(_lib.lib().exl3_gemv_prerot_rows())") % os.path.join(REPO, "qwen38-27b-exl3-rdna4_amd")
+    out = subprocess.run([sys.executable, "-c", code], env=e, capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert int(out.stdout.strip().splitlines()[-1]) == want
