@@ -205,7 +205,8 @@ struct Split {
 // a ring deep enough that one wave alone keeps its SIMD busy.
 // MT: 16-row MFMA tiles of the input rows (0: exactly one row, a compile-time M; 1 to 4; 5 and 6:
 // one tile, like 1, with the 16-byte-load reduction of the multi-tile forms, 6 with one quad of
-// loads in flight per contributor batch instead of four).  FORM:
+// loads in flight per contributor batch instead of four; 7: two tiles, like 2, with two quads).
+// FORM:
 //   FORM_PLAIN   the EXL3 linear of each group;
 //   FORM_GATED   groups 0 (gate) and 1 (up) of equal width; the workgroup completing a block of
 //                both writes fp16(fp16(silu(gate)) * up) to g[0].y instead of the two outputs;
@@ -258,7 +259,7 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
     // scratch memory, and every later read of it would be a vector-memory load
     const GemvGroup gg = grp == 0 ? a.g[0] : grp == 1 ? a.g[1] : grp == 2 ? a.g[2] : a.g[3];
     const int w = older ? b - gg.o0 : gg.nold + (b - gg.y0);
-    constexpr int MT = MT_ == 0 || MT_ >= 5 ? 1 : MT_;
+    constexpr int MT = MT_ == 0 || MT_ == 5 || MT_ == 6 ? 1 : MT_ == 7 ? 2 : MT_;
     // approximate mul1 routes (CB 3: affine, CB 4: int8 activations): the decoder emits 1024 + s
     // unscaled; per (unit, row) the input rotation leaves in the LDS row's padding the row's input
     // sum (affine) or its int8 scale q and integer sum (int8)
@@ -983,8 +984,9 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_
                 // 64 rows 35 us); with these loads down takes 41.1 against 48.9 us at 32 rows, 67.3
                 // against 83.3 at 64.  MT 6 keeps one quad per thread (J = 1: the 1024 elements of two
                 // blocks of up to 4 rows in one pass, more rows in further passes): the 128 VGPRs of
-                // four quads would raise the whole kernel's allocation (MT 5: 220, MT 6: 172)
-                constexpr int J = MT_ == 6 ? 1 : 4;
+                // four quads would raise the whole kernel's allocation (MT 5: 220, MT 6: 172; MT 2:
+                // 220, MT 7 with two quads: 155)
+                constexpr int J = MT_ == 6 ? 1 : MT_ == 7 ? 2 : 4;
                 const int half = M * 128;
                 const int bi0 = s_list[r0], bi1 = s_list[r0 + (rb == 2 ? 1 : 0)];
                 const uint32_t cs4 = (uint32_t) gg.max_seg * (uint32_t) M * 512u;   // bytes between slots
@@ -1218,6 +1220,17 @@ int launch_gemv_m(const GemvArgs& a, int wgs, hipStream_t s)
     if constexpr (FORM == FORM_PLAIN && CB <= 2) {
         if (a.M > 48) return launch_gemv_t<BITS, CB, 4, FORM>(a, wgs, s);
         if (a.M > 32) return launch_gemv_t<BITS, CB, 3, FORM>(a, wgs, s);
+        // 17-32 rows: two quads of partial loads in flight (MT 7, 155 VGPRs against MT 2's 220)
+        // when every block has at most 8 contributors (one batch of loads per pass: the second
+        // pass is one round trip); with more, the extra pass costs more than the registers save
+        // (A/B in one call: gate/up, ~3 contributors, 1.4-2.3 us faster at 17-32 rows, gate, ~5,
+        // up to 1 us; down, q/k/v and the k/v pair, 10-21, up to 1.7 us slower)
+        int wpb = 0;
+        for (int i = 0; i < a.groups; ++i) {
+            const int w = (a.g[i].G * 128 + a.g[i].n - 1) / a.g[i].n;     // workgroups per block
+            wpb = w > wpb ? w : wpb;
+        }
+        if (wpb + 1 <= 8) return launch_gemv_t<BITS, CB, 7, FORM>(a, wgs, s);
     }
     return launch_gemv_t<BITS, CB, 2, FORM>(a, wgs, s);
 }

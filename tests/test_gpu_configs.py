@@ -350,6 +350,26 @@ def test_gemv_small_rows_every_codebook(k, n, bits, cb):
     assert_close(rows1.cpu().numpy(), cpu.linear(x, tr, bits, su, sv, cb), (k, n, bits, cb))
 
 
+@pytest.mark.parametrize("k,n,bits,cb", [(5120, 17408, 4, 2), (1024, 16384, 5, 1), (2048, 4096, 3, 0)])
+def test_gemv_17_32_rows_bitwise_rows_and_oracle(k, n, bits, cb):
+    """Two 16-row tiles (17-32 rows): MT 7 (two quads of partial loads in flight) where every block
+    has at most 8 contributors (5120 -> 17408: ~5; 1024 -> 16384: 5), MT 2 otherwise (2048 -> 4096:
+    17): every row bitwise equal to its M = 1 call, the rows against the oracle."""
+    tr, su, sv = synth.layer("rows32", f"{k}x{n}x{bits}x{cb}", k, n, bits)
+    x = synth.activations(synth.key_of("rows32", f"{k}x{n}x{bits}", "x"), 32, k, heavy_tail=True)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    print(f"17-32-row GEMV k={k} n={n} bits={bits} cb={cb} grid={_lib.lib().exl3_gemv_grid(k, n, 1)}", flush=True)
+    rows1 = torch.empty(32, n, dtype=torch.float16, device=DEV)
+    for r in range(32):
+        assert E.exl3_gemv_mr(X[r:r + 1], T, rows1[r:r + 1], SU, None, SV, bits, cb == 1, cb == 2) == 0
+    for m in (17, 20, 25, 31, 32):
+        ym = torch.full((m, n), float("nan"), dtype=torch.float16, device=DEV)
+        assert E.exl3_gemv_mr(X[:m], T, ym, SU, None, SV, bits, cb == 1, cb == 2) == 0
+        assert torch.equal(ym.view(torch.int16), rows1[:m].view(torch.int16)), m
+    torch.cuda.synchronize()
+    assert_close(rows1.cpu().numpy(), cpu.linear(x, tr, bits, su, sv, cb), (k, n, bits, cb))
+
+
 def test_fused_forms_decline_above_32_rows():
     """The fused-epilogue GEMV forms take at most 32 rows: 33 declines without writing."""
     k, n, bits = 1024, 512, 4
