@@ -283,15 +283,21 @@ def checkpoint_shapes(torch, reps=32, m_prefill=2048):
     for name, k, n, bits in CKPT_PREFILL:
         w = _device_layer(torch, k, n, bits, g)
         x = torch.randn(m_prefill, k, device="cuda", dtype=torch.float16, generator=g)
-        torch.ops.exl3rocm.linear(x, *w, bits, False, True)
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(4):
+        # ~2 ms of warm calls first (a quarter-millisecond launch timed right after a host pause read
+        # 15-20 % slow), then the median of three blocks of 4 calls
+        for _ in range(8):
             torch.ops.exl3rocm.linear(x, *w, bits, False, True)
-        e1.record()
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / 4
+        blocks = []
+        for _ in range(3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(4):
+                torch.ops.exl3rocm.linear(x, *w, bits, False, True)
+            e1.record()
+            torch.cuda.synchronize()
+            blocks.append(e0.elapsed_time(e1) * 1e3 / 4)
+        us = sorted(blocks)[1]
         prefill[name] = {"m": m_prefill, "k": k, "n": n, "bits": bits, "us": round(us, 1),
                          "tflops": round(2 * m_prefill * k * n / us / 1e6, 1)}
         del w, x
