@@ -243,6 +243,17 @@ def _device_layer(torch, k, n, bits, g):
     return T, su, sv
 
 
+def _warm(torch, fn, seconds, stream=None):
+    """Call fn in batches of 4 until `seconds` of wall time have passed (clocks up to speed)."""
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(4):
+            fn()
+        (stream or torch.cuda).synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            return
+
+
 def checkpoint_shapes(torch, reps=32, m_prefill=2048):
     """The reference checkpoint's own shapes: every M = 1 case of the reference's GEMV scoreboard
     (device-generated weights, enough copies for >= 1 GiB so they stream from HBM; mean of a graph
@@ -265,7 +276,7 @@ def checkpoint_shapes(torch, reps=32, m_prefill=2048):
             for r in range(reps):
                 y = torch.ops.exl3rocm.linear(x, *ws[r % copies], bits, False, True)
         with torch.cuda.stream(s):
-            graph.replay()
+            _warm(torch, graph.replay, 0.1, s)
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record(s)
             for _ in range(3):
@@ -283,11 +294,9 @@ def checkpoint_shapes(torch, reps=32, m_prefill=2048):
     for name, k, n, bits in CKPT_PREFILL:
         w = _device_layer(torch, k, n, bits, g)
         x = torch.randn(m_prefill, k, device="cuda", dtype=torch.float16, generator=g)
-        # ~2 ms of warm calls first (a quarter-millisecond launch timed right after a host pause read
-        # 15-20 % slow), then the median of three blocks of 4 calls
-        for _ in range(8):
-            torch.ops.exl3rocm.linear(x, *w, bits, False, True)
-        torch.cuda.synchronize()
+        # 0.3 s of warm calls first (the first milliseconds of GEMM work after a host pause ran up to
+        # 30 % slow, the clocks still rising), then the median of three blocks of 4 calls
+        _warm(torch, lambda: torch.ops.exl3rocm.linear(x, *w, bits, False, True), 0.3)
         blocks = []
         for _ in range(3):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
