@@ -138,6 +138,10 @@ def test_had_r_128_f32_vs_exact():
     e = ex.cpu().numpy().view(np.int16).astype(np.int32)
     f = fa.cpu().numpy().view(np.int16).astype(np.int32)
     assert np.abs(e - f).max() <= 1 and (e != f).mean() < 0.01
+    import os
+    override = os.environ.get("EXL3_GEMV_PREROT_M")
+    if override and int(override) > 64:
+        pytest.skip("EXL3_GEMV_PREROT_M above 64 keeps this launch's rotation in LDS (A_had unwritten)")
     tr, _, sv = synth.layer("hadf32", 0, 5120, 256, 4)
     T, SV = to_dev(tr.view(np.int16), sv)
     A_had = torch.zeros(64, 5120, dtype=torch.float16, device=DEV)

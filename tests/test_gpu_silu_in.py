@@ -70,12 +70,13 @@ def test_silu_in_matches_two_launches(m, k, n, bits, cb):
     got = fused(GU, T, SU, SV, k, bits, mcg, mul1)
     assert same(got, want), "fused input == silu_mul then exl3_gemv_mr"
     if m > 1:
-        # the pre-rotation pass (m >= 4) leaves the rotated activation in A_had; without A_had the
-        # kernel forms and rotates it in LDS
+        # the pre-rotation pass (from the library's SiLU pre-rotation row count, 4 unless
+        # EXL3_GEMV_SILU_PREROT_M sets it) leaves the rotated activation in A_had; without A_had
+        # the kernel forms and rotates it in LDS
         xr = torch.empty(m * k, dtype=torch.float16, device=DEV)
         assert same(fused(GU, T, SU, SV, k, bits, mcg, mul1, A_had=xr), want)
         assert same(raw_silu_in(GU, T, SU, SV, k, bits, mcg, mul1), want), "in-LDS form"
-        if m >= 4:
+        if m >= int(_lib.lib().exl3_gemv_silu_prerot_rows()):
             xw = torch.empty(m, k, dtype=torch.float16, device=DEV)
             E.had_r_128(act, xw, SU, None, 1.0)
             assert same(xr.view(m, k), xw), "A_had == the exact rotation of the activation"
