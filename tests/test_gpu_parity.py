@@ -263,6 +263,8 @@ def test_prerotation_rule_and_lds_rotation_bitwise(k, n, m, pre):
     import os
     if os.environ.get("EXL3_GEMV_PREROT_M"):
         pytest.skip("EXL3_GEMV_PREROT_M fixes the row count for every shape")
+    if os.environ.get("EXL3_GEMV_GRID"):
+        pytest.skip("EXL3_GEMV_GRID changes the units per workgroup the rule reads")
     x, tr, su, sv = layer(k, n, 4, tag="prerot", m=m)
     X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
     L = _lib.lib()
@@ -785,7 +787,8 @@ def test_linear_method_end_to_end():
         lay.svh.weight_loader(lay.svh, torch.from_numpy(sv), i)
         lay.mul1.weight_loader(lay.mul1, torch.tensor(0x83DCD12D), i)
     method.process_weights_after_loading(lay)
-    assert lay.exl3_mgemm_ptrs is not None
+    import os
+    assert (lay.exl3_mgemm_ptrs is not None) == (os.environ.get("EXL3_MGEMM", "1") != "0")
     x = synth.activations(synth.key_of("plug", "x"), 3, 1024)
     X = to_dev(x)[0]
     y3 = method.apply(lay, X)
