@@ -247,8 +247,9 @@ GridPlan plan_grid(int k, const int* widths, int groups)
     int64_t Utot = 0;
     for (int i = 0; i < groups; ++i) Utot += (int64_t) (widths[i] / 128) * UPB;
     const int forced = env_int("EXL3_GEMV_GRID", 0);
-    // at most ~max_contrib workgroups sharing one block
-    const int max_contrib = env_int("EXL3_GEMV_MAX_CONTRIB", 32);
+    // at most ~max_contrib workgroups sharing one block (EXL3_GEMV_MAX_CONTRIB below 1: the default)
+    const int mc = env_int("EXL3_GEMV_MAX_CONTRIB", 32);
+    const int max_contrib = mc >= 1 ? mc : 32;
     const int64_t min_units = std::max<int64_t>(1, (UPB + max_contrib - 1) / max_contrib);
     int64_t Gt = forced > 0 ? (int64_t) forced * groups : std::min<int64_t>(RESIDENT_WGS, Utot / min_units);
     Gt = std::max<int64_t>(Gt, groups);

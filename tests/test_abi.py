@@ -176,3 +176,22 @@ def test_prerot_override_in_a_fresh_process(env, want):
     out = subprocess.run([sys.executable, "-c", code], env=e, capture_output=True, text=True, timeout=120)
     assert out.returncode == 0, out.stderr
     assert int(out.stdout.strip().splitlines()[-1]) == want
+
+
+@pytest.mark.parametrize("env", ["0", "-3", "1", "8", "junk"])
+def test_gemv_plan_knobs_out_of_range_in_a_fresh_process(env):
+    """The measurement knobs of the GEMV grid plan never break sizing: EXL3_GEMV_MAX_CONTRIB of 0,
+    a negative value or a non-number plans as the default (no division by zero); EXL3_GEMV_GRID
+    and EXL3_GEMV_WEIGHTS with the same values fall back or clamp.  Every workspace size stays
+    positive.  Checked in a fresh interpreter (no GPU call)."""
+    import subprocess
+    import sys
+    e = dict(os.environ)
+    e.update({"EXL3_GEMV_MAX_CONTRIB": env, "EXL3_GEMV_GRID": env, "EXL3_GEMV_WEIGHTS": env + "," + env})
+    code = ("import sys; sys.path.insert(0, %r); from exl3rocm import _lib; L = _lib.lib(); "
+            "print(min(L.exl3_gemv_workspace_size(m, k, n, 4, g) for m in (1, 16, 64) "
+            "for k, n in ((5120, 5120), (17408, 5120), (5120, 17408), (128, 128)) for g in (1, 2)))"
+            ) % os.path.join(REPO, "qwen38-27b-exl3-rdna4_amd")
+    out = subprocess.run([sys.executable, "-c", code], env=e, capture_output=True, text=True, timeout=120)
+    assert out.returncode == 0, out.stderr
+    assert int(out.stdout.strip().splitlines()[-1]) > 0
