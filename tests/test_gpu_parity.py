@@ -263,8 +263,9 @@ def test_prerotation_rule_and_lds_rotation_bitwise(k, n, m, pre):
     import os
     if os.environ.get("EXL3_GEMV_PREROT_M"):
         pytest.skip("EXL3_GEMV_PREROT_M fixes the row count for every shape")
-    if os.environ.get("EXL3_GEMV_GRID"):
-        pytest.skip("EXL3_GEMV_GRID changes the units per workgroup the rule reads")
+    knobs = [v for v in ("EXL3_GEMV_GRID", "EXL3_GEMV_WEIGHTS", "EXL3_GEMV_MAX_CONTRIB") if os.environ.get(v)]
+    if knobs:
+        pytest.skip(f"{', '.join(knobs)} changes the units per workgroup the rule reads")
     x, tr, su, sv = layer(k, n, 4, tag="prerot", m=m)
     X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
     L = _lib.lib()
