@@ -8,6 +8,9 @@ codebook, and runs torch.ops.exl3rocm.linear / linear_groups as a model would.  
   * on the columns of every run of equal-K groups that takes the GEMV (rows <= that run's route
     boundary), those rows bitwise equal to the m == 1 call of the same op;
   * a second call bitwise equal to the first (completion counters and split workspaces reset).
+A second sweep runs a gated MLP (hidden k, intermediate n) through linear_silu_mul and
+silu_mul_linear: each equal, bitwise, to its unfused composition (linear_groups + silu_mul;
+silu_mul + linear) on whatever route the rows take, and both against the oracle.
 The draws cover shapes no hand-written case has (k = 128, single-unit blocks, uneven grouped
 widths, GEMM launches of a few tiles), at sizes the oracle finishes in well under a second.
 """
@@ -16,7 +19,8 @@ import pytest
 import torch
 
 import cpu
-from exl3rocm import _lib, ops, synth
+import exl3_oracle as O
+from exl3rocm import _lib, kernels as E, ops, synth
 from test_gpu_parity import DEV, assert_close, to_dev
 
 pytestmark = [pytest.mark.gpu,
@@ -104,5 +108,74 @@ def test_sweep_routed_ops_vs_oracle(case):
             y1 = run(X[r:r + 1], Ts, SUs, SVs, K, cb)
             assert torch.equal(y[r, c0:c1].view(torch.int16), y1[0, c0:c1].view(torch.int16)), ("row == m=1", r, c0)
     again = run(X, Ts, SUs, SVs, K, cb)
+    assert torch.equal(y.view(torch.int16), again.view(torch.int16)), "repeat call"
+    torch.cuda.synchronize()
+
+
+def draw_mlp(n_cases=48, seed=20261204):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n_cases):
+        if i % 8 == 7:                                            # the reference model's MLP
+            k, n = 5120, 17408
+        else:
+            k = 128 * int(rng.integers(1, 33))                    # hidden 128 .. 4096
+            n = 128 * int(rng.integers(1, 25))                    # intermediate 128 .. 3072
+        bits = int(rng.integers(1, 9))
+        cb = int(rng.integers(0, 3))
+        m = 1 if i % 6 == 0 else int(rng.choice(ROWS))
+        out.append((i, m, k, n, bits, cb))
+    return out
+
+
+MLP_CASES = draw_mlp()
+
+
+def silu_mul_ref(g, u):
+    """fp16(fp16(silu(g)) * u) in float64, one rounding each."""
+    g, u = np.asarray(g, np.float64), np.asarray(u, np.float64)
+    with np.errstate(over="ignore"):                  # exp(-g) = inf for very negative g: silu -> -0
+        return O.to_f16(O.to_f16(g / (1.0 + np.exp(-g))) * u)
+
+
+@pytest.mark.parametrize("case", MLP_CASES, ids=[f"{c[0]}-m{c[1]}-k{c[2]}-n{c[3]}-K{c[4]}-cb{c[5]}" for c in MLP_CASES])
+def test_sweep_mlp_ops_vs_oracle(case):
+    i, m, k, n, bits, cb = case
+    print(f"mlp sweep case {i}: m={m} k={k} n={n} K={bits} cb={cb}", flush=True)
+    mcg, mul1 = cb == 1, cb == 2
+    tag = f"mlpsweep{i}"
+    gate, up = (synth.layer(tag, g, k, n, bits) for g in range(2))
+    down = synth.layer(tag, 2, n, k, bits)
+    x = synth.activations(synth.key_of(tag, "x"), m, k)
+    rows = sorted({0, m // 2, m - 1})
+    # a power-of-two input scale that puts the gate outputs near unit RMS, as a normalised MLP
+    # input would (unit-scale random weights give outputs ~ sqrt(k): SiLU(g) * u and then the down
+    # projection would overflow fp16)
+    g0 = cpu.linear(x[rows], gate[0], bits, gate[1], gate[2], cb).astype(np.float64)
+    x = (x.astype(np.float32) * 2.0 ** -np.round(np.log2(np.sqrt(np.mean(g0 ** 2)) + 1e-30))).astype(np.float16)
+    X = to_dev(x)[0]
+    Tgu = [to_dev(tr.view(np.int16))[0] for tr, _, _ in (gate, up)]
+    SUgu = [to_dev(su)[0] for _, su, _ in (gate, up)]
+    SVgu = [to_dev(sv)[0] for _, _, sv in (gate, up)]
+    Td, SUd, SVd = to_dev(down[0].view(np.int16), down[1], down[2])
+    act = torch.ops.exl3rocm.linear_silu_mul(X, Tgu, SUgu, SVgu, [bits, bits], mcg, mul1)
+    gu = torch.ops.exl3rocm.linear_groups(X, Tgu, SUgu, SVgu, [bits, bits], mcg, mul1)
+    act2 = torch.empty_like(act)
+    E.silu_mul(gu[:, :n], gu[:, n:], act2)
+    assert torch.equal(act.view(torch.int16), act2.view(torch.int16)), "linear_silu_mul == linear_groups + silu_mul"
+    assert torch.isfinite(act).all()
+    g_ref, u_ref = (cpu.linear(x[rows], tr, bits, su, sv, cb) for tr, su, sv in (gate, up))
+    assert_close(act[rows].cpu().numpy(), silu_mul_ref(g_ref, u_ref), "act vs oracle")
+    y = torch.ops.exl3rocm.silu_mul_linear(gu, Td, SUd, SVd, bits, mcg, mul1)
+    y2 = torch.ops.exl3rocm.linear(act, Td, SUd, SVd, bits, mcg, mul1)
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16)), "silu_mul_linear == silu_mul + linear"
+    assert torch.isfinite(y).all()
+    act_rows = act[rows].cpu().numpy()
+    assert_close(y[rows].cpu().numpy(), cpu.linear(act_rows, down[0], bits, down[1], down[2], cb), "down vs oracle")
+    if ops.gemv_rows(m, n, k):
+        for r in rows:
+            y1 = torch.ops.exl3rocm.silu_mul_linear(gu[r:r + 1], Td, SUd, SVd, bits, mcg, mul1)
+            assert torch.equal(y[r].view(torch.int16), y1[0].view(torch.int16)), ("row == m=1", r)
+    again = torch.ops.exl3rocm.silu_mul_linear(gu, Td, SUd, SVd, bits, mcg, mul1)
     assert torch.equal(y.view(torch.int16), again.view(torch.int16)), "repeat call"
     torch.cuda.synchronize()
