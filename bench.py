@@ -827,7 +827,8 @@ def main() -> int:
         return 2
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this engine runs on one GPU; multi-GPU runs are not part of this build "
-              "(see DESIGN.md for how the path would shard)", file=sys.stderr)
+              "(the path would shard q/k/v/gate/up by 128-column blocks and o/down by 128-row "
+              "blocks, each GPU running these kernels on its shard)", file=sys.stderr)
         return 2
 
     if args.timeline:
