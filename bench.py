@@ -20,6 +20,8 @@ configuration 3 small-batch crossover, configuration 2 bitrate sweep.
   python bench.py [--steps K] [--warmup W] [--no-prefill] [--no-sweep] [--no-cpu]
   python bench.py --traffic-probe      (what the PMC traffic passes profile)
   python bench.py --prefill-only       (configuration 4 alone, for the prefill PMC passes)
+  python bench.py --config3-only       (configuration 3 alone, for its kernel trace)
+  python bench.py --checkpoint-only    (the reference checkpoint's shapes alone, for their kernel trace)
 """
 from __future__ import annotations
 
@@ -819,6 +821,9 @@ def main() -> int:
     ap.add_argument("--timeline", action="store_true",
                     help="only the per-workgroup phase timeline of each configuration-1 GEMV launch (loads the "
                          "tracing library exl3rocm/libexl3_mi355x_timeline.so: build_ext.py --timeline)")
+    ap.add_argument("--checkpoint-only", action="store_true",
+                    help="only the reference checkpoint's shapes (GEMV at M = 1, prefill at M = 2048; what "
+                         "its kernel-trace profile reads); prints its dict")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the configuration-4 prefill chunk (what the prefill PMC passes read); prints its dict")
     args = ap.parse_args()
@@ -842,6 +847,9 @@ def main() -> int:
         return traffic_probe(torch, bits, args.copies)
     if args.prefill_only:
         print(json.dumps(prefill_chunk(torch)), flush=True)
+        return 0
+    if args.checkpoint_only:
+        print(json.dumps(checkpoint_shapes(torch)), flush=True)
         return 0
     if args.timeline:
         _, sets = build_layers(torch, bits, args.copies)
