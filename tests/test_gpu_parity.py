@@ -495,6 +495,49 @@ def test_hgemm_recon_vs_fp32():
     assert err < 1e-3, err
 
 
+@pytest.mark.parametrize("m", [2, 5, 20, 40, 64, 100, 300])
+def test_row_strided_operands_bitwise(m):
+    """x as a column slice of a wider buffer (row stride k + 72, first column 0 or 8) and y as a
+    column slice of a wider output: the GEMV (m <= 64) and the prefill GEMM (single and grouped)
+    give bitwise the contiguous operands' result, and write nothing outside the slice."""
+    k, n, bits = 1024, 768, 4
+    x, tr, su, sv = layer(k, n, bits, tag="strided", m=m)
+    X, T, SU, SV = to_dev(x, tr.view(np.int16), su, sv)
+    want = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    gemv = m <= _lib.GEMV_MAX_ROWS
+    if gemv:
+        assert E.exl3_gemv_mr(X, T, want, SU, None, SV, bits, False, True) == 0
+    else:
+        E.exl3_gemm_trellis(X, T, want, SU, torch.empty_like(X), SV, bits, False, True)
+    for c0 in (0, 8):
+        wide = torch.full((m, k + 72), float("nan"), dtype=torch.float16, device=DEV)
+        wide[:, c0:c0 + k] = X
+        xs = wide[:, c0:c0 + k]
+        assert xs.stride(0) == k + 72
+        out = torch.full((m, n + 40), float("nan"), dtype=torch.float16, device=DEV)
+        ys = out[:, 8:8 + n]
+        if gemv:
+            assert E.exl3_gemv_mr(xs, T, ys, SU, None, SV, bits, False, True) == 0
+        else:
+            E.exl3_gemm_trellis(xs, T, ys, SU, torch.empty(m, k, dtype=torch.float16, device=DEV), SV, bits, False, True)
+        torch.cuda.synchronize()
+        assert torch.equal(ys.view(torch.int16), want.view(torch.int16)), ("strided", c0)
+        assert torch.isnan(out[:, :8]).all() and torch.isnan(out[:, 8 + n:]).all(), "wrote outside the slice"
+    if not gemv:
+        # grouped prefill over the same strided input, the same weights twice: every tile of this
+        # launch is split alike, so the two groups agree bitwise; both meet the bar against the
+        # single launch (whose split plan differs) and the oracle
+        wide = torch.full((m, k + 72), float("nan"), dtype=torch.float16, device=DEV)
+        wide[:, 8:8 + k] = X
+        y2 = torch.empty(m, 2 * n, dtype=torch.float16, device=DEV)
+        E.exl3_gemm_trellis_grouped(wide[:, 8:8 + k], [T, T], y2, [SU, SU],
+                                    torch.empty(2, m, k, dtype=torch.float16, device=DEV), [SV, SV], bits, False, True)
+        torch.cuda.synchronize()
+        assert torch.equal(y2[:, :n].view(torch.int16), y2[:, n:].view(torch.int16))
+        assert_close(y2[:, :n].cpu().numpy(), want.cpu().numpy(), "grouped vs single launch")
+        assert_close(y2[:, :n].cpu().numpy(), cpu.linear(x, tr, bits, su, sv, 2), "grouped strided vs oracle")
+
+
 def test_prefill_wide_ragged_parity():
     """A wide layer (512 column tiles) with a ragged last row tile against the oracle: the fused
     output transform writes only the valid rows."""
