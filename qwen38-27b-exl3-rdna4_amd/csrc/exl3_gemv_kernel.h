@@ -105,7 +105,8 @@ constexpr int LDS_BUDGET = 64 * 1024;           // per workgroup: 2 workgroups p
 // and o -1.7, -1.2 and -0.3 us alone): at launch every wave of every CU requests its first ring
 // half at once, and the CUs' load queues stall each wave's issue until early data returns, so a
 // shallower ring starts the first decode sooner (the first step of gate/up completed ~5 us after
-// launch with 8 in flight).
+// launch with 8 in flight).  2 and 6 measured slower too: config-1 step 67.1 and 66.1 us against
+// 65.3 (one process, outputs bitwise equal).
 constexpr int RING = 4;
 constexpr int WAVES_PER_SIMD = 2;
 
