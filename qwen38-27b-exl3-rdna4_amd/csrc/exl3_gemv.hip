@@ -136,6 +136,36 @@ __global__ void __launch_bounds__(256) had_kernel(const uint16_t* __restrict__ i
     }
 }
 
+// The same exact transform with one 128-block per wave, two elements a lane (had128_x2): the
+// latency form, for launches of at most EXL3_GEMV_MAX_ROWS rows (the GEMV's pre-rotation pass).
+// There had_kernel's grid of one 8-lane group per block leaves most CUs idle (16 rows x 40
+// blocks: 20 workgroups) and each lane's 16-element butterflies are the critical path.  The
+// same values bit for bit: both sum exactly in float64 and round once (scaled_f16), with the
+// same fp16 products for pre, post and the SiLU input.  A wave reads its whole block before any
+// lane writes, so in == out is safe.
+template <class T>
+__global__ void __launch_bounds__(256) had_kernel_x2(const uint16_t* __restrict__ in, const uint16_t* __restrict__ in_up,
+                                                     int64_t ld_in, HadGroups hg, int groups, int64_t ld_out, int rows,
+                                                     int cols, const uint16_t* __restrict__ post, T scale)
+{
+    const int blocks_per_row = cols / 128;
+    const int64_t job = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);       // one 128-block per wave
+    if (job >= (int64_t) rows * blocks_per_row) return;                      // whole waves leave together
+    const int lane = threadIdx.x & 63;
+    const int64_t row = job / blocks_per_row;
+    const int col = (int) (job % blocks_per_row) * 128 + 2 * lane;
+    uint32_t v = *reinterpret_cast<const uint32_t*>(in + row * ld_in + col);
+    if (in_up) v = silu_mul_x2(v, *reinterpret_cast<const uint32_t*>(in_up + row * ld_in + col));
+    const uint32_t q = post ? *reinterpret_cast<const uint32_t*>(post + col) : 0u;
+    for (int g = 0; g < groups; ++g) {
+        // constant indices into the argument struct (a runtime index would copy it to scratch)
+        const uint16_t* pre = g == 0 ? hg.pre[0] : g == 1 ? hg.pre[1] : g == 2 ? hg.pre[2] : hg.pre[3];
+        uint16_t* out = g == 0 ? hg.out[0] : g == 1 ? hg.out[1] : g == 2 ? hg.out[2] : hg.out[3];
+        const uint32_t p = pre ? *reinterpret_cast<const uint32_t*>(pre + col) : 0u;
+        *reinterpret_cast<uint32_t*>(out + row * ld_out + col) = had128_x2<T>(v, p, pre != nullptr, q, post != nullptr, scale);
+    }
+}
+
 // the float transform's launch (exl3_had.hip)
 void launch_had_mfma(const uint16_t* in, const uint16_t* up, int64_t ld_in, const HadGroups& hg, int groups,
                      int64_t ld_out, int rows, int cols, const uint16_t* post, float scale, bool has_pre, hipStream_t s);
@@ -170,6 +200,11 @@ int launch_had(const void* in, int64_t ld_in, void* const* out, int64_t ld_out, 
         if (n_pre != 0 && n_pre != groups) return EXL3_EINVAL;      // pre for every group or for none
         launch_had_mfma((const uint16_t*) in, (const uint16_t*) in_up, ld_in, hg, groups, ld_out, rows, cols,
                         (const uint16_t*) post, sc, n_pre != 0, (hipStream_t) stream);
+    } else if (rows <= EXL3_GEMV_MAX_ROWS) {
+        // the latency form: one block per wave, four waves a workgroup
+        hipLaunchKernelGGL(had_kernel_x2<double>, dim3((unsigned) ((jobs + 3) / 4)), dim3(256), 0, (hipStream_t) stream,
+                           (const uint16_t*) in, (const uint16_t*) in_up, ld_in, hg, groups, ld_out, rows, cols,
+                           (const uint16_t*) post, R_SCALE * (double) scale);
     } else {
         hipLaunchKernelGGL(had_kernel<double>, grid, dim3(256), 0, (hipStream_t) stream, (const uint16_t*) in,
                            (const uint16_t*) in_up, ld_in, hg, groups, ld_out, rows, cols, (const uint16_t*) post,

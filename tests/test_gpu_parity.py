@@ -185,9 +185,12 @@ def test_had_r_128_f32_ragged_and_in_place(rows, cols):
         assert np.array_equal(f[rows:].view(np.int16), x[rows:].view(np.int16)), "rows past the call untouched"
 
 
-def test_had_r_128_bitexact():
-    rng = np.random.default_rng(3)
-    x = (rng.standard_normal((5, 640)) * 2).astype(np.float16)
+@pytest.mark.parametrize("rows", [5, 64, 65, 130])
+def test_had_r_128_bitexact(rows):
+    """The exact transform against the oracle, bitwise, on both of its kernels: one block per wave
+    up to 64 rows (the GEMV's pre-rotation), 8 lanes per block above."""
+    rng = np.random.default_rng(3 + rows)
+    x = (rng.standard_normal((rows, 640)) * 2).astype(np.float16)
     su = synth.scales(1, 640)
     X, SU = to_dev(x, su)
     out = torch.empty_like(X)
@@ -203,12 +206,13 @@ def test_had_r_128_bitexact():
 
 
 
-def test_had_r_128_bitexact_full_fp16_range():
+@pytest.mark.parametrize("blocks,rows", [(48, 16), (240, 80)])
+def test_had_r_128_bitexact_full_fp16_range(blocks, rows):
     """The exact transform on blocks spanning the whole fp16 range (+-65504 beside 2^-24 and every
     binade between): float64 sums of fp16 data are exact whatever the span (test_oracle pins the
-    arithmetic), so the kernel's butterflies equal the oracle's bit for bit here too."""
+    arithmetic), so either kernel's butterflies equal the oracle's bit for bit here too."""
     from test_oracle import _full_range_blocks
-    x = _full_range_blocks(np.random.default_rng(41), 48).reshape(16, 384)
+    x = _full_range_blocks(np.random.default_rng(41), blocks).reshape(rows, 384)
     X = to_dev(x)[0]
     out = torch.empty_like(X)
     E.had_r_128(X, out, None, None, 1.0)
