@@ -258,11 +258,12 @@ def test_rows_bitwise_equal_to_m1(k, n, bits, monkeypatch):
 
 
 @pytest.mark.parametrize("k,n,m,pre", [(5120, 256, 16, False), (5120, 256, 64, True), (5120, 5120, 20, False),
-                                       (5120, 5120, 24, True), (5120, 17408, 8, False), (5120, 17408, 9, True)])
+                                       (5120, 5120, 24, True), (5120, 17408, 5, False), (5120, 17408, 6, True)])
 def test_prerotation_rule_and_lds_rotation_bitwise(k, n, m, pre):
     """Through the C ABI: the library rotates the input by a separate pass into A_had exactly when
-    rows x the most units one workgroup owns >= 60 x (groups + 1) (5120 -> 256: 4 units, from 30
-    rows; 5120 x 5120: 5, from 24; 5120 -> 17408: 14, from 9), else in LDS leaving A_had as it
+    rows x the most units one workgroup owns >= 42 x (groups + 1) for workgroups of at least 6
+    units, else 60 x (groups + 1) (5120 -> 256: 4 units, from 30 rows; 5120 x 5120: 5, from 24;
+    5120 -> 17408: 14, from 6), else in LDS leaving A_had as it
     was; the outputs of the two are bitwise equal, and equal to A_had = NULL (always in LDS)."""
     import os
     if os.environ.get("EXL3_GEMV_PREROT_M"):
