@@ -41,16 +41,18 @@ DEFAULT_MR = 32
 # 64, graphs of 24 launches over 8 weight copies, 4 bpw, and 2 / 3 bpw where a checkpoint holds them
 # (the boundary moved by <= 4 rows).  Each entry is a boundary b within 1 % of the least summed time
 # over M with no step above 5 % from the GEMV at b rows to the GEMM at b + 1, for every bitrate
-# measured (re-checked for every entry after the GEMV's per-launch input-rotation rule; moved only
-# where the old b failed it: 5120 x 5120 15 -> 17, q/k/v 15 -> 19, the k/v pair 33 -> 58).  The
+# measured (re-checked for every entry after each change to the GEMV's input rotation; moved only
+# where the old b failed it: 5120 x 5120 15 -> 17, q/k/v 15 -> 19, the k/v pair 33 -> 58; after the
+# one-block-per-wave pre-rotation pass, the 14336-column q/k/v 17 -> 25, 6144 x 5120 32 -> 30 and
+# 17408 x 5120 35 -> 39).  The
 # GEMM's cost is flat within each 16-row MFMA tile; the GEMV's grows with every row and 16-row tile,
 # so the GEMM wins early where its 128-column tiles fill the chip (5120 - 7168 columns: b = 17 - 19)
 # and late where they do not (the k/v launches, 2 x 17408 columns and lm_head: 58 to the GEMV's
 # 64-row limit).
 GEMV_CROSSOVER = {
     (5120, 1024): 64, (5120, 2048): 58, (5120, 5120): 17, (5120, 6144): 17, (5120, 7168): 19,
-    (5120, 10240): 31, (5120, 12288): 33, (5120, 14336): 17, (5120, 16384): 33, (5120, 17408): 46,
-    (5120, 34816): 64, (5120, 248320): 64, (6144, 5120): 32, (17408, 5120): 35,
+    (5120, 10240): 31, (5120, 12288): 33, (5120, 14336): 25, (5120, 16384): 33, (5120, 17408): 46,
+    (5120, 34816): 64, (5120, 248320): 64, (6144, 5120): 30, (17408, 5120): 39,
 }
 
 
