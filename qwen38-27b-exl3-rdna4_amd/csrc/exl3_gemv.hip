@@ -372,8 +372,8 @@ bool shape_ok(int m, int k, int n, int K)
 // units a workgroup owns), or once per group by a separate pass into the caller's A_had scratch
 // (a launch and one rotated copy per group: a fixed cost that grows with the groups).  The pass
 // pays from rows x max_per >= unit_rows x (groups + 1), unit_rows = PREROT_UNIT_ROWS where the
-// workgroups own at least PREROT_SMALL_PER units, else PREROT_UNIT_ROWS_SMALL (a few units per
-// workgroup rotate in LDS under the first trellis data wait).  Measured crossovers with the
+// workgroups own at least PREROT_SMALL_PER units, else PREROT_UNIT_ROWS_SMALL (launches of a few
+// units per workgroup measured their in-LDS rotation cheaper per row-unit).  Measured crossovers with the
 // one-block-per-wave pass (rows where the pass first wins, max_per): gate 6 (14), down 5-6 (14),
 // gate/up 4 (27), 6144 x 5120 14 (6), the 3-group q/k/v 24 (7); o 24 (5), the 2-group 1024-wide
 // k/v pair 40 (4).  Outputs are bitwise the same either way.  EXL3_GEMV_PREROT_M, when set, fixes
