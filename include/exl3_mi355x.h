@@ -121,7 +121,7 @@ int exl3_gemv_f32(const void* x, int64_t ldx, const void* trellis, void* y, int6
 /* 1 <= m <= EXL3_GEMV_MAX_ROWS (64) EXL3 linear, output rows with stride ldy.
  * A_had: optional fp16 scratch of m * k elements (groups * m * k for the grouped forms).  When
  * given and the launch takes the pre-rotation pass (m x the most units one workgroup owns >=
- * 42 x (groups + 1) where that is at least 6 units, else 60 x (groups + 1); or m >=
+ * u x (groups + 1), u = 60 below 6 units per workgroup, 42 from 6, 36 from 20; or m >=
  * EXL3_GEMV_PREROT_M when that is set; exl3_gemv_prerot_rows), the input
  * is rotated once per group into it,
  * A_had = fp16(Had128(fp16(x * suh))) as in the reference, and the GEMV reads those rows; otherwise
@@ -176,9 +176,9 @@ size_t exl3_gemv_workspace_size_widths(int m, int k, const int* widths, int grou
 
 /* Rows from which the multi-row GEMV entry points may rotate the input once per group into A_had;
  * callers need not provide A_had below it.  2 by default: the library pre-rotates a launch when
- * rows x the most units one workgroup owns >= 42 x (groups + 1) where that is at least 6 units,
- * else 60 x (groups + 1) (gate and down at 6 rows, gate/up at 5, q/k/v at 24, o at 24) and rotates
- * in LDS otherwise, with the same outputs bitwise.  EXL3_GEMV_PREROT_M
+ * rows x the most units one workgroup owns >= u x (groups + 1), u = 60 below 6 units per
+ * workgroup, 42 from 6, 36 from 20 (gate and down at 6 rows, gate/up at 4, q/k/v at 24, o at 24)
+ * and rotates in LDS otherwise, with the same outputs bitwise.  EXL3_GEMV_PREROT_M
  * fixes one row count for every shape instead and is returned.  No reference counterpart.
  * Callers: exl3rocm's kernel wrappers. */
 int exl3_gemv_prerot_rows(void);

@@ -371,16 +371,15 @@ bool shape_ok(int m, int k, int n, int K)
 // The input is rotated either by every workgroup for its own k-range, in LDS (work ~ rows x the
 // units a workgroup owns), or once per group by a separate pass into the caller's A_had scratch
 // (a launch and one rotated copy per group: a fixed cost that grows with the groups).  The pass
-// pays from rows x max_per >= unit_rows x (groups + 1), unit_rows = PREROT_UNIT_ROWS where the
-// workgroups own at least PREROT_SMALL_PER units, else PREROT_UNIT_ROWS_SMALL (launches of a few
-// units per workgroup measured their in-LDS rotation cheaper per row-unit).  Measured crossovers with the
+// pays from rows x max_per >= unit_rows x (groups + 1): unit_rows falls as the workgroups own more
+// units (60 below PREROT_SMALL_PER units, 42 up to PREROT_LARGE_PER, 36 from there; launches of a
+// few units per workgroup measured their in-LDS rotation cheaper per row-unit).  Measured crossovers with the
 // one-block-per-wave pass (rows where the pass first wins, max_per): gate 6 (14), down 5-6 (14),
 // gate/up 4 (27), 6144 x 5120 14 (6), the 3-group q/k/v 24 (7); o 24 (5), the 2-group 1024-wide
 // k/v pair 40 (4).  Outputs are bitwise the same either way.  EXL3_GEMV_PREROT_M, when set, fixes
 // one row count for every shape.
-constexpr int PREROT_UNIT_ROWS = 42;
-constexpr int PREROT_UNIT_ROWS_SMALL = 60;
 constexpr int PREROT_SMALL_PER = 6;
+constexpr int PREROT_LARGE_PER = 20;
 
 int prerot_override()
 {
@@ -392,7 +391,7 @@ bool prerot(int m, int max_per, int groups)
 {
     const int o = prerot_override();
     if (o > 0) return m >= o;
-    const int unit_rows = max_per >= PREROT_SMALL_PER ? PREROT_UNIT_ROWS : PREROT_UNIT_ROWS_SMALL;
+    const int unit_rows = max_per >= PREROT_LARGE_PER ? 36 : max_per >= PREROT_SMALL_PER ? 42 : 60;
     return m > 1 && (int64_t) m * max_per >= (int64_t) unit_rows * (groups + 1);
 }
 
